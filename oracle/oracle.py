@@ -1,0 +1,230 @@
+"""numpy front end of the CPU oracle (libq35oracle.so).
+
+TEST INFRASTRUCTURE ONLY: tests/ use it as the parity checker and bench.py's
+cpu_baseline leg times it.  The product library never imports it.  Each
+function forwards to the C restatement in q35_oracle.c, which cites the
+reference file:line it follows.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "libq35oracle.so")
+_lib = None
+
+F = ctypes.POINTER(ctypes.c_float)
+
+
+def build() -> None:
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        _lib = ctypes.CDLL(_LIB_PATH)
+    return _lib
+
+
+class Dims(ctypes.Structure):
+    _fields_ = [("n_k_heads", ctypes.c_int), ("n_v_heads", ctypes.c_int),
+                ("head_k_dim", ctypes.c_int), ("conv_kernel", ctypes.c_int),
+                ("n_heads", ctypes.c_int), ("n_kv_heads", ctypes.c_int),
+                ("head_dim", ctypes.c_int), ("rope_dim", ctypes.c_int),
+                ("rope_base", ctypes.c_float), ("eps", ctypes.c_float)]
+
+
+def dims(n_k_heads=16, n_v_heads=32, head_k_dim=128, conv_kernel=4, n_heads=16, n_kv_heads=4,
+         head_dim=256, rope_dim=64, rope_base=1e7, eps=1e-6) -> Dims:
+    return Dims(n_k_heads, n_v_heads, head_k_dim, conv_kernel, n_heads, n_kv_heads, head_dim,
+                rope_dim, rope_base, eps)
+
+
+def _p(a: np.ndarray):
+    if a is None:
+        return None
+    assert a.dtype == np.float32 and a.flags.c_contiguous, (a.dtype, a.flags)
+    return a.ctypes.data_as(F)
+
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(np.asarray(a, dtype=np.float32))
+
+
+# ---- scalar helpers ------------------------------------------------------
+
+def silu(x: float) -> float:
+    lib().q35o_silu.restype = ctypes.c_float
+    return lib().q35o_silu(ctypes.c_float(x))
+
+
+def softplus(x: float) -> float:
+    lib().q35o_softplus.restype = ctypes.c_float
+    return lib().q35o_softplus(ctypes.c_float(x))
+
+
+def log1p_safe(x: float) -> float:
+    lib().q35o_log1p_safe.restype = ctypes.c_float
+    return lib().q35o_log1p_safe(ctypes.c_float(x))
+
+
+def fast_exp(x) -> np.ndarray:
+    x = _f32(x)
+    y = np.empty_like(x)
+    lib().q35o_fast_exp_n(_p(x), _p(y), x.size)
+    return y
+
+
+def sigmoid(x) -> np.ndarray:
+    x = _f32(x)
+    y = np.empty_like(x)
+    lib().q35o_sigmoid(_p(x), _p(y), x.size)
+    return y
+
+
+# ---- DeltaNet ops --------------------------------------------------------
+
+def causal_conv1d(inp, kernel, kernel_size, channels, seq):
+    inp, kernel = _f32(inp), _f32(kernel)
+    out = np.empty(channels * seq, np.float32)
+    lib().q35o_causal_conv1d(_p(inp), _p(kernel), kernel_size, channels, seq, _p(out))
+    return out.reshape(channels, seq)
+
+
+def causal_conv1d_update(inp, kernel, kernel_size, channels, conv_state):
+    """Returns (out, new_conv_state); conv_state is not modified."""
+    inp, kernel = _f32(inp), _f32(kernel)
+    cs = _f32(conv_state).copy()
+    out = np.empty(channels, np.float32)
+    lib().q35o_causal_conv1d_update(_p(inp), _p(kernel), kernel_size, channels, _p(cs), _p(out))
+    return out, cs
+
+
+def recurrent_gated_delta_rule(q, k, v, g, beta, state, tokens, n_heads, head_dim, v_head_dim,
+                               eps, l2norm_qk=True):
+    """Returns (out [tokens][n_heads][v_head_dim], new_state)."""
+    q, k, v, g, beta = map(_f32, (q, k, v, g, beta))
+    st = _f32(state).copy()
+    out = np.empty(tokens * n_heads * v_head_dim, np.float32)
+    lib().q35o_recurrent_gated_delta_rule(_p(q), _p(k), _p(v), _p(g), _p(beta), _p(st), tokens,
+                                          n_heads, head_dim, v_head_dim, ctypes.c_float(eps),
+                                          _p(out), int(l2norm_qk))
+    return out.reshape(tokens, n_heads, v_head_dim), st
+
+
+# ---- norms ---------------------------------------------------------------
+
+def rms_norm_zero_centered(x, weight, rows, dim, eps):
+    x = _f32(x)
+    y = np.empty_like(x)
+    w = None if weight is None else _f32(weight)
+    lib().q35o_rms_norm_zero_centered(_p(x), _p(w), _p(y), rows, dim, ctypes.c_float(eps))
+    return y
+
+
+def gated_rms_norm(x, weight, gate, rows, dim, eps):
+    x, gate = _f32(x), _f32(gate)
+    y = np.empty_like(x)
+    w = None if weight is None else _f32(weight)
+    lib().q35o_gated_rms_norm(_p(x), _p(w), _p(gate), _p(y), rows, dim, ctypes.c_float(eps))
+    return y
+
+
+# ---- attention -----------------------------------------------------------
+
+def rope_table(cap, half, base):
+    c = np.empty(cap * half, np.float32)
+    s = np.empty(cap * half, np.float32)
+    lib().q35o_rope_table(cap, half, ctypes.c_float(base), _p(c), _p(s))
+    return c.reshape(cap, half), s.reshape(cap, half)
+
+
+def neox_rope(x, tokens, heads, head_dim, rope_dim, start_pos, base):
+    y = _f32(x).copy()
+    lib().q35o_neox_rope(_p(y), tokens, heads, head_dim, rope_dim, start_pos, ctypes.c_float(base))
+    return y
+
+
+def attention_scores(q, cache_k, heads, kv_heads, head_dim, q_len, kv_len, q_dim, kv_stride,
+                     scale, start_pos, n_threads=1):
+    q, cache_k = _f32(q), _f32(cache_k)
+    sc = np.zeros(heads * q_len * kv_len, np.float32)
+    lib().q35o_attention_scores(_p(q), _p(cache_k), _p(sc), heads, kv_heads, head_dim, q_len,
+                                kv_len, q_dim, kv_stride, ctypes.c_float(scale), start_pos,
+                                n_threads)
+    return sc.reshape(heads, q_len, kv_len)
+
+
+def softmax_causal(scores, heads, q_len, kv_len, start_pos, n_threads=1):
+    sc = _f32(scores).copy()
+    lib().q35o_softmax_causal(_p(sc), heads, q_len, kv_len, start_pos, n_threads)
+    return sc
+
+
+def attention_combine(cache_v, scores, heads, kv_heads, head_dim, q_len, kv_len, q_dim,
+                      kv_stride, start_pos, n_threads=1):
+    cache_v, scores = _f32(cache_v), _f32(scores)
+    out = np.zeros(q_len * q_dim, np.float32)
+    lib().q35o_attention_combine(_p(cache_v), _p(scores), _p(out), heads, kv_heads, head_dim,
+                                 q_len, kv_len, q_dim, kv_stride, start_pos, n_threads)
+    return out.reshape(q_len, q_dim)
+
+
+# ---- mixers --------------------------------------------------------------
+
+def deltanet_decode(d: Dims, qkv, z, b, a, w: dict, conv_state, state):
+    """One token.  Returns (out, new_conv_state, new_state, core_out)."""
+    qkv, z, b, a = map(_f32, (qkv, z, b, a))
+    cs, st = _f32(conv_state).copy(), _f32(state).copy()
+    nv, hd = d.n_v_heads, d.head_k_dim
+    out = np.empty(nv * hd, np.float32)
+    core = np.empty(nv * hd, np.float32)
+    lib().q35o_deltanet_decode(ctypes.byref(d), _p(qkv), _p(z), _p(b), _p(a),
+                               _p(_f32(w["conv_w"])), _p(_f32(w["ssm_a"])),
+                               _p(_f32(w["dt_bias"])), _p(_f32(w["ssm_norm"])), _p(cs), _p(st),
+                               _p(out), _p(core))
+    return out, cs, st, core
+
+
+def deltanet_prefill(d: Dims, T, qkv, z, b, a, w: dict, state, conv_state=None):
+    """T tokens.  Returns (out [T][nv*hd], new_conv_state, new_state, core_out)."""
+    qkv, z, b, a = map(_f32, (qkv, z, b, a))
+    nv, nk, hd = d.n_v_heads, d.n_k_heads, d.head_k_dim
+    conv_dim = 2 * nk * hd + nv * hd
+    cs = np.zeros((conv_dim, d.conv_kernel - 1), np.float32) if conv_state is None \
+        else _f32(conv_state).copy()
+    st = _f32(state).copy()
+    out = np.empty((T, nv * hd), np.float32)
+    core = np.empty((T, nv * hd), np.float32)
+    lib().q35o_deltanet_prefill(ctypes.byref(d), T, _p(qkv), _p(z), _p(b), _p(a),
+                                _p(_f32(w["conv_w"])), _p(_f32(w["ssm_a"])),
+                                _p(_f32(w["dt_bias"])), _p(_f32(w["ssm_norm"])), _p(cs), _p(st),
+                                _p(out), _p(core))
+    return out, cs, st, core
+
+
+def attn_decode(d: Dims, start, q_gate, k, v, w: dict, cache_k, cache_v, n_threads=1):
+    """Returns (out [n_heads*head_dim], cache_k', cache_v') with row `start` written."""
+    ck, cv = _f32(cache_k).copy(), _f32(cache_v).copy()
+    out = np.empty(d.n_heads * d.head_dim, np.float32)
+    lib().q35o_attn_decode(ctypes.byref(d), start, _p(_f32(q_gate)), _p(_f32(k)), _p(_f32(v)),
+                           _p(_f32(w["q_norm"])), _p(_f32(w["k_norm"])), _p(ck), _p(cv),
+                           _p(out), n_threads)
+    return out, ck, cv
+
+
+def attn_prefill(d: Dims, start, T, q_gate, k, v, w: dict, cache_k, cache_v, n_threads=1):
+    """Returns (out [T][n_heads*head_dim], cache_k', cache_v') with rows start.. written."""
+    ck, cv = _f32(cache_k).copy(), _f32(cache_v).copy()
+    out = np.empty((T, d.n_heads * d.head_dim), np.float32)
+    lib().q35o_attn_prefill(ctypes.byref(d), start, T, _p(_f32(q_gate)), _p(_f32(k)),
+                            _p(_f32(v)), _p(_f32(w["q_norm"])), _p(_f32(w["k_norm"])), _p(ck),
+                            _p(cv), _p(out), n_threads)
+    return out, ck, cv
