@@ -1,0 +1,375 @@
+#!/usr/bin/env python3
+"""Token-mixer benchmark on one MI355X (gfx950).
+
+Headline line (one JSON object on stdout): Gated-DeltaNet prefill of one
+2048-token sequence through one layer (16 k-heads, 32 v-heads, dk = dv = 128,
+conv 4, zero state, fp32), tokens/s, with the roofline of its dominant kernel
+and the CPU restatement timed beside it.  The same line carries the decode
+mixers (one DeltaNet layer at batch 1; one GQA layer at 8193 cached rows), the
+GQA prefill at T = 2048 and the 32-layer mixer stack (24 DeltaNet + 8 GQA
+layers, 8 sequences at context 32768, 128 decode steps) under "workloads".
+
+A step is one pass of the measured mixer over its synthetic inputs, which are
+resident in HBM before the timed region.  Timing uses HIP events on the
+library's own stream; per-kernel durations come from the library's event
+timers in a second, separately timed pass.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "qwen3.5sharp_amd"))
+
+import q35mix  # noqa: E402
+import synth  # noqa: E402
+
+HBM_PEAK = 8.0e12          # B/s, MI355X datasheet
+FP32_PEAK = 157.3e12       # FLOP/s, MI355X dense fp32 (matrix = vector)
+NK, NV, DK = 16, 32, 128
+NH, NKV, HD = 16, 4, 256
+CONV_DIM = 2 * NK * DK + NV * DK
+VALUE_DIM = NV * DK
+Q_DIM, KV_DIM = NH * HD, NKV * HD
+
+# Algorithmic work per unit.
+DN_DECODE_BYTES = 4_588_544               # 1 token, 1 layer, 1 sequence
+
+
+def attn_decode_bytes(kv_len: int) -> int:
+    return 8192 * kv_len + 59_648          # K+V rows + q|gate, new k/v, out, norms, RoPE row
+
+
+DN_PREFILL_FLOP = 11_811_160_064           # T=2048, chunked WY form (32 heads x 32 chunks)
+DN_SCAN_FLOP_PER_TOKEN = 7 * DK * DK * NV   # sequential delta rule: 7 dk dv per head-token
+ATTN_PREFILL_FLOP = 4 * HD * NH * 2048 * 2049 // 2
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def time_calls(ctx, fn, steps, warmup):
+    for i in range(warmup):
+        fn(i)
+    ctx.sync()
+    e0, e1 = q35mix.Event(), q35mix.Event()
+    e0.record(ctx.stream)
+    for i in range(steps):
+        fn(warmup + i)
+    e1.record(ctx.stream)
+    ms = e0.elapsed_ms(e1)
+    return ms / steps
+
+
+def kernel_times(ctx, fn, steps):
+    ctx.profile(True)
+    for i in range(steps):
+        fn(i)
+    res = ctx.profile_read()
+    ctx.profile(False)
+    return {k: (ms / n, n) for k, (ms, n) in res.items()}
+
+
+def dominant(ktimes):
+    name = max(ktimes, key=lambda k: ktimes[k][0] * ktimes[k][1])
+    return name, ktimes[name][0]
+
+
+# --------------------------------------------------------------------------
+# workloads
+# --------------------------------------------------------------------------
+
+def bench_dn_prefill(steps, warmup, T=2048):
+    ctx = q35mix.Context(q35mix.qwen35_config(num_layers=1, is_recurrent=[1]), 1, 16)
+    ctx.set_deltanet_weights(0, synth.deltanet_weights(NK, NV, DK))
+    x = synth.deltanet_inputs(T, NK, NV, DK)
+    qkv, z = ctx.array((T, CONV_DIM), x["qkv"]), ctx.array((T, VALUE_DIM), x["z"])
+    b, a = ctx.array((T, NV), x["b"]), ctx.array((T, NV), x["a"])
+    out = ctx.array((T, VALUE_DIM))
+
+    def step(i):
+        ctx.deltanet_prefill(0, 0, T, qkv, z, b, a, out)
+
+    ms = time_calls(ctx, step, steps, warmup)
+    kt = kernel_times(ctx, step, steps)
+    ctx.close()
+    return ms, kt, x
+
+
+def bench_dn_decode(steps, warmup, n_layers=160):
+    """Batch 1; rotates over n_layers distinct states (> MALL) between calls."""
+    ctx = q35mix.Context(q35mix.qwen35_config(num_layers=n_layers, is_recurrent=[1] * n_layers),
+                         1, 16)
+    w = synth.deltanet_weights(NK, NV, DK)
+    for layer in range(n_layers):
+        ctx.set_deltanet_weights(layer, w)
+    x = synth.deltanet_inputs(1, NK, NV, DK)
+    qkv, z = ctx.array((1, CONV_DIM), x["qkv"]), ctx.array((1, VALUE_DIM), x["z"])
+    b, a = ctx.array((1, NV), x["b"]), ctx.array((1, NV), x["a"])
+    out = ctx.array((1, VALUE_DIM))
+
+    def step(i):
+        ctx.deltanet_decode(i % n_layers, [0], qkv, z, b, a, out)
+
+    ms = time_calls(ctx, step, steps, warmup)
+    kt = kernel_times(ctx, step, steps)
+    ctx.close()
+    return ms, kt
+
+
+def bench_attn_decode(steps, warmup, n_layers=8, pos=8192):
+    """One token at position 8192 (8193 rows); rotates over 8 distinct caches."""
+    ctx = q35mix.Context(q35mix.qwen35_config(num_layers=n_layers, is_recurrent=[0] * n_layers),
+                         1, pos + 1)
+    wts = synth.attn_weights(HD)
+    k, v = synth.kv_prefill(pos, KV_DIM)
+    for layer in range(n_layers):
+        ctx.set_attn_weights(layer, wts)
+        ctx.state_write(layer, 0, q35mix.STATE_KEYS, k)
+        ctx.state_write(layer, 0, q35mix.STATE_VALUES, v)
+    ctx.advance(0, pos)
+    x = synth.attn_inputs(1, NH, NKV, HD)
+    qg, kk, vv = ctx.array((1, 2 * Q_DIM), x["q_gate"]), ctx.array((1, KV_DIM), x["k"]), \
+        ctx.array((1, KV_DIM), x["v"])
+    out = ctx.array((1, Q_DIM))
+
+    def step(i):
+        ctx.attn_decode(i % n_layers, [0], qg, kk, vv, out)
+
+    ms = time_calls(ctx, step, steps, warmup)
+    kt = kernel_times(ctx, step, steps)
+    ctx.close()
+    return ms, kt
+
+
+def bench_attn_prefill(steps, warmup, T=2048):
+    ctx = q35mix.Context(q35mix.qwen35_config(num_layers=1, is_recurrent=[0]), 1, T)
+    ctx.set_attn_weights(0, synth.attn_weights(HD))
+    x = synth.attn_inputs(T, NH, NKV, HD)
+    qg, kk, vv = ctx.array((T, 2 * Q_DIM), x["q_gate"]), ctx.array((T, KV_DIM), x["k"]), \
+        ctx.array((T, KV_DIM), x["v"])
+    out = ctx.array((T, Q_DIM))
+
+    def step(i):
+        ctx.attn_prefill(0, 0, T, qg, kk, vv, out)
+
+    ms = time_calls(ctx, step, steps, warmup)
+    kt = kernel_times(ctx, step, steps)
+    ctx.close()
+    return ms, kt
+
+
+def bench_stack(n_steps=128, warmup=4, n_seqs=8, ctx_len=32768, n_layers=32):
+    """32-layer mixer stack, 8 sequences decoding from context 32640 to 32768."""
+    is_rec = [(i + 1) % 4 != 0 for i in range(n_layers)]
+    ctx = q35mix.Context(q35mix.qwen35_config(num_layers=n_layers, is_recurrent=is_rec), n_seqs,
+                         ctx_len)
+    start = ctx_len - n_steps
+    # Pre-filled KV rows ~N(0,1) (a 16 MiB block of normals tiled over the cache).
+    block = synth.normal(1234, 4 << 20)
+    wd, wa = synth.deltanet_weights(NK, NV, DK), synth.attn_weights(HD)
+    st = synth.deltanet_state(NK, NV, DK)
+    for layer in range(n_layers):
+        if is_rec[layer]:
+            ctx.set_deltanet_weights(layer, wd)
+            for s in range(n_seqs):
+                ctx.state_write(layer, s, q35mix.STATE_RECURRENT, st["state"])
+                ctx.state_write(layer, s, q35mix.STATE_CONV, st["conv_state"])
+        else:
+            ctx.set_attn_weights(layer, wa)
+            for s in range(n_seqs):
+                for kind in (q35mix.STATE_KEYS, q35mix.STATE_VALUES):
+                    ptr, nbytes = ctx.state_device_ptr(layer, s, kind)
+                    fill = start * KV_DIM * 4
+                    off = 0
+                    while off < fill:
+                        n = min(block.nbytes, fill - off)
+                        q35mix.check(q35mix.lib().q35m_copy_h2d(ctx.handle, ptr + off,
+                                                                block.ctypes.data, n))
+                        off += n
+    for s in range(n_seqs):
+        ctx.advance(s, start)
+    seqs = list(range(n_seqs))
+    # Eight distinct input sets, cycled over (step, layer).
+    pools = []
+    for j in range(8):
+        xd = synth.deltanet_inputs(n_seqs, NK, NV, DK, salt=500 + j)
+        xa = synth.attn_inputs(n_seqs, NH, NKV, HD, salt=600 + j)
+        pools.append((
+            [ctx.array((n_seqs, CONV_DIM), xd["qkv"]), ctx.array((n_seqs, VALUE_DIM), xd["z"]),
+             ctx.array((n_seqs, NV), xd["b"]), ctx.array((n_seqs, NV), xd["a"])],
+            [ctx.array((n_seqs, 2 * Q_DIM), xa["q_gate"]), ctx.array((n_seqs, KV_DIM), xa["k"]),
+             ctx.array((n_seqs, KV_DIM), xa["v"])]))
+    out_d = ctx.array((n_seqs, VALUE_DIM))
+    out_a = ctx.array((n_seqs, Q_DIM))
+
+    def one_step(step):
+        for layer in range(n_layers):
+            pd, pa = pools[(step * n_layers + layer) % 8]
+            if is_rec[layer]:
+                ctx.deltanet_decode(layer, seqs, *pd, out_d)
+            else:
+                ctx.attn_decode(layer, seqs, *pa, out_a)
+        for s in seqs:
+            ctx.advance(s, 1)
+
+    for i in range(warmup):
+        one_step(i)
+    ctx.sync()
+    for s in seqs:
+        ctx.truncate(s, start)
+    e0, e1 = q35mix.Event(), q35mix.Event()
+    e0.record(ctx.stream)
+    for i in range(n_steps):
+        one_step(i)
+    e1.record(ctx.stream)
+    ms = e0.elapsed_ms(e1)
+    for s in seqs:
+        ctx.truncate(s, start)
+    kt = kernel_times(ctx, one_step, 4)
+    ctx.close()
+    bytes_total = 0
+    for i in range(n_steps):
+        kv_len = start + i + 1
+        bytes_total += n_seqs * (24 * DN_DECODE_BYTES + 8 * attn_decode_bytes(kv_len))
+    return ms, kt, bytes_total
+
+
+# --------------------------------------------------------------------------
+# CPU restatement timed beside the GPU
+# --------------------------------------------------------------------------
+
+def cpu_baseline_prefill(x, T=2048):
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle
+    d = oracle.dims()
+    w = synth.deltanet_weights(NK, NV, DK)
+    st = np.zeros((NV, DK, DK), np.float32)
+    t0 = time.perf_counter()
+    oracle.deltanet_prefill(d, T, x["qkv"], x["z"], x["b"], x["a"], w, st)
+    dt = time.perf_counter() - t0
+    return T / dt, dt
+
+
+def cpu_info():
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return model, os.cpu_count()
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--only", default="", help="comma list of: dn_prefill,dn_decode,attn_decode,"
+                                               "attn_prefill,stack")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one MI355X only; --gpus {args.gpus} is not supported "
+              "(the mixers shard with no exchange inside the layer; see the sharding design)",
+              file=sys.stderr)
+        sys.exit(2)
+    only = set(filter(None, args.only.split(",")))
+
+    def want(name):
+        return not only or name in only
+
+    K, W = args.steps, args.warmup
+    workloads = {}
+    result = None
+
+    if want("dn_prefill"):
+        log("[bench] DeltaNet prefill T=2048 ...")
+        ms, kt, x = bench_dn_prefill(K, W)
+        tok_s = 2048 / (ms / 1e3)
+        kname, kms = dominant(kt)
+        log(f"[bench] DeltaNet prefill: {ms:.3f} ms/step, {tok_s:.0f} tok/s; kernels {kt}")
+        scan_flop = DN_SCAN_FLOP_PER_TOKEN * 2048
+        roof = {"bound": "mfma", "achieved": scan_flop / (kms / 1e3) / 1e12,
+                "peak": FP32_PEAK / 1e12, "unit": "TFLOP/s",
+                "frac": scan_flop / (kms / 1e3) / FP32_PEAK, "traffic": None,
+                "kernel": kname, "kernel_ms": kms,
+                "algorithmic": f"{scan_flop} FLOP per launch (7*dk*dv per head-token, 32 heads, "
+                               "2048 tokens)"}
+        cpu = None
+        if not args.no_cpu:
+            log("[bench] CPU restatement, one 2048-token DeltaNet prefill layer ...")
+            cpu_tok_s, cpu_s = cpu_baseline_prefill(x)
+            model, ncpu = cpu_info()
+            cpu = {"value": cpu_tok_s, "unit": "tokens/s", "cores": 1, "kind": "port",
+                   "sample": f"one full 2048-token DeltaNet prefill layer ({cpu_s:.2f} s, "
+                             f"single thread as the reference, {model}, {ncpu} logical CPUs)"}
+        result = {"metric": "token-mixer µs/token decode + % HBM peak; prefill tokens/s @T=2048",
+                  "value": tok_s, "unit": "tokens/s", "n_gpus": 1, "steps": K, "warmup": W,
+                  "ms_per_step": ms, "higher_is_better": True, "scaling": "weak",
+                  "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+                  "config": {"workload": "Gated-DeltaNet prefill, 1 layer, T=2048, batch 1, "
+                                         "16 k / 32 v heads, dk=dv=128, conv 4, zero state",
+                             "global_batch": 1, "seq_len": 2048, "parallelism": "none"},
+                  "roofline": roof, "cpu_baseline": cpu,
+                  "prefill_dn_mflop_frac": DN_PREFILL_FLOP / (ms / 1e3) / FP32_PEAK}
+
+    if want("dn_decode"):
+        log("[bench] DeltaNet decode batch 1 ...")
+        ms, kt = bench_dn_decode(max(K, 100), max(W, 20))
+        kname, kms = dominant(kt)
+        workloads["deltanet_decode_b1"] = {
+            "us_per_token": ms * 1e3, "hbm_frac_call": DN_DECODE_BYTES / (ms / 1e3) / HBM_PEAK,
+            "kernel": kname, "kernel_us": kms * 1e3,
+            "hbm_frac_kernel": DN_DECODE_BYTES / (kms / 1e3) / HBM_PEAK}
+        log(f"[bench] DeltaNet decode: {workloads['deltanet_decode_b1']}")
+
+    if want("attn_decode"):
+        log("[bench] GQA decode at 8193 rows ...")
+        ms, kt = bench_attn_decode(max(K, 100), max(W, 20))
+        by = attn_decode_bytes(8193)
+        kname, kms = dominant(kt)
+        workloads["attn_decode_8193"] = {
+            "us_per_token": ms * 1e3, "hbm_frac_call": by / (ms / 1e3) / HBM_PEAK,
+            "kernels_us": {k: v[0] * 1e3 for k, v in kt.items()}}
+        log(f"[bench] GQA decode: {workloads['attn_decode_8193']}")
+
+    if want("attn_prefill"):
+        log("[bench] GQA prefill T=2048 ...")
+        ms, kt = bench_attn_prefill(K, W)
+        workloads["attn_prefill_2048"] = {
+            "tokens_per_s": 2048 / (ms / 1e3), "ms": ms,
+            "mfma_frac": ATTN_PREFILL_FLOP / (ms / 1e3) / FP32_PEAK,
+            "kernels_ms": {k: v[0] for k, v in kt.items()}}
+        log(f"[bench] GQA prefill: {workloads['attn_prefill_2048']}")
+
+    if want("stack"):
+        log("[bench] 32-layer mixer stack, 8 seqs x ctx 32768, 128 decode steps ...")
+        ms, kt, by = bench_stack()
+        workloads["stack_decode_8x32k"] = {
+            "us_per_token": ms * 1e3 / (128 * 8), "ms_per_step": ms / 128,
+            "hbm_frac": by / (ms / 1e3) / HBM_PEAK, "gb_per_step": by / 128 / 1e9,
+            "kernels_us": {k: v[0] * 1e3 for k, v in kt.items()}}
+        log(f"[bench] stack: {workloads['stack_decode_8x32k']}")
+
+    if result is None:
+        result = {"metric": "token-mixer µs/token decode + % HBM peak; prefill tokens/s @T=2048",
+                  "value": None, "unit": "tokens/s", "n_gpus": 1, "steps": K, "warmup": W,
+                  "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+                  "dtype": "f32", "data": "synthetic", "config": {"workload": "partial run"}}
+    result["workloads"] = workloads
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,181 @@
+/*
+ * q35mix.h -- C ABI of libq35mix.so, the MI355X (gfx950) token mixers of
+ * Qwen3.5-style hybrid models: the Gated-DeltaNet recurrence and the gated
+ * GQA full-attention layer, for decode and prefill.
+ *
+ * The library is a drop-in for the mixer section of the reference's layer
+ * (between the projections and the output projection).  It owns, in HBM, the
+ * state the reference keeps in Qwen35Model fields: the DeltaNet recurrent
+ * state [H_v][dk][dv] and conv state [conv_dim][K-1] of every linear layer,
+ * and the K/V cache [capacity][kv_heads*head_dim] of every full-attention
+ * layer, per sequence.  Paths in citations are relative to the reference
+ * repository root.
+ *
+ * Conventions
+ *  - Every entry point returns an int status: Q35M_OK (0) or a negative
+ *    Q35M_ERR_* code; q35m_last_error() returns a thread-local message.
+ *  - Activation pointers (qkv, z, b, a, q_gate, k, v, out) are DEVICE
+ *    pointers to fp32, row-major, last index fastest.  Weight setters and
+ *    state read/write take HOST pointers.
+ *  - One context = one device and one HIP stream.  Mixer calls enqueue on
+ *    that stream and return; q35m_sync() waits.  A context has no internal
+ *    locking (the reference model is single-threaded too); separate contexts
+ *    may be driven from separate threads.
+ *  - Positions follow the reference: every layer of a forward pass writes
+ *    K/V at the sequence's current length, and q35m_advance() moves the
+ *    length once per pass (Qwen35Model.cs:235, 287).
+ */
+#ifndef Q35MIX_H
+#define Q35MIX_H
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define Q35M_OK 0
+#define Q35M_ERR_INVALID (-1)     /* bad argument (ArgumentException family)         */
+#define Q35M_ERR_UNSUPPORTED (-2) /* dims the kernels are not built for              */
+#define Q35M_ERR_CAPACITY (-3)    /* KV capacity or batch limit exceeded             */
+#define Q35M_ERR_NO_DEVICE (-4)   /* no usable HIP device                            */
+#define Q35M_ERR_HIP (-5)         /* HIP runtime error                               */
+#define Q35M_ERR_OOM (-6)         /* device allocation failed                        */
+#define Q35M_ERR_RANGE (-7)       /* truncate beyond the current length              */
+
+/* Mixer hyper-parameters: the mixer fields of ModelConfig
+ * (src/Qwen35Sharp.Model/ModelConfig.cs:19-54).  The kernels are built for
+ * ssm_state_size = 128 (dk = dv), head_dim = 256, rope_dim = 64,
+ * ssm_conv_kernel = 4, num_heads = 4 * num_kv_heads; head counts are free
+ * (ssm_time_step_rank a multiple of ssm_group_count). */
+typedef struct q35m_config {
+    int num_layers;
+    int num_heads;          /* full-attention q heads            (16)  */
+    int num_kv_heads;       /* full-attention kv heads           (4)   */
+    int head_dim;           /* full-attention head dim           (256) */
+    int rope_dim;           /* rotated dims per head             (64)  */
+    float rope_base;        /* NeoX RoPE base                    (1e7) */
+    int ssm_conv_kernel;    /* depthwise conv taps               (4)   */
+    int ssm_inner_size;     /* value dim = v_heads * dv          (4096)*/
+    int ssm_state_size;     /* dk = dv                           (128) */
+    int ssm_time_step_rank; /* DeltaNet v heads                  (32)  */
+    int ssm_group_count;    /* DeltaNet k heads                  (16)  */
+    float eps;              /* RMS / L2 epsilon                  (1e-6)*/
+    int full_attention_interval; /* layer i is GQA iff (i+1) % interval == 0 (4);
+                                    ignored when is_recurrent != NULL      */
+    const unsigned char* is_recurrent; /* [num_layers] or NULL (ModelConfig.cs:75-103) */
+} q35m_config;
+
+typedef struct q35m_ctx q35m_ctx;
+
+/* State kinds for q35m_state_read / q35m_state_write / q35m_state_device_ptr. */
+#define Q35M_STATE_RECURRENT 0 /* DeltaNet S [H_v][dk][dv], Qwen35Model.cs:31-32          */
+#define Q35M_STATE_CONV 1      /* DeltaNet conv window [conv_dim][K-1], oldest first,
+                                  GatedDeltaNetOps.cs:76 (code layout)                    */
+#define Q35M_STATE_KEYS 2      /* K cache rows [len][kv_heads*head_dim], post-RoPE/norm */
+#define Q35M_STATE_VALUES 3    /* V cache rows [len][kv_heads*head_dim]                 */
+
+/* ---- lifecycle -------------------------------------------------------- */
+
+/* Replaces the state allocation of the Qwen35Model constructor
+ * (Qwen35Model.cs:100-136): allocates, zero-filled, the per-(layer, seq)
+ * recurrent state, conv state and K/V cache of `kv_capacity` rows for
+ * `n_seqs` independent sequences, builds the RoPE table, creates the stream. */
+int q35m_create(const q35m_config* cfg, int n_seqs, int kv_capacity, q35m_ctx** out);
+int q35m_destroy(q35m_ctx* ctx);
+/* Qwen35Model.ResetCache (Qwen35Model.cs:200-212): zero the DeltaNet state
+ * and conv state of every linear layer for `seq`, and set its length to 0. */
+int q35m_reset(q35m_ctx* ctx, int seq);
+/* Qwen35Model.TruncateCache (Qwen35Model.cs:214-222): move the KV length only;
+ * refuses to extend (Q35M_ERR_RANGE).  The linear state is not rolled back. */
+int q35m_truncate(q35m_ctx* ctx, int seq, int length);
+/* `_cacheLen += seq` at the end of Qwen35Model.Forward (Qwen35Model.cs:287). */
+int q35m_advance(q35m_ctx* ctx, int seq, int n);
+int q35m_kv_len(const q35m_ctx* ctx, int seq, int* length);
+
+/* ---- weights (host -> HBM once; Qwen35Model.LoadWeights F32 tensors,
+ *      Qwen35Model.cs:468-474) --------------------------------------------- */
+
+/* conv_w [K][conv_dim] indexed W[j*conv_dim + c] (GatedDeltaNetOps.cs:48, 82);
+ * ssm_a [H_v] already -exp(A_log) (Qwen35Model.Decode.cs:379); dt_bias [H_v];
+ * ssm_norm [dv]. */
+int q35m_set_deltanet_weights(q35m_ctx* ctx, int layer, const float* conv_w, const float* ssm_a,
+                              const float* dt_bias, const float* ssm_norm);
+/* q_norm, k_norm [head_dim], applied as (1 + w) (Qwen35Ops.cs:59-63). */
+int q35m_set_attn_weights(q35m_ctx* ctx, int layer, const float* q_norm, const float* k_norm);
+
+/* ---- mixers (device pointers; enqueue on the context stream) ---------- */
+
+/* DecodeLinearAttn steps 2-6 (Qwen35Model.Decode.cs:348-397) for n
+ * sequences at once (seqs: HOST array of n distinct sequence ids):
+ * conv update + SiLU, q/k L2 norm, beta = sigmoid(b),
+ * g = ssm_a * softplus(a + dt_bias), one delta-rule step of the state,
+ * gated RMSNorm.  qkv [n][conv_dim], z [n][H_v*dv], b, a [n][H_v];
+ * out [n][H_v*dv]. */
+int q35m_deltanet_decode(q35m_ctx* ctx, int layer, int n, const int* seqs, const float* qkv,
+                         const float* z, const float* b, const float* a, float* out);
+
+/* PrefillLinearAttn steps 2-6 (Qwen35Model.Prefill.cs:181-260) for T >= 1
+ * tokens of one sequence: zero-padded causal conv (the stored conv window is
+ * ignored, GatedDeltaNetOps.cs:45-47), conv-window write-back of the last
+ * K-1 raw inputs (Qwen35Model.Prefill.cs:192-204, including its read past
+ * the channel row when T < K-1), the delta rule from the current state, and
+ * the gated RMSNorm.  qkv [T][conv_dim], z [T][H_v*dv], b, a [T][H_v];
+ * out [T][H_v*dv]. */
+int q35m_deltanet_prefill(q35m_ctx* ctx, int layer, int seq, int T, const float* qkv,
+                          const float* z, const float* b, const float* a, float* out);
+
+/* DecodeAttention steps after the projections (Qwen35Model.Decode.cs:294-323)
+ * for n sequences: writes K (RoPE'd, (1+w)-normed) and V at row kv_len(seq),
+ * RoPEs and norms q, attends causally over kv_len+1 rows with scale
+ * 1/sqrt(head_dim), multiplies by sigmoid(gate).  q_gate [n][heads*2*head_dim]
+ * interleaved per head [q_h | gate_h]; k, v [n][kv_heads*head_dim];
+ * out [n][heads*head_dim].  Does not advance the length. */
+int q35m_attn_decode(q35m_ctx* ctx, int layer, int n, const int* seqs, const float* q_gate,
+                     const float* k, const float* v, float* out);
+
+/* PrefillAttention steps after the projections (Qwen35Model.Prefill.cs:
+ * 113-149) for T tokens of one sequence starting at row kv_len(seq).
+ * q_gate [T][heads*2*head_dim]; k, v [T][kv_heads*head_dim];
+ * out [T][heads*head_dim].  Does not advance the length. */
+int q35m_attn_prefill(q35m_ctx* ctx, int layer, int seq, int T, const float* q_gate,
+                      const float* k, const float* v, float* out);
+
+/* ---- state I/O in the reference layouts (snapshot / restore / parity) -- */
+
+int q35m_state_read(q35m_ctx* ctx, int layer, int seq, int kind, void* host, size_t bytes);
+int q35m_state_write(q35m_ctx* ctx, int layer, int seq, int kind, const void* host,
+                     size_t bytes);
+/* Device address and size of one state buffer, for zero-copy callers. */
+int q35m_state_device_ptr(q35m_ctx* ctx, int layer, int seq, int kind, void** dptr,
+                          size_t* bytes);
+
+/* ---- stream, staging memory, errors ----------------------------------- */
+
+int q35m_sync(q35m_ctx* ctx);
+/* The context's hipStream_t, for event timing and ordering by the caller. */
+void* q35m_stream(q35m_ctx* ctx);
+int q35m_device_count(int* count);
+
+/* Per-kernel HIP event timers, the device-side counterpart of the
+ * reference's Qwen35Model.ProfileEnabled / Ticks* counters
+ * (Qwen35Model.cs:42-72).  q35m_profile(ctx, 1) zeroes the totals and times
+ * every following kernel launch on the context stream with events recorded
+ * around it; q35m_profile_read synchronises and returns the total
+ * milliseconds and launch count of kernel id `kernel`; kernel ids run from 0
+ * up to the first id for which q35m_profile_kernel_name returns NULL.
+ * Timing adds event records between launches: leave it off when measuring
+ * throughput. */
+int q35m_profile(q35m_ctx* ctx, int enable);
+int q35m_profile_read(q35m_ctx* ctx, int kernel, double* total_ms, long* launches);
+const char* q35m_profile_kernel_name(int kernel);
+int q35m_malloc(void** dptr, size_t bytes);
+int q35m_free(void* dptr);
+int q35m_copy_h2d(q35m_ctx* ctx, void* dst, const void* src, size_t bytes);
+int q35m_copy_d2h(q35m_ctx* ctx, void* dst, const void* src, size_t bytes);
+const char* q35m_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

@@ -1,0 +1,615 @@
+// Host side of libq35mix.so: context lifecycle, state ownership, weights,
+// argument checking and the C ABI entry points of include/q35mix.h.
+//
+// The context replaces the mixer-state fields of Qwen35Model
+// (src/Qwen35Sharp.Model/Qwen35Model.cs:23-36, allocation :100-136) with
+// hipMalloc'd HBM buffers carrying an extra sequence dimension.
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "q35mix_internal.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof(buf), fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+    if (e == hipErrorOutOfMemory) return fail(Q35M_ERR_OOM, "%s: %s", what, hipGetErrorString(e));
+    return fail(Q35M_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+#define HIP_TRY(expr, what)                        \
+    do {                                           \
+        hipError_t e_ = (expr);                    \
+        if (e_ != hipSuccess) return hip_fail(e_, what); \
+    } while (0)
+
+int alloc_zero(q35m_ctx* c, void** p, size_t bytes) {
+    *p = nullptr;
+    if (bytes == 0) return Q35M_OK;
+    hipError_t e = hipMalloc(p, bytes);
+    if (e != hipSuccess) return hip_fail(e, "hipMalloc");
+    c->allocations.push_back(*p);
+    e = hipMemsetAsync(*p, 0, bytes, c->stream);
+    if (e != hipSuccess) return hip_fail(e, "hipMemsetAsync");
+    return Q35M_OK;
+}
+
+void release(q35m_ctx* c) {
+    if (c->stream) (void)hipStreamSynchronize(c->stream);
+    for (auto& p : c->pending) {
+        c->event_pool.push_back(p.a);
+        c->event_pool.push_back(p.b);
+    }
+    c->pending.clear();
+    for (hipEvent_t e : c->event_pool) (void)hipEventDestroy(e);
+    c->event_pool.clear();
+    for (void* p : c->allocations) (void)hipFree(p);
+    c->allocations.clear();
+    if (c->work) (void)hipFree(c->work);
+    c->work = nullptr;
+    if (c->stream) (void)hipStreamDestroy(c->stream);
+    c->stream = nullptr;
+}
+
+int check_ctx(const q35m_ctx* c) {
+    if (!c) return fail(Q35M_ERR_INVALID, "null context");
+    return Q35M_OK;
+}
+
+int check_seq(const q35m_ctx* c, int seq) {
+    if (seq < 0 || seq >= c->n_seqs)
+        return fail(Q35M_ERR_INVALID, "sequence %d out of range [0, %d)", seq, c->n_seqs);
+    return Q35M_OK;
+}
+
+int check_layer(const q35m_ctx* c, int layer, bool recurrent) {
+    if (layer < 0 || layer >= c->cfg.num_layers)
+        return fail(Q35M_ERR_INVALID, "layer %d out of range [0, %d)", layer, c->cfg.num_layers);
+    if ((c->is_recurrent[layer] != 0) != recurrent)
+        return fail(Q35M_ERR_INVALID, "layer %d is a %s layer", layer,
+                    c->is_recurrent[layer] ? "Gated-DeltaNet" : "full-attention");
+    return Q35M_OK;
+}
+
+// Ops.EnsureRopeTable (src/Qwen35Sharp.Model/Ops.cs:135-160), built on the
+// host with the same fp32 operations (powf, fp32 angle, cosf/sinf) so the
+// device table equals the reference's bit for bit.
+void build_rope_table(int cap, int half, float base, std::vector<float>& cs,
+                      std::vector<float>& sn) {
+    std::vector<float> freqs(half);
+    for (int i = 0; i < half; i++) freqs[i] = 1.0f / powf(base, (float)i / (float)half);
+    cs.resize((size_t)cap * half);
+    sn.resize((size_t)cap * half);
+    for (int pos = 0; pos < cap; pos++)
+        for (int i = 0; i < half; i++) {
+            volatile float angle = (float)pos * freqs[i];
+            cs[(size_t)pos * half + i] = cosf(angle);
+            sn[(size_t)pos * half + i] = sinf(angle);
+        }
+}
+
+int build_seq_batch(const q35m_ctx* c, int n, const int* seqs, bool with_pos, q35::SeqBatch* sb) {
+    if (n < 1 || n > q35::kMaxBatch)
+        return fail(Q35M_ERR_CAPACITY, "batch of %d sequences (1..%d per call)", n, q35::kMaxBatch);
+    if (!seqs) return fail(Q35M_ERR_INVALID, "null seqs");
+    sb->n = n;
+    for (int i = 0; i < n; i++) {
+        int r = check_seq(c, seqs[i]);
+        if (r) return r;
+        for (int j = 0; j < i; j++)
+            if (seqs[j] == seqs[i]) return fail(Q35M_ERR_INVALID, "sequence %d repeated", seqs[i]);
+        sb->seq[i] = seqs[i];
+        sb->pos[i] = 0;
+        if (with_pos) {
+            int p = c->kv_len[seqs[i]];
+            if (p >= c->cap)
+                return fail(Q35M_ERR_CAPACITY, "sequence %d: KV cache full (%d rows)", seqs[i],
+                            c->cap);
+            sb->pos[i] = p;
+        }
+    }
+    return Q35M_OK;
+}
+
+}  // namespace
+
+namespace q35 {
+
+const char* kernel_name(int id) {
+    static const char* names[K_COUNT] = {
+        "deltanet_decode_kernel", "deltanet_prefill_prep", "deltanet_conv_writeback",
+        "deltanet_prefill_scan",  "deltanet_gated_norm",   "attn_decode_partial",
+        "attn_decode_merge",      "attn_prefill_prep",     "attn_prefill_flash"};
+    return (id >= 0 && id < K_COUNT) ? names[id] : nullptr;
+}
+
+static hipEvent_t take_event(q35m_ctx* c) {
+    if (!c->event_pool.empty()) {
+        hipEvent_t e = c->event_pool.back();
+        c->event_pool.pop_back();
+        return e;
+    }
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    return e;
+}
+
+ProfScope::ProfScope(q35m_ctx* ctx, int id) : c(ctx), kid(id) {
+    if (!c->profile) return;
+    a = take_event(c);
+    if (a) (void)hipEventRecord(a, c->stream);
+}
+
+ProfScope::~ProfScope() {
+    if (!c->profile || !a) return;
+    hipEvent_t b = take_event(c);
+    if (!b) return;
+    (void)hipEventRecord(b, c->stream);
+    c->pending.push_back({a, b, kid});
+}
+
+// Folds finished event pairs into the per-kernel totals.
+static hipError_t collect_profile(q35m_ctx* c) {
+    hipError_t e = hipStreamSynchronize(c->stream);
+    if (e != hipSuccess) return e;
+    for (auto& p : c->pending) {
+        float ms = 0.0f;
+        if (hipEventElapsedTime(&ms, p.a, p.b) == hipSuccess) {
+            c->prof_ms[p.kid] += ms;
+            c->prof_n[p.kid] += 1;
+        }
+        c->event_pool.push_back(p.a);
+        c->event_pool.push_back(p.b);
+    }
+    c->pending.clear();
+    return hipSuccess;
+}
+
+hipError_t ensure_work(q35m_ctx* c, size_t bytes) {
+    if (bytes <= c->work_bytes) return hipSuccess;
+    hipError_t e = hipStreamSynchronize(c->stream);
+    if (e != hipSuccess) return e;
+    if (c->work) (void)hipFree(c->work);
+    c->work = nullptr;
+    c->work_bytes = 0;
+    size_t want = bytes + (bytes >> 3);
+    e = hipMalloc((void**)&c->work, want);
+    if (e != hipSuccess) return e;
+    c->work_bytes = want;
+    return hipSuccess;
+}
+
+}  // namespace q35
+
+extern "C" {
+
+const char* q35m_last_error(void) { return g_last_error.c_str(); }
+
+int q35m_device_count(int* count) {
+    if (!count) return fail(Q35M_ERR_INVALID, "null count");
+    *count = 0;
+    hipError_t e = hipGetDeviceCount(count);
+    if (e != hipSuccess) {
+        *count = 0;
+        return fail(Q35M_ERR_NO_DEVICE, "no HIP device: %s", hipGetErrorString(e));
+    }
+    return Q35M_OK;
+}
+
+int q35m_create(const q35m_config* cfg, int n_seqs, int kv_capacity, q35m_ctx** out) {
+    if (!out) return fail(Q35M_ERR_INVALID, "null output pointer");
+    *out = nullptr;
+    if (!cfg) return fail(Q35M_ERR_INVALID, "null config");
+    if (cfg->num_layers <= 0) return fail(Q35M_ERR_INVALID, "num_layers must be positive");
+    if (n_seqs <= 0) return fail(Q35M_ERR_INVALID, "n_seqs must be positive");
+    if (kv_capacity <= 0) return fail(Q35M_ERR_INVALID, "kv_capacity must be positive");
+    if (cfg->ssm_state_size != q35::kDk || cfg->ssm_conv_kernel != q35::kConvK)
+        return fail(Q35M_ERR_UNSUPPORTED, "DeltaNet kernels are built for dk = dv = %d, %d taps",
+                    q35::kDk, q35::kConvK);
+    if (cfg->ssm_group_count <= 0 || cfg->ssm_time_step_rank <= 0 ||
+        cfg->ssm_time_step_rank % cfg->ssm_group_count != 0)
+        return fail(Q35M_ERR_INVALID, "ssm_time_step_rank must be a positive multiple of "
+                                      "ssm_group_count");
+    if (cfg->ssm_inner_size != cfg->ssm_time_step_rank * cfg->ssm_state_size)
+        return fail(Q35M_ERR_INVALID, "ssm_inner_size must equal ssm_time_step_rank * "
+                                      "ssm_state_size");
+    if (cfg->head_dim != q35::kHd || cfg->rope_dim != q35::kRopeDim)
+        return fail(Q35M_ERR_UNSUPPORTED, "attention kernels are built for head_dim %d, rope_dim %d",
+                    q35::kHd, q35::kRopeDim);
+    if (cfg->num_kv_heads <= 0 || cfg->num_heads != q35::kGqaGroup * cfg->num_kv_heads)
+        return fail(Q35M_ERR_UNSUPPORTED, "attention kernels are built for %d q heads per kv head",
+                    q35::kGqaGroup);
+    if (!(cfg->eps > 0.0f) || !(cfg->rope_base > 0.0f))
+        return fail(Q35M_ERR_INVALID, "eps and rope_base must be positive");
+    if (!cfg->is_recurrent && cfg->full_attention_interval <= 0)
+        return fail(Q35M_ERR_INVALID, "full_attention_interval must be positive");
+
+    int ndev = 0;
+    if (hipGetDeviceCount(&ndev) != hipSuccess || ndev <= 0)
+        return fail(Q35M_ERR_NO_DEVICE, "no HIP device available");
+
+    q35m_ctx* c = new q35m_ctx();
+    c->cfg = *cfg;
+    c->cfg.is_recurrent = nullptr;
+    c->n_seqs = n_seqs;
+    c->cap = kv_capacity;
+    (void)hipGetDevice(&c->device);
+    q35::Dims& d = c->d;
+    d.nk = cfg->ssm_group_count;
+    d.nv = cfg->ssm_time_step_rank;
+    d.key_dim = d.nk * q35::kDk;
+    d.value_dim = d.nv * q35::kDk;
+    d.conv_dim = 2 * d.key_dim + d.value_dim;
+    d.nh = cfg->num_heads;
+    d.nkv = cfg->num_kv_heads;
+    d.q_dim = d.nh * q35::kHd;
+    d.kv_dim = d.nkv * q35::kHd;
+    d.eps = cfg->eps;
+    d.rope_base = cfg->rope_base;
+    c->is_recurrent.resize(cfg->num_layers);
+    for (int l = 0; l < cfg->num_layers; l++)
+        c->is_recurrent[l] = cfg->is_recurrent ? (cfg->is_recurrent[l] != 0)
+                                               : ((l + 1) % cfg->full_attention_interval != 0);
+    c->kv_len.assign(n_seqs, 0);
+
+    int r = Q35M_OK;
+    hipError_t e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
+    if (e != hipSuccess) {
+        r = hip_fail(e, "hipStreamCreate");
+        delete c;
+        return r;
+    }
+    c->lin.resize(cfg->num_layers);
+    c->full.resize(cfg->num_layers);
+    size_t state_bytes = (size_t)n_seqs * d.nv * q35::kDk * q35::kDk * sizeof(float);
+    size_t conv_bytes = (size_t)n_seqs * d.conv_dim * q35::kConvState * sizeof(float);
+    size_t kv_bytes = (size_t)n_seqs * kv_capacity * d.kv_dim * sizeof(float);
+    for (int l = 0; l < cfg->num_layers && r == Q35M_OK; l++) {
+        if (c->is_recurrent[l]) {
+            q35::DeltaNetLayer& L = c->lin[l];
+            r = alloc_zero(c, (void**)&L.state, state_bytes);
+            if (!r) r = alloc_zero(c, (void**)&L.conv, conv_bytes);
+            if (!r) r = alloc_zero(c, (void**)&L.conv_w, (size_t)q35::kConvK * d.conv_dim * 4);
+            if (!r) r = alloc_zero(c, (void**)&L.ssm_a, (size_t)d.nv * 4);
+            if (!r) r = alloc_zero(c, (void**)&L.dt_bias, (size_t)d.nv * 4);
+            if (!r) r = alloc_zero(c, (void**)&L.ssm_norm, (size_t)q35::kDk * 4);
+        } else {
+            q35::AttnLayer& L = c->full[l];
+            r = alloc_zero(c, (void**)&L.k_cache, kv_bytes);
+            if (!r) r = alloc_zero(c, (void**)&L.v_cache, kv_bytes);
+            if (!r) r = alloc_zero(c, (void**)&L.q_norm, (size_t)q35::kHd * 4);
+            if (!r) r = alloc_zero(c, (void**)&L.k_norm, (size_t)q35::kHd * 4);
+        }
+    }
+    if (!r) r = alloc_zero(c, (void**)&c->counters, (size_t)q35::kMaxBatch * d.nk * sizeof(unsigned));
+    if (!r) {
+        c->rope_cap = kv_capacity > 4096 ? kv_capacity : 4096;
+        std::vector<float> cs, sn;
+        build_rope_table(c->rope_cap, q35::kRopeHalf, cfg->rope_base, cs, sn);
+        size_t tb = cs.size() * sizeof(float);
+        r = alloc_zero(c, (void**)&c->rope_cos, tb);
+        if (!r) r = alloc_zero(c, (void**)&c->rope_sin, tb);
+        if (!r) {
+            e = hipMemcpyAsync(c->rope_cos, cs.data(), tb, hipMemcpyHostToDevice, c->stream);
+            if (e == hipSuccess)
+                e = hipMemcpyAsync(c->rope_sin, sn.data(), tb, hipMemcpyHostToDevice, c->stream);
+            if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+            if (e != hipSuccess) r = hip_fail(e, "RoPE table upload");
+        }
+    }
+    if (r) {
+        std::string msg = g_last_error;
+        release(c);
+        delete c;
+        g_last_error = msg;
+        return r;
+    }
+    *out = c;
+    return Q35M_OK;
+}
+
+int q35m_destroy(q35m_ctx* ctx) {
+    int r = check_ctx(ctx);
+    if (r) return r;
+    release(ctx);
+    delete ctx;
+    return Q35M_OK;
+}
+
+int q35m_reset(q35m_ctx* ctx, int seq) {
+    int r = check_ctx(ctx);
+    if (!r) r = check_seq(ctx, seq);
+    if (r) return r;
+    const q35::Dims& d = ctx->d;
+    size_t sb = (size_t)d.nv * q35::kDk * q35::kDk * sizeof(float);
+    size_t cb = (size_t)d.conv_dim * q35::kConvState * sizeof(float);
+    for (int l = 0; l < ctx->cfg.num_layers; l++) {
+        if (!ctx->is_recurrent[l]) continue;
+        HIP_TRY(hipMemsetAsync((char*)ctx->lin[l].state + sb * seq, 0, sb, ctx->stream), "reset");
+        HIP_TRY(hipMemsetAsync((char*)ctx->lin[l].conv + cb * seq, 0, cb, ctx->stream), "reset");
+    }
+    ctx->kv_len[seq] = 0;
+    return Q35M_OK;
+}
+
+int q35m_truncate(q35m_ctx* ctx, int seq, int length) {
+    int r = check_ctx(ctx);
+    if (!r) r = check_seq(ctx, seq);
+    if (r) return r;
+    if (length < 0) return fail(Q35M_ERR_INVALID, "negative length %d", length);
+    if (length > ctx->kv_len[seq])
+        return fail(Q35M_ERR_RANGE, "cannot extend cache from %d to %d", ctx->kv_len[seq], length);
+    ctx->kv_len[seq] = length;
+    return Q35M_OK;
+}
+
+int q35m_advance(q35m_ctx* ctx, int seq, int n) {
+    int r = check_ctx(ctx);
+    if (!r) r = check_seq(ctx, seq);
+    if (r) return r;
+    if (n < 0) return fail(Q35M_ERR_INVALID, "negative advance %d", n);
+    if ((long)ctx->kv_len[seq] + n > ctx->cap)
+        return fail(Q35M_ERR_CAPACITY, "sequence %d: length %d + %d exceeds capacity %d", seq,
+                    ctx->kv_len[seq], n, ctx->cap);
+    ctx->kv_len[seq] += n;
+    return Q35M_OK;
+}
+
+int q35m_kv_len(const q35m_ctx* ctx, int seq, int* length) {
+    int r = check_ctx(ctx);
+    if (!r) r = check_seq(ctx, seq);
+    if (r) return r;
+    if (!length) return fail(Q35M_ERR_INVALID, "null length");
+    *length = ctx->kv_len[seq];
+    return Q35M_OK;
+}
+
+int q35m_set_deltanet_weights(q35m_ctx* ctx, int layer, const float* conv_w, const float* ssm_a,
+                              const float* dt_bias, const float* ssm_norm) {
+    int r = check_ctx(ctx);
+    if (!r) r = check_layer(ctx, layer, true);
+    if (r) return r;
+    if (!conv_w || !ssm_a || !dt_bias || !ssm_norm) return fail(Q35M_ERR_INVALID, "null weight");
+    q35::DeltaNetLayer& L = ctx->lin[layer];
+    const q35::Dims& d = ctx->d;
+    HIP_TRY(hipMemcpyAsync(L.conv_w, conv_w, (size_t)q35::kConvK * d.conv_dim * 4,
+                           hipMemcpyHostToDevice, ctx->stream), "upload conv_w");
+    HIP_TRY(hipMemcpyAsync(L.ssm_a, ssm_a, (size_t)d.nv * 4, hipMemcpyHostToDevice, ctx->stream),
+            "upload ssm_a");
+    HIP_TRY(hipMemcpyAsync(L.dt_bias, dt_bias, (size_t)d.nv * 4, hipMemcpyHostToDevice,
+                           ctx->stream), "upload dt_bias");
+    HIP_TRY(hipMemcpyAsync(L.ssm_norm, ssm_norm, (size_t)q35::kDk * 4, hipMemcpyHostToDevice,
+                           ctx->stream), "upload ssm_norm");
+    HIP_TRY(hipStreamSynchronize(ctx->stream), "upload weights");
+    L.has_weights = true;
+    return Q35M_OK;
+}
+
+int q35m_set_attn_weights(q35m_ctx* ctx, int layer, const float* q_norm, const float* k_norm) {
+    int r = check_ctx(ctx);
+    if (!r) r = check_layer(ctx, layer, false);
+    if (r) return r;
+    if (!q_norm || !k_norm) return fail(Q35M_ERR_INVALID, "null weight");
+    q35::AttnLayer& L = ctx->full[layer];
+    HIP_TRY(hipMemcpyAsync(L.q_norm, q_norm, q35::kHd * 4, hipMemcpyHostToDevice, ctx->stream),
+            "upload q_norm");
+    HIP_TRY(hipMemcpyAsync(L.k_norm, k_norm, q35::kHd * 4, hipMemcpyHostToDevice, ctx->stream),
+            "upload k_norm");
+    HIP_TRY(hipStreamSynchronize(ctx->stream), "upload weights");
+    L.has_weights = true;
+    return Q35M_OK;
+}
+
+int q35m_deltanet_decode(q35m_ctx* ctx, int layer, int n, const int* seqs, const float* qkv,
+                         const float* z, const float* b, const float* a, float* out) {
+    int r = check_ctx(ctx);
+    if (!r) r = check_layer(ctx, layer, true);
+    if (r) return r;
+    if (!ctx->lin[layer].has_weights) return fail(Q35M_ERR_INVALID, "layer %d has no weights", layer);
+    if (!qkv || !z || !b || !a || !out) return fail(Q35M_ERR_INVALID, "null activation pointer");
+    q35::SeqBatch sb;
+    r = build_seq_batch(ctx, n, seqs, false, &sb);
+    if (r) return r;
+    HIP_TRY(q35::launch_deltanet_decode(ctx, layer, sb, qkv, z, b, a, out), "deltanet_decode");
+    return Q35M_OK;
+}
+
+int q35m_deltanet_prefill(q35m_ctx* ctx, int layer, int seq, int T, const float* qkv,
+                          const float* z, const float* b, const float* a, float* out) {
+    int r = check_ctx(ctx);
+    if (!r) r = check_layer(ctx, layer, true);
+    if (!r) r = check_seq(ctx, seq);
+    if (r) return r;
+    if (!ctx->lin[layer].has_weights) return fail(Q35M_ERR_INVALID, "layer %d has no weights", layer);
+    if (T < 1) return fail(Q35M_ERR_INVALID, "T must be >= 1 (got %d)", T);
+    if (!qkv || !z || !b || !a || !out) return fail(Q35M_ERR_INVALID, "null activation pointer");
+    HIP_TRY(q35::ensure_work(ctx, q35::deltanet_prefill_work_bytes(ctx->d, T)), "workspace");
+    HIP_TRY(q35::launch_deltanet_prefill(ctx, layer, seq, T, qkv, z, b, a, out), "deltanet_prefill");
+    return Q35M_OK;
+}
+
+int q35m_attn_decode(q35m_ctx* ctx, int layer, int n, const int* seqs, const float* q_gate,
+                     const float* k, const float* v, float* out) {
+    int r = check_ctx(ctx);
+    if (!r) r = check_layer(ctx, layer, false);
+    if (r) return r;
+    if (!ctx->full[layer].has_weights) return fail(Q35M_ERR_INVALID, "layer %d has no weights", layer);
+    if (!q_gate || !k || !v || !out) return fail(Q35M_ERR_INVALID, "null activation pointer");
+    q35::SeqBatch sb;
+    r = build_seq_batch(ctx, n, seqs, true, &sb);
+    if (r) return r;
+    int max_len = 0;
+    for (int i = 0; i < n; i++) max_len = sb.pos[i] + 1 > max_len ? sb.pos[i] + 1 : max_len;
+    HIP_TRY(q35::ensure_work(ctx, q35::attn_decode_work_bytes(ctx->d, n, max_len)), "workspace");
+    HIP_TRY(q35::launch_attn_decode(ctx, layer, sb, q_gate, k, v, out), "attn_decode");
+    return Q35M_OK;
+}
+
+int q35m_attn_prefill(q35m_ctx* ctx, int layer, int seq, int T, const float* q_gate,
+                      const float* k, const float* v, float* out) {
+    int r = check_ctx(ctx);
+    if (!r) r = check_layer(ctx, layer, false);
+    if (!r) r = check_seq(ctx, seq);
+    if (r) return r;
+    if (!ctx->full[layer].has_weights) return fail(Q35M_ERR_INVALID, "layer %d has no weights", layer);
+    if (T < 1) return fail(Q35M_ERR_INVALID, "T must be >= 1 (got %d)", T);
+    if (!q_gate || !k || !v || !out) return fail(Q35M_ERR_INVALID, "null activation pointer");
+    int start = ctx->kv_len[seq];
+    if ((long)start + T > ctx->cap)
+        return fail(Q35M_ERR_CAPACITY, "sequence %d: %d + %d rows exceed KV capacity %d", seq, start,
+                    T, ctx->cap);
+    HIP_TRY(q35::ensure_work(ctx, q35::attn_prefill_work_bytes(ctx->d, T)), "workspace");
+    HIP_TRY(q35::launch_attn_prefill(ctx, layer, seq, start, T, q_gate, k, v, out), "attn_prefill");
+    return Q35M_OK;
+}
+
+static int state_locate(q35m_ctx* ctx, int layer, int seq, int kind, char** base, size_t* bytes) {
+    int r = check_ctx(ctx);
+    if (!r) r = check_seq(ctx, seq);
+    if (r) return r;
+    const q35::Dims& d = ctx->d;
+    if (kind == Q35M_STATE_RECURRENT || kind == Q35M_STATE_CONV) {
+        r = check_layer(ctx, layer, true);
+        if (r) return r;
+        if (kind == Q35M_STATE_RECURRENT) {
+            *bytes = (size_t)d.nv * q35::kDk * q35::kDk * sizeof(float);
+            *base = (char*)ctx->lin[layer].state + *bytes * seq;
+        } else {
+            *bytes = (size_t)d.conv_dim * q35::kConvState * sizeof(float);
+            *base = (char*)ctx->lin[layer].conv + *bytes * seq;
+        }
+        return Q35M_OK;
+    }
+    if (kind == Q35M_STATE_KEYS || kind == Q35M_STATE_VALUES) {
+        r = check_layer(ctx, layer, false);
+        if (r) return r;
+        *bytes = (size_t)ctx->cap * d.kv_dim * sizeof(float);
+        float* cache = kind == Q35M_STATE_KEYS ? ctx->full[layer].k_cache : ctx->full[layer].v_cache;
+        *base = (char*)cache + *bytes * seq;
+        return Q35M_OK;
+    }
+    return fail(Q35M_ERR_INVALID, "unknown state kind %d", kind);
+}
+
+int q35m_state_read(q35m_ctx* ctx, int layer, int seq, int kind, void* host, size_t bytes) {
+    char* base;
+    size_t cap_bytes;
+    int r = state_locate(ctx, layer, seq, kind, &base, &cap_bytes);
+    if (r) return r;
+    if (!host) return fail(Q35M_ERR_INVALID, "null host buffer");
+    if (bytes > cap_bytes)
+        return fail(Q35M_ERR_INVALID, "read of %zu bytes exceeds the %zu-byte state", bytes, cap_bytes);
+    HIP_TRY(hipMemcpyAsync(host, base, bytes, hipMemcpyDeviceToHost, ctx->stream), "state_read");
+    HIP_TRY(hipStreamSynchronize(ctx->stream), "state_read");
+    return Q35M_OK;
+}
+
+int q35m_state_write(q35m_ctx* ctx, int layer, int seq, int kind, const void* host,
+                     size_t bytes) {
+    char* base;
+    size_t cap_bytes;
+    int r = state_locate(ctx, layer, seq, kind, &base, &cap_bytes);
+    if (r) return r;
+    if (!host) return fail(Q35M_ERR_INVALID, "null host buffer");
+    if (bytes > cap_bytes)
+        return fail(Q35M_ERR_INVALID, "write of %zu bytes exceeds the %zu-byte state", bytes,
+                    cap_bytes);
+    HIP_TRY(hipMemcpyAsync(base, host, bytes, hipMemcpyHostToDevice, ctx->stream), "state_write");
+    HIP_TRY(hipStreamSynchronize(ctx->stream), "state_write");
+    return Q35M_OK;
+}
+
+int q35m_state_device_ptr(q35m_ctx* ctx, int layer, int seq, int kind, void** dptr,
+                          size_t* bytes) {
+    char* base;
+    size_t cap_bytes;
+    int r = state_locate(ctx, layer, seq, kind, &base, &cap_bytes);
+    if (r) return r;
+    if (dptr) *dptr = base;
+    if (bytes) *bytes = cap_bytes;
+    return Q35M_OK;
+}
+
+int q35m_sync(q35m_ctx* ctx) {
+    int r = check_ctx(ctx);
+    if (r) return r;
+    HIP_TRY(hipStreamSynchronize(ctx->stream), "sync");
+    return Q35M_OK;
+}
+
+void* q35m_stream(q35m_ctx* ctx) { return ctx ? (void*)ctx->stream : nullptr; }
+
+int q35m_profile(q35m_ctx* ctx, int enable) {
+    int r = check_ctx(ctx);
+    if (r) return r;
+    HIP_TRY(q35::collect_profile(ctx), "profile");
+    ctx->profile = enable != 0;
+    for (int k = 0; k < q35::K_COUNT; k++) {
+        ctx->prof_ms[k] = 0.0;
+        ctx->prof_n[k] = 0;
+    }
+    return Q35M_OK;
+}
+
+int q35m_profile_read(q35m_ctx* ctx, int kernel, double* total_ms, long* launches) {
+    int r = check_ctx(ctx);
+    if (r) return r;
+    if (kernel < 0 || kernel >= q35::K_COUNT)
+        return fail(Q35M_ERR_INVALID, "kernel id %d out of range [0, %d)", kernel, q35::K_COUNT);
+    HIP_TRY(q35::collect_profile(ctx), "profile_read");
+    if (total_ms) *total_ms = ctx->prof_ms[kernel];
+    if (launches) *launches = ctx->prof_n[kernel];
+    return Q35M_OK;
+}
+
+const char* q35m_profile_kernel_name(int kernel) { return q35::kernel_name(kernel); }
+
+int q35m_malloc(void** dptr, size_t bytes) {
+    if (!dptr) return fail(Q35M_ERR_INVALID, "null pointer");
+    *dptr = nullptr;
+    int ndev = 0;
+    if (hipGetDeviceCount(&ndev) != hipSuccess || ndev <= 0)
+        return fail(Q35M_ERR_NO_DEVICE, "no HIP device available");
+    HIP_TRY(hipMalloc(dptr, bytes), "hipMalloc");
+    return Q35M_OK;
+}
+
+int q35m_free(void* dptr) {
+    if (!dptr) return Q35M_OK;
+    HIP_TRY(hipFree(dptr), "hipFree");
+    return Q35M_OK;
+}
+
+int q35m_copy_h2d(q35m_ctx* ctx, void* dst, const void* src, size_t bytes) {
+    int r = check_ctx(ctx);
+    if (r) return r;
+    if (!dst || !src) return fail(Q35M_ERR_INVALID, "null pointer");
+    HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream), "copy_h2d");
+    HIP_TRY(hipStreamSynchronize(ctx->stream), "copy_h2d");
+    return Q35M_OK;
+}
+
+int q35m_copy_d2h(q35m_ctx* ctx, void* dst, const void* src, size_t bytes) {
+    int r = check_ctx(ctx);
+    if (r) return r;
+    if (!dst || !src) return fail(Q35M_ERR_INVALID, "null pointer");
+    HIP_TRY(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream), "copy_d2h");
+    HIP_TRY(hipStreamSynchronize(ctx->stream), "copy_d2h");
+    return Q35M_OK;
+}
+
+}  // extern "C"

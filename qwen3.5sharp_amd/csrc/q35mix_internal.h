@@ -1,0 +1,131 @@
+// Internal declarations shared by the host ABI (context.cpp) and the kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <vector>
+
+#include "../../include/q35mix.h"
+
+namespace q35 {
+
+// Dims the kernels are compiled for.
+constexpr int kDk = 128;        // DeltaNet key/value head dim (ssm_state_size)
+constexpr int kConvK = 4;       // conv taps
+constexpr int kConvState = 3;   // conv window length (K - 1)
+constexpr int kHd = 256;        // full-attention head dim
+constexpr int kRopeDim = 64;    // rotated dims
+constexpr int kRopeHalf = 32;
+constexpr int kGqaGroup = 4;    // q heads per kv head
+constexpr int kMaxBatch = 64;   // sequences per mixer launch
+
+// Per-launch sequence batch, passed by value in the kernel arguments.
+struct SeqBatch {
+    int n;
+    int seq[kMaxBatch];
+    int pos[kMaxBatch];  // attention: row the new token is written to
+};
+
+struct DeltaNetLayer {
+    float* conv_w = nullptr;   // [K][conv_dim]
+    float* ssm_a = nullptr;    // [H_v]
+    float* dt_bias = nullptr;  // [H_v]
+    float* ssm_norm = nullptr; // [dv]
+    float* state = nullptr;    // [n_seqs][H_v][dk][dv]
+    float* conv = nullptr;     // [n_seqs][conv_dim][3]
+    bool has_weights = false;
+};
+
+struct AttnLayer {
+    float* q_norm = nullptr;   // [head_dim]
+    float* k_norm = nullptr;   // [head_dim]
+    float* k_cache = nullptr;  // [n_seqs][cap][kv_dim]
+    float* v_cache = nullptr;  // [n_seqs][cap][kv_dim]
+    bool has_weights = false;
+};
+
+// Kernel ids for the optional per-kernel event timers (the device-side
+// counterpart of the reference's Qwen35Model.ProfileEnabled/Ticks* counters,
+// Qwen35Model.cs:42-72).
+enum KernelId {
+    K_DN_DECODE = 0,
+    K_DN_PREFILL_PREP,
+    K_DN_CONV_WRITEBACK,
+    K_DN_PREFILL_SCAN,
+    K_DN_GATED_NORM,
+    K_ATTN_DECODE_PARTIAL,
+    K_ATTN_DECODE_MERGE,
+    K_ATTN_PREFILL_PREP,
+    K_ATTN_PREFILL_FLASH,
+    K_COUNT
+};
+const char* kernel_name(int id);
+
+struct Dims {
+    int nk, nv;          // DeltaNet k / v heads
+    int key_dim, value_dim, conv_dim;
+    int nh, nkv;         // attention heads
+    int q_dim, kv_dim;
+    float eps;
+    float rope_base;
+};
+
+}  // namespace q35
+
+struct q35m_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    q35m_config cfg{};
+    q35::Dims d{};
+    int n_seqs = 0;
+    int cap = 0;                       // KV rows per (layer, seq)
+    std::vector<unsigned char> is_recurrent;
+    std::vector<q35::DeltaNetLayer> lin;   // indexed by layer (empty for GQA layers)
+    std::vector<q35::AttnLayer> full;      // indexed by layer (empty for DeltaNet layers)
+    std::vector<int> kv_len;           // per seq
+    float* rope_cos = nullptr;         // [rope_cap][32]
+    float* rope_sin = nullptr;
+    int rope_cap = 0;
+    unsigned* counters = nullptr;      // decode completion counters [kMaxBatch][nk]
+    float* work = nullptr;             // scratch for split-K partials and prefill
+    size_t work_bytes = 0;
+    std::vector<void*> allocations;
+    // Per-kernel event timers (off unless q35m_profile enables them).
+    bool profile = false;
+    struct EventPair { hipEvent_t a, b; int kid; };
+    std::vector<EventPair> pending;
+    std::vector<hipEvent_t> event_pool;
+    double prof_ms[q35::K_COUNT] = {};
+    long prof_n[q35::K_COUNT] = {};
+};
+
+namespace q35 {
+
+// Kernel launchers (return hipError_t of the launch).
+hipError_t launch_deltanet_decode(q35m_ctx* c, int layer, const SeqBatch& sb, const float* qkv,
+                                  const float* z, const float* b, const float* a, float* out);
+hipError_t launch_deltanet_prefill(q35m_ctx* c, int layer, int seq, int T, const float* qkv,
+                                   const float* z, const float* b, const float* a, float* out);
+size_t deltanet_prefill_work_bytes(const Dims& d, int T);
+hipError_t launch_attn_decode(q35m_ctx* c, int layer, const SeqBatch& sb, const float* q_gate,
+                              const float* k, const float* v, float* out);
+size_t attn_decode_work_bytes(const Dims& d, int n, int max_kv_len);
+hipError_t launch_attn_prefill(q35m_ctx* c, int layer, int seq, int start, int T,
+                               const float* q_gate, const float* k, const float* v, float* out);
+size_t attn_prefill_work_bytes(const Dims& d, int T);
+
+// Ensures ctx->work holds at least `bytes` (synchronises before regrowing).
+hipError_t ensure_work(q35m_ctx* c, size_t bytes);
+
+// Event timer bracketing one kernel launch when profiling is on.
+struct ProfScope {
+    q35m_ctx* c;
+    int kid;
+    hipEvent_t a = nullptr;
+    ProfScope(q35m_ctx* ctx, int id);
+    ~ProfScope();
+};
+
+}  // namespace q35

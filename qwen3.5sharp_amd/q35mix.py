@@ -1,0 +1,310 @@
+"""ctypes front end of libq35mix.so (include/q35mix.h).
+
+This is the Python view of the C ABI that tests and bench.py drive.  It
+loads the in-tree libq35mix.so and raises if it is missing: there is no
+CPU fallback.  Device memory is the library's own (q35m_malloc); the HIP
+runtime it links is used directly only for event timing on the context
+stream.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libq35mix.so")
+
+OK = 0
+ERR_INVALID, ERR_UNSUPPORTED, ERR_CAPACITY, ERR_NO_DEVICE, ERR_HIP, ERR_OOM, ERR_RANGE = \
+    -1, -2, -3, -4, -5, -6, -7
+STATE_RECURRENT, STATE_CONV, STATE_KEYS, STATE_VALUES = 0, 1, 2, 3
+
+_lib = None
+_hip = None
+
+
+class Q35Error(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"q35mix error {code}: {msg}")
+        self.code = code
+
+
+def build() -> None:
+    subprocess.run(["make", "-s", "-j8", "-C", HERE], check=True)
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise FileNotFoundError(f"{LIB_PATH} is not built (run __graft_entry__.build())")
+        _lib = ctypes.CDLL(LIB_PATH)
+        _lib.q35m_last_error.restype = ctypes.c_char_p
+        _lib.q35m_stream.restype = ctypes.c_void_p
+        _lib.q35m_stream.argtypes = [ctypes.c_void_p]
+        for name in ("q35m_malloc",):
+            getattr(_lib, name).argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_size_t]
+        _lib.q35m_free.argtypes = [ctypes.c_void_p]
+        for name in ("q35m_copy_h2d", "q35m_copy_d2h"):
+            getattr(_lib, name).argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                            ctypes.c_size_t]
+        for name in ("q35m_state_read", "q35m_state_write"):
+            getattr(_lib, name).argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
+                                            ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t]
+        _lib.q35m_profile_kernel_name.restype = ctypes.c_char_p
+        _lib.q35m_profile.argtypes = [ctypes.c_void_p, ctypes.c_int]
+        _lib.q35m_profile_read.argtypes = [ctypes.c_void_p, ctypes.c_int,
+                                           ctypes.POINTER(ctypes.c_double),
+                                           ctypes.POINTER(ctypes.c_long)]
+        _lib.q35m_state_device_ptr.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
+                                               ctypes.c_int, ctypes.POINTER(ctypes.c_void_p),
+                                               ctypes.POINTER(ctypes.c_size_t)]
+    return _lib
+
+
+def check(code: int) -> None:
+    if code != OK:
+        raise Q35Error(code, lib().q35m_last_error().decode())
+
+
+def device_count() -> int:
+    n = ctypes.c_int(0)
+    r = lib().q35m_device_count(ctypes.byref(n))
+    return n.value if r == OK else 0
+
+
+class Config(ctypes.Structure):
+    _fields_ = [("num_layers", ctypes.c_int), ("num_heads", ctypes.c_int),
+                ("num_kv_heads", ctypes.c_int), ("head_dim", ctypes.c_int),
+                ("rope_dim", ctypes.c_int), ("rope_base", ctypes.c_float),
+                ("ssm_conv_kernel", ctypes.c_int), ("ssm_inner_size", ctypes.c_int),
+                ("ssm_state_size", ctypes.c_int), ("ssm_time_step_rank", ctypes.c_int),
+                ("ssm_group_count", ctypes.c_int), ("eps", ctypes.c_float),
+                ("full_attention_interval", ctypes.c_int),
+                ("is_recurrent", ctypes.POINTER(ctypes.c_ubyte))]
+
+
+def qwen35_config(num_layers=32, num_heads=16, num_kv_heads=4, n_k_heads=16, n_v_heads=32,
+                  interval=4, is_recurrent=None) -> Config:
+    """Mixer dims of the 4B-class family member: hd 256, rope 64 (base 1e7),
+    dk = dv = 128, conv 4, eps 1e-6; GQA at (i+1) % 4 == 0."""
+    c = Config(num_layers, num_heads, num_kv_heads, 256, 64, 1e7, 4, n_v_heads * 128, 128,
+               n_v_heads, n_k_heads, 1e-6, interval, None)
+    if is_recurrent is not None:
+        arr = (ctypes.c_ubyte * num_layers)(*[1 if x else 0 for x in is_recurrent])
+        c.is_recurrent = ctypes.cast(arr, ctypes.POINTER(ctypes.c_ubyte))
+        c._keep = arr
+    return c
+
+
+class DeviceArray:
+    """fp32 device buffer owned by the library allocator."""
+
+    def __init__(self, ctx: "Context", shape, data: np.ndarray | None = None):
+        self.ctx = ctx
+        self.shape = tuple(int(s) for s in np.atleast_1d(shape)) if not isinstance(shape, tuple) \
+            else shape
+        self.nbytes = int(np.prod(self.shape)) * 4
+        p = ctypes.c_void_p()
+        check(lib().q35m_malloc(ctypes.byref(p), max(self.nbytes, 4)))
+        self.ptr = p.value
+        if data is not None:
+            self.upload(data)
+
+    def upload(self, data: np.ndarray) -> None:
+        a = np.ascontiguousarray(data, dtype=np.float32)
+        assert a.nbytes == self.nbytes, (a.shape, self.shape)
+        check(lib().q35m_copy_h2d(self.ctx.handle, self.ptr, a.ctypes.data, a.nbytes))
+
+    def download(self) -> np.ndarray:
+        a = np.empty(self.shape, np.float32)
+        check(lib().q35m_copy_d2h(self.ctx.handle, a.ctypes.data, self.ptr, a.nbytes))
+        return a
+
+    def free(self) -> None:
+        if self.ptr:
+            lib().q35m_free(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+def _seqs(seqs):
+    arr = (ctypes.c_int * len(seqs))(*seqs)
+    return arr
+
+
+class Context:
+    """One q35m_ctx: the mixer state of every layer for n_seqs sequences."""
+
+    def __init__(self, cfg: Config, n_seqs: int = 1, kv_capacity: int = 4096):
+        self.cfg = cfg
+        h = ctypes.c_void_p()
+        check(lib().q35m_create(ctypes.byref(cfg), n_seqs, kv_capacity, ctypes.byref(h)))
+        self.handle = h.value
+        self.n_seqs = n_seqs
+        self.kv_capacity = kv_capacity
+        nv, nk = cfg.ssm_time_step_rank, cfg.ssm_group_count
+        self.conv_dim = 2 * nk * 128 + nv * 128
+        self.value_dim = nv * 128
+        self.q_dim = cfg.num_heads * 256
+        self.kv_dim = cfg.num_kv_heads * 256
+
+    def close(self) -> None:
+        if self.handle:
+            check(lib().q35m_destroy(ctypes.c_void_p(self.handle)))
+            self.handle = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    def array(self, shape, data=None) -> DeviceArray:
+        return DeviceArray(self, shape, data)
+
+    @property
+    def stream(self) -> int:
+        return lib().q35m_stream(self.handle)
+
+    def sync(self) -> None:
+        check(lib().q35m_sync(ctypes.c_void_p(self.handle)))
+
+    # ---- lifecycle (Qwen35Model.ResetCache / TruncateCache / Forward) ----
+    def reset(self, seq: int) -> None:
+        check(lib().q35m_reset(ctypes.c_void_p(self.handle), seq))
+
+    def truncate(self, seq: int, length: int) -> None:
+        check(lib().q35m_truncate(ctypes.c_void_p(self.handle), seq, length))
+
+    def advance(self, seq: int, n: int) -> None:
+        check(lib().q35m_advance(ctypes.c_void_p(self.handle), seq, n))
+
+    def kv_len(self, seq: int) -> int:
+        n = ctypes.c_int()
+        check(lib().q35m_kv_len(ctypes.c_void_p(self.handle), seq, ctypes.byref(n)))
+        return n.value
+
+    # ---- weights -----------------------------------------------------------
+    def set_deltanet_weights(self, layer: int, w: dict) -> None:
+        arrs = [np.ascontiguousarray(w[k], np.float32) for k in
+                ("conv_w", "ssm_a", "dt_bias", "ssm_norm")]
+        check(lib().q35m_set_deltanet_weights(ctypes.c_void_p(self.handle), layer,
+                                              *[a.ctypes.data_as(ctypes.c_void_p) for a in arrs]))
+
+    def set_attn_weights(self, layer: int, w: dict) -> None:
+        arrs = [np.ascontiguousarray(w[k], np.float32) for k in ("q_norm", "k_norm")]
+        check(lib().q35m_set_attn_weights(ctypes.c_void_p(self.handle), layer,
+                                          *[a.ctypes.data_as(ctypes.c_void_p) for a in arrs]))
+
+    # ---- mixers (device arrays) -----------------------------------------
+    def deltanet_decode(self, layer, seqs, qkv, z, b, a, out) -> None:
+        check(lib().q35m_deltanet_decode(ctypes.c_void_p(self.handle), layer, len(seqs),
+                                         _seqs(seqs), *[ctypes.c_void_p(x.ptr) for x in
+                                                        (qkv, z, b, a, out)]))
+
+    def deltanet_prefill(self, layer, seq, T, qkv, z, b, a, out) -> None:
+        check(lib().q35m_deltanet_prefill(ctypes.c_void_p(self.handle), layer, seq, T,
+                                          *[ctypes.c_void_p(x.ptr) for x in (qkv, z, b, a, out)]))
+
+    def attn_decode(self, layer, seqs, q_gate, k, v, out) -> None:
+        check(lib().q35m_attn_decode(ctypes.c_void_p(self.handle), layer, len(seqs),
+                                     _seqs(seqs), *[ctypes.c_void_p(x.ptr) for x in
+                                                    (q_gate, k, v, out)]))
+
+    def attn_prefill(self, layer, seq, T, q_gate, k, v, out) -> None:
+        check(lib().q35m_attn_prefill(ctypes.c_void_p(self.handle), layer, seq, T,
+                                      *[ctypes.c_void_p(x.ptr) for x in (q_gate, k, v, out)]))
+
+    # ---- per-kernel event timers -----------------------------------------
+    def profile(self, enable: bool) -> None:
+        check(lib().q35m_profile(self.handle, int(enable)))
+
+    def profile_read(self) -> dict:
+        """{kernel name: (total ms, launches)} for kernels launched since profile(True)."""
+        res = {}
+        k = 0
+        while True:
+            name = lib().q35m_profile_kernel_name(k)
+            if not name:
+                break
+            ms, n = ctypes.c_double(), ctypes.c_long()
+            check(lib().q35m_profile_read(self.handle, k, ctypes.byref(ms), ctypes.byref(n)))
+            if n.value:
+                res[name.decode()] = (ms.value, n.value)
+            k += 1
+        return res
+
+    # ---- state I/O -----------------------------------------------------------
+    def _state_shape(self, kind: int, rows: int | None):
+        cfg = self.cfg
+        if kind == STATE_RECURRENT:
+            return (cfg.ssm_time_step_rank, 128, 128)
+        if kind == STATE_CONV:
+            return (self.conv_dim, 3)
+        return (self.kv_capacity if rows is None else rows, self.kv_dim)
+
+    def state_read(self, layer: int, seq: int, kind: int, rows: int | None = None) -> np.ndarray:
+        a = np.empty(self._state_shape(kind, rows), np.float32)
+        check(lib().q35m_state_read(self.handle, layer, seq, kind, a.ctypes.data, a.nbytes))
+        return a
+
+    def state_write(self, layer: int, seq: int, kind: int, data: np.ndarray) -> None:
+        a = np.ascontiguousarray(data, np.float32)
+        check(lib().q35m_state_write(self.handle, layer, seq, kind, a.ctypes.data, a.nbytes))
+
+    def state_device_ptr(self, layer: int, seq: int, kind: int):
+        p = ctypes.c_void_p()
+        n = ctypes.c_size_t()
+        check(lib().q35m_state_device_ptr(self.handle, layer, seq, kind, ctypes.byref(p),
+                                          ctypes.byref(n)))
+        return p.value, n.value
+
+
+# ---- HIP event timing on the context stream ------------------------------
+
+def hip() -> ctypes.CDLL:
+    """The HIP runtime libq35mix.so itself links (same process-wide instance)."""
+    global _hip
+    if _hip is None:
+        lib()
+        _hip = ctypes.CDLL("libamdhip64.so.7")
+        _hip.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+        _hip.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+        _hip.hipEventSynchronize.argtypes = [ctypes.c_void_p]
+        _hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p,
+                                             ctypes.c_void_p]
+        _hip.hipEventDestroy.argtypes = [ctypes.c_void_p]
+    return _hip
+
+
+class Event:
+    def __init__(self):
+        self.h = ctypes.c_void_p()
+        r = hip().hipEventCreate(ctypes.byref(self.h))
+        if r != 0:
+            raise RuntimeError(f"hipEventCreate failed: {r}")
+
+    def record(self, stream: int) -> None:
+        r = hip().hipEventRecord(self.h, ctypes.c_void_p(stream))
+        if r != 0:
+            raise RuntimeError(f"hipEventRecord failed: {r}")
+
+    def synchronize(self) -> None:
+        hip().hipEventSynchronize(self.h)
+
+    def elapsed_ms(self, end: "Event") -> float:
+        ms = ctypes.c_float()
+        end.synchronize()
+        r = hip().hipEventElapsedTime(ctypes.byref(ms), self.h, end.h)
+        if r != 0:
+            raise RuntimeError(f"hipEventElapsedTime failed: {r}")
+        return ms.value

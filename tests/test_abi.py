@@ -1,0 +1,82 @@
+"""C ABI checks that need no GPU: the library loads, exports every entry point
+include/q35mix.h declares, and rejects bad arguments before touching a device."""
+import ctypes
+import os
+import re
+
+import pytest
+
+import q35mix
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def declared_symbols():
+    names = set()
+    for fn in os.listdir(os.path.join(ROOT, "include")):
+        if fn.endswith(".h"):
+            text = open(os.path.join(ROOT, "include", fn)).read()
+            names |= set(re.findall(r"^\s*(?:int|void\*|const char\*|void)\s+(q35m_\w+)\s*\(",
+                                    text, re.M))
+    return sorted(names)
+
+
+def test_header_declares_entry_points():
+    names = declared_symbols()
+    for must in ("q35m_create", "q35m_destroy", "q35m_deltanet_decode", "q35m_deltanet_prefill",
+                 "q35m_attn_decode", "q35m_attn_prefill", "q35m_state_read", "q35m_last_error"):
+        assert must in names
+
+
+@pytest.mark.parametrize("name", declared_symbols())
+def test_library_exports(name):
+    assert hasattr(q35mix.lib(), name), name
+
+
+def _cfg(**kw):
+    c = q35mix.qwen35_config(num_layers=4)
+    for k, v in kw.items():
+        setattr(c, k, v)
+    return c
+
+
+def _create(cfg, n_seqs=1, cap=16):
+    h = ctypes.c_void_p()
+    r = q35mix.lib().q35m_create(ctypes.byref(cfg) if cfg is not None else None, n_seqs, cap,
+                                 ctypes.byref(h))
+    return r, h
+
+
+def test_create_rejects_bad_config():
+    assert _create(None)[0] == q35mix.ERR_INVALID
+    assert _create(_cfg(), n_seqs=0)[0] == q35mix.ERR_INVALID
+    assert _create(_cfg(), cap=0)[0] == q35mix.ERR_INVALID
+    assert _create(_cfg(ssm_state_size=64, ssm_inner_size=32 * 64))[0] == q35mix.ERR_UNSUPPORTED
+    assert _create(_cfg(head_dim=128))[0] == q35mix.ERR_UNSUPPORTED
+    assert _create(_cfg(num_heads=12))[0] == q35mix.ERR_UNSUPPORTED
+    assert _create(_cfg(ssm_time_step_rank=24, ssm_inner_size=24 * 128))[0] == q35mix.ERR_INVALID
+    assert _create(_cfg(ssm_inner_size=1000))[0] == q35mix.ERR_INVALID
+    assert _create(_cfg(eps=0.0))[0] == q35mix.ERR_INVALID
+    msg = q35mix.lib().q35m_last_error().decode()
+    assert "eps" in msg
+
+
+def test_null_context_is_rejected():
+    L = q35mix.lib()
+    assert L.q35m_reset(None, 0) == q35mix.ERR_INVALID
+    assert L.q35m_truncate(None, 0, 0) == q35mix.ERR_INVALID
+    assert L.q35m_sync(None) == q35mix.ERR_INVALID
+    assert L.q35m_destroy(None) == q35mix.ERR_INVALID
+    assert L.q35m_stream(None) is None
+    n = ctypes.c_int()
+    assert L.q35m_kv_len(None, 0, ctypes.byref(n)) == q35mix.ERR_INVALID
+
+
+def test_no_device_here_is_an_error_not_a_fallback():
+    if q35mix.device_count() > 0:
+        pytest.skip("a HIP device is present")
+    r, h = _create(_cfg())
+    assert r == q35mix.ERR_NO_DEVICE
+    assert h.value is None
+    p = ctypes.c_void_p()
+    assert q35mix.lib().q35m_malloc(ctypes.byref(p), 64) == q35mix.ERR_NO_DEVICE
