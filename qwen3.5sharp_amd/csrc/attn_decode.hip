@@ -10,14 +10,17 @@
 // P.V (Ops.AttentionCombine, Ops.cs:360-415), times sigmoid(gate).
 //
 // Pass 1 (attn_decode_partial): one workgroup per (sequence, kv head, chunk of
-// P positions).  The 4 q heads of the kv head share every K/V row it reads,
-// so each cache byte is read once per token.  Each workgroup recomputes the
-// 4 rotated, normed q rows (4 KiB of input); the workgroup whose chunk holds
-// the new position also rotates/norms the new K row and writes K and V into
-// the cache (single writer) and uses them from LDS.  It emits, per q head, the
-// chunk's max score m, sum of exp l, and unnormalised o = sum exp(s-m) v.
-// Pass 2 (attn_decode_merge): per (sequence, q head) the chunks are merged
-// with the usual log-sum-exp rescaling and the sigmoid gate is applied.
+// NSUB x 64 positions).  The 4 q heads of the kv head share every K/V row it
+// reads, so each cache byte is read once per token.  A 64-row sub-chunk is
+// processed with every K and V load issued before any arithmetic (64 KiB of
+// K and 64 KiB of V in flight per workgroup), which is what keeps HBM busy.
+// Each workgroup recomputes the 4 rotated, normed q rows (4 KiB of input); the
+// workgroup whose chunk holds the new position also rotates/norms the new K
+// row and writes K and V into the cache (single writer) and takes them from
+// LDS.  It emits, per q head, the chunk's max score m, sum of exp l and
+// unnormalised o = sum exp(s - m) v.
+// Pass 2 (attn_decode_merge): per (sequence, q head) the chunks are merged by
+// log-sum-exp rescaling and the sigmoid gate is applied.
 //
 // Online softmax is the two-pass softmax regrouped; it omits the reference's
 // -80 floor on shifted logits, which only touches weights below e^-80
@@ -29,46 +32,10 @@ namespace q35 {
 namespace {
 
 constexpr int NT = 256;
+constexpr int SUB = 64;   // positions per sub-chunk
 
-// RoPE (pairs (d, d+32), d < 32) and the (1+w) RMSNorm of one 256-wide head
-// row held as one float4 per lane of a wave (lane l: dims 4l..4l+3).
-__device__ __forceinline__ float4 rope_norm_row(float4 x, int lane, const float* __restrict__ cs,
-                                                const float* __restrict__ sn,
-                                                const float* __restrict__ w, float eps,
-                                                float post_scale) {
-    float4 p;
-    p.x = __shfl_xor(x.x, 8, kWave);
-    p.y = __shfl_xor(x.y, 8, kWave);
-    p.z = __shfl_xor(x.z, 8, kWave);
-    p.w = __shfl_xor(x.w, 8, kWave);
-    if (lane < 16) {
-        const int i0 = 4 * (lane & 7);
-        const float4 c = *reinterpret_cast<const float4*>(cs + i0);
-        const float4 s = *reinterpret_cast<const float4*>(sn + i0);
-        if (lane < 8) {   // x0' = x0 c - x1 s
-            x.x = x.x * c.x - p.x * s.x;
-            x.y = x.y * c.y - p.y * s.y;
-            x.z = x.z * c.z - p.z * s.z;
-            x.w = x.w * c.w - p.w * s.w;
-        } else {          // x1' = x0 s + x1 c
-            x.x = p.x * s.x + x.x * c.x;
-            x.y = p.y * s.y + x.y * c.y;
-            x.z = p.z * s.z + x.z * c.z;
-            x.w = p.w * s.w + x.w * c.w;
-        }
-    }
-    const float ss = wave_sum(x.x * x.x + x.y * x.y + x.z * x.z + x.w * x.w);
-    const float scale = 1.0f / sqrtf(ss / (float)kHd + eps);
-    const float4 ww = *reinterpret_cast<const float4*>(w + 4 * lane);
-    x.x = x.x * scale * (1.0f + ww.x) * post_scale;
-    x.y = x.y * scale * (1.0f + ww.y) * post_scale;
-    x.z = x.z * scale * (1.0f + ww.z) * post_scale;
-    x.w = x.w * scale * (1.0f + ww.w) * post_scale;
-    return x;
-}
-
-template <int P>
-__global__ __launch_bounds__(NT) void attn_decode_partial(
+template <int NSUB>
+__global__ __launch_bounds__(NT, 2) void attn_decode_partial(
     const float* __restrict__ q_gate, const float* __restrict__ knew,
     const float* __restrict__ vnew, const float* __restrict__ q_norm,
     const float* __restrict__ k_norm, float* __restrict__ k_cache, float* __restrict__ v_cache,
@@ -77,9 +44,8 @@ __global__ __launch_bounds__(NT) void attn_decode_partial(
     float eps, SeqBatch sb) {
     const int c = blockIdx.x, kvh = blockIdx.y, i = blockIdx.z;
     const int pos = sb.pos[i];
-    const int p0 = c * P;
+    const int p0 = c * SUB * NSUB;
     if (p0 > pos) return;
-    const int np = min(P, pos + 1 - p0);
     const int nh = nkv * kGqaGroup;
     const int kv_dim = nkv * kHd;
     const size_t seq_off = (size_t)sb.seq[i] * cap * kv_dim + (size_t)kvh * kHd;
@@ -90,167 +56,230 @@ __global__ __launch_bounds__(NT) void attn_decode_partial(
     __shared__ float4 q_s[kGqaGroup][kHd / 4];
     __shared__ float4 knew_s[kHd / 4];
     __shared__ float4 vnew_s[kHd / 4];
-    __shared__ float sc[kGqaGroup][P];
-    __shared__ float ml[kGqaGroup][2];
+    __shared__ float sc[kGqaGroup][SUB];
+    __shared__ float ml_s[kGqaGroup][2];
     __shared__ float4 obuf[4][kGqaGroup][kHd / 4];
 
     const float* cs = rope_cos + (size_t)pos * kRopeHalf;
     const float* sn = rope_sin + (size_t)pos * kRopeHalf;
-    const bool has_new = pos < p0 + P;
     {
-        // q of head kvh*4 + wave; the attention scale 1/16 is folded in.
+        // q of head kvh*4 + wave; the attention scale 1/sqrt(256) is folded in.
         const int h = kvh * kGqaGroup + wave;
         const float* qrow = q_gate + (size_t)i * 2 * nh * kHd + (size_t)h * 2 * kHd;
-        float4 x = *reinterpret_cast<const float4*>(qrow + 4 * lane);
+        const float4 x = *reinterpret_cast<const float4*>(qrow + 4 * lane);
         q_s[wave][lane] = rope_norm_row(x, lane, cs, sn, q_norm, eps, 1.0f / sqrtf((float)kHd));
     }
-    if (has_new) {
+    if (pos < p0 + SUB * NSUB) {
         if (wave == 0) {
             float4 x = *reinterpret_cast<const float4*>(knew + (size_t)i * kv_dim + kvh * kHd + 4 * lane);
             x = rope_norm_row(x, lane, cs, sn, k_norm, eps, 1.0f);
             knew_s[lane] = x;
             *reinterpret_cast<float4*>(K + (size_t)pos * kv_dim + 4 * lane) = x;
         } else if (wave == 1) {
-            float4 x = *reinterpret_cast<const float4*>(vnew + (size_t)i * kv_dim + kvh * kHd + 4 * lane);
+            const float4 x = *reinterpret_cast<const float4*>(vnew + (size_t)i * kv_dim + kvh * kHd + 4 * lane);
             vnew_s[lane] = x;
             *reinterpret_cast<float4*>(V + (size_t)pos * kv_dim + 4 * lane) = x;
         }
     }
     __syncthreads();
 
-    // Scores: 16 teams of 16 lanes; a lane holds dims {4*l16 + 64*m .. +3}.
-    {
-        const int team = tid >> 4, l16 = tid & 15;
-        float4 qr[kGqaGroup][4];
+    // Score layout: 16 teams of 16 lanes, team t scores positions t + 16m
+    // (m < 4); lane l16 holds dims {4*l16 + 64*j .. +3}, j < 4.
+    // P.V layout: thread holds dims 4*d4..+3 of all 4 heads, positions ps + 4m.
+    const int team = tid >> 4, l16 = tid & 15;
+    const int d4 = tid & 63, ps = tid >> 6;
+    float4 qr[kGqaGroup][4];
 #pragma unroll
-        for (int h = 0; h < kGqaGroup; ++h)
+    for (int h = 0; h < kGqaGroup; ++h)
 #pragma unroll
-            for (int m = 0; m < 4; ++m) qr[h][m] = q_s[h][l16 + 16 * m];
-        for (int pp = team; pp < np; pp += 16) {
-            const int pabs = p0 + pp;
-            float4 kk[4];
-            if (pabs == pos) {
+        for (int j = 0; j < 4; ++j) qr[h][j] = q_s[h][l16 + 16 * j];
+
+    float m_run = -INFINITY, l_run = 0.0f;     // per head (wave = head in the softmax step)
+    float4 acc[kGqaGroup];
 #pragma unroll
-                for (int m = 0; m < 4; ++m) kk[m] = knew_s[l16 + 16 * m];
-            } else {
-                const float4* krow = reinterpret_cast<const float4*>(K + (size_t)pabs * kv_dim);
+    for (int h = 0; h < kGqaGroup; ++h) acc[h] = make_float4(0.f, 0.f, 0.f, 0.f);
+
+    for (int sub = 0; sub < NSUB; ++sub) {
+        const int s0 = p0 + sub * SUB;
+        if (s0 > pos) break;                    // uniform across the workgroup
+        const int np = min(SUB, pos + 1 - s0);
+        float4 kk[4][4];
+        float4 vv[16];
 #pragma unroll
-                for (int m = 0; m < 4; ++m) kk[m] = krow[l16 + 16 * m];
-            }
-            float acc[kGqaGroup];
+        for (int m = 0; m < 4; ++m) {
+            const int pp = team + 16 * m;
+            const int pabs = s0 + pp;
+            const bool live = pp < np && pabs != pos;
+            const float4* krow = reinterpret_cast<const float4*>(K + (size_t)(live ? pabs : 0) * kv_dim);
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                kk[m][j] = live ? krow[l16 + 16 * j] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int m = 0; m < 16; ++m) {
+            const int pp = ps + 4 * m;
+            const int pabs = s0 + pp;
+            const bool live = pp < np && pabs != pos;
+            const float4* vrow = reinterpret_cast<const float4*>(V + (size_t)(live ? pabs : 0) * kv_dim);
+            vv[m] = live ? vrow[d4] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        // The new row comes from LDS.
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+            if (s0 + team + 16 * m == pos)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) kk[m][j] = knew_s[l16 + 16 * j];
+#pragma unroll
+        for (int m = 0; m < 16; ++m)
+            if (s0 + ps + 4 * m == pos) vv[m] = vnew_s[d4];
+
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            float a[kGqaGroup];
 #pragma unroll
             for (int h = 0; h < kGqaGroup; ++h) {
-                float a = 0.0f;
+                float t = 0.0f;
 #pragma unroll
-                for (int m = 0; m < 4; ++m)
-                    a += qr[h][m].x * kk[m].x + qr[h][m].y * kk[m].y + qr[h][m].z * kk[m].z +
-                         qr[h][m].w * kk[m].w;
-                acc[h] = group_sum<16>(a);
+                for (int j = 0; j < 4; ++j)
+                    t += qr[h][j].x * kk[m][j].x + qr[h][j].y * kk[m][j].y +
+                         qr[h][j].z * kk[m][j].z + qr[h][j].w * kk[m][j].w;
+                a[h] = group_sum<16>(t);
             }
             if (l16 == 0)
 #pragma unroll
-                for (int h = 0; h < kGqaGroup; ++h) sc[h][pp] = acc[h];
+                for (int h = 0; h < kGqaGroup; ++h) sc[h][team + 16 * m] = a[h];
         }
-    }
-    __syncthreads();
-
-    // Chunk softmax, one wave per q head.
-    {
-        float m = -INFINITY;
-        for (int pp = lane; pp < np; pp += 64) m = fmaxf(m, sc[wave][pp]);
-        m = wave_max(m);
-        float l = 0.0f;
-        for (int pp = lane; pp < np; pp += 64) {
-            const float e = __expf(sc[wave][pp] - m);
-            sc[wave][pp] = e;
-            l += e;
+        __syncthreads();
+        // Online softmax over the sub-chunk: wave h owns head h, lane = position.
+        {
+            const float s = lane < np ? sc[wave][lane] : -INFINITY;
+            const float mx = fmaxf(m_run, wave_max(s));
+            const float e = lane < np ? __expf(s - mx) : 0.0f;
+            const float alpha = __expf(m_run - mx);     // 0 on the first sub-chunk
+            l_run = l_run * alpha + wave_sum(e);
+            m_run = mx;
+            sc[wave][lane] = e;
+            if (lane == 0) ml_s[wave][0] = alpha;
         }
-        l = wave_sum(l);
-        if (lane == 0) {
-            ml[wave][0] = m;
-            ml[wave][1] = l;
-        }
-    }
-    __syncthreads();
-
-    // P.V: thread owns dims 4*d4..+3 of all 4 heads over positions pp = ps mod 4.
-    {
-        const int d4 = tid & 63, ps = tid >> 6;
-        float4 acc[kGqaGroup];
+        __syncthreads();
 #pragma unroll
-        for (int h = 0; h < kGqaGroup; ++h) acc[h] = make_float4(0.f, 0.f, 0.f, 0.f);
-        for (int pp = ps; pp < np; pp += 4) {
-            const int pabs = p0 + pp;
-            const float4 vv = pabs == pos
-                                  ? vnew_s[d4]
-                                  : reinterpret_cast<const float4*>(V + (size_t)pabs * kv_dim)[d4];
+        for (int h = 0; h < kGqaGroup; ++h) {
+            const float alpha = ml_s[h][0];
+            acc[h].x *= alpha; acc[h].y *= alpha; acc[h].z *= alpha; acc[h].w *= alpha;
+        }
+#pragma unroll
+        for (int m = 0; m < 16; ++m) {
+            const int pp = ps + 4 * m;
 #pragma unroll
             for (int h = 0; h < kGqaGroup; ++h) {
                 const float e = sc[h][pp];
-                acc[h].x += e * vv.x;
-                acc[h].y += e * vv.y;
-                acc[h].z += e * vv.z;
-                acc[h].w += e * vv.w;
+                acc[h].x += e * vv[m].x;
+                acc[h].y += e * vv[m].y;
+                acc[h].z += e * vv[m].z;
+                acc[h].w += e * vv[m].w;
             }
         }
+        __syncthreads();
+    }
+
 #pragma unroll
-        for (int h = 0; h < kGqaGroup; ++h) obuf[ps][h][d4] = acc[h];
+    for (int h = 0; h < kGqaGroup; ++h) obuf[ps][h][d4] = acc[h];
+    if (lane == 0) {
+        ml_s[wave][0] = m_run;
+        ml_s[wave][1] = l_run;
     }
     __syncthreads();
     {
-        const int h = tid >> 6, d4 = tid & 63;
+        const int h = tid >> 6;
         float4 o = obuf[0][h][d4];
 #pragma unroll
-        for (int ps = 1; ps < 4; ++ps) {
-            const float4 t = obuf[ps][h][d4];
+        for (int q = 1; q < 4; ++q) {
+            const float4 t = obuf[q][h][d4];
             o.x += t.x; o.y += t.y; o.z += t.z; o.w += t.w;
         }
         const size_t pidx = (((size_t)i * nkv + kvh) * nchunks + c) * kGqaGroup + h;
         reinterpret_cast<float4*>(part_o + pidx * kHd)[d4] = o;
         if (d4 == 0) {
-            part_ml[2 * pidx] = ml[h][0];
-            part_ml[2 * pidx + 1] = ml[h][1];
+            part_ml[2 * pidx] = ml_s[h][0];
+            part_ml[2 * pidx + 1] = ml_s[h][1];
         }
     }
 }
 
-__global__ __launch_bounds__(kHd) void attn_decode_merge(
+// Merge of the chunk partials of one (sequence, q head): 512 threads; thread
+// holds 4 dims (d4 = t % 64) and merges chunks c = t / 64 (mod 8); the chunk
+// weights exp(m_c - M) come from one shared maximum M.
+constexpr int MT = 512;
+
+__global__ __launch_bounds__(MT) void attn_decode_merge(
     const float* __restrict__ part_o, const float* __restrict__ part_ml,
-    const float* __restrict__ q_gate, float* __restrict__ out, int nkv, int nchunks, int P,
+    const float* __restrict__ q_gate, float* __restrict__ out, int nkv, int nchunks, int chunk,
     SeqBatch sb) {
-    const int h = blockIdx.x, i = blockIdx.y, d = threadIdx.x;
+    const int h = blockIdx.x, i = blockIdx.y, t = threadIdx.x;
     const int nh = nkv * kGqaGroup;
     const int kvh = h / kGqaGroup, hl = h % kGqaGroup;
-    const int nc = (sb.pos[i] + 1 + P - 1) / P;
-    float M = -INFINITY, Lsum = 0.0f, O = 0.0f;
+    const int nc = (sb.pos[i] + chunk) / chunk;
     const size_t base = ((size_t)i * nkv + kvh) * nchunks;
-    for (int c = 0; c < nc; ++c) {
+    __shared__ float red[MT / kWave];
+    __shared__ float4 obuf[MT / kWave][kHd / 4];
+    __shared__ float lbuf[MT / kWave];
+
+    float mx = -INFINITY;
+    for (int c = t; c < nc; c += MT) mx = fmaxf(mx, part_ml[2 * ((base + c) * kGqaGroup + hl)]);
+    mx = wave_max(mx);
+    if ((t & 63) == 0) red[t >> 6] = mx;
+    __syncthreads();
+    float M = red[0];
+#pragma unroll
+    for (int w = 1; w < MT / kWave; ++w) M = fmaxf(M, red[w]);
+
+    const int d4 = t & 63, g = t >> 6;
+    float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+    float l = 0.0f;
+#pragma unroll 4
+    for (int c = g; c < nc; c += MT / kWave) {
         const size_t pidx = (base + c) * kGqaGroup + hl;
-        const float m = part_ml[2 * pidx], l = part_ml[2 * pidx + 1];
-        const float o = part_o[pidx * kHd + d];
-        const float mn = fmaxf(M, m);
-        const float a = __expf(M - mn), b = __expf(m - mn);
-        Lsum = Lsum * a + l * b;
-        O = O * a + o * b;
-        M = mn;
+        const float wgt = __expf(part_ml[2 * pidx] - M);
+        const float4 oc = reinterpret_cast<const float4*>(part_o + pidx * kHd)[d4];
+        l += wgt * part_ml[2 * pidx + 1];
+        o.x += wgt * oc.x; o.y += wgt * oc.y; o.z += wgt * oc.z; o.w += wgt * oc.w;
     }
-    const float gate = q_gate[(size_t)i * 2 * nh * kHd + (size_t)h * 2 * kHd + kHd + d];
-    out[(size_t)i * nh * kHd + (size_t)h * kHd + d] = (O / Lsum) * (1.0f / (1.0f + expf(-gate)));
+    obuf[g][d4] = o;
+    if (d4 == 0) lbuf[g] = l;
+    __syncthreads();
+    if (t < kHd / 4) {
+        float4 s = obuf[0][t];
+        float L = lbuf[0];
+#pragma unroll
+        for (int w = 1; w < MT / kWave; ++w) {
+            s.x += obuf[w][t].x; s.y += obuf[w][t].y; s.z += obuf[w][t].z; s.w += obuf[w][t].w;
+            L += lbuf[w];
+        }
+        const float inv = 1.0f / L;
+        const float4 gt = *reinterpret_cast<const float4*>(
+            q_gate + (size_t)i * 2 * nh * kHd + (size_t)h * 2 * kHd + kHd + 4 * t);
+        float4 r;
+        r.x = s.x * inv * (1.0f / (1.0f + expf(-gt.x)));
+        r.y = s.y * inv * (1.0f / (1.0f + expf(-gt.y)));
+        r.z = s.z * inv * (1.0f / (1.0f + expf(-gt.z)));
+        r.w = s.w * inv * (1.0f / (1.0f + expf(-gt.w)));
+        *reinterpret_cast<float4*>(out + (size_t)i * nh * kHd + (size_t)h * kHd + 4 * t) = r;
+    }
 }
 
-int pick_chunk(int n, int nkv, int max_len) {
-    // Smallest chunk that still gives >= 4 workgroups per CU (256 CUs); at least 64.
-    static const int sizes[3] = {256, 128, 64};
-    for (int s : sizes)
-        if ((long)n * nkv * ((max_len + s - 1) / s) >= 1024) return s;
-    return 64;
+// Sub-chunks per workgroup: as many as keep >= 1024 workgroups (4 per CU),
+// at most 4, so partials stay small next to the cache they summarise.
+int pick_nsub(int n, int nkv, int max_len) {
+    for (int ns = 4; ns > 1; ns >>= 1)
+        if ((long)n * nkv * ((max_len + SUB * ns - 1) / (SUB * ns)) >= 1024) return ns;
+    return 1;
 }
 
 }  // namespace
 
 size_t attn_decode_work_bytes(const Dims& d, int n, int max_kv_len) {
-    const int P = pick_chunk(n, d.nkv, max_kv_len);
-    const size_t nchunks = (max_kv_len + P - 1) / P;
+    const int chunk = SUB * pick_nsub(n, d.nkv, max_kv_len);
+    const size_t nchunks = (max_kv_len + chunk - 1) / chunk;
     return (size_t)n * d.nkv * nchunks * kGqaGroup * (kHd + 2) * sizeof(float);
 }
 
@@ -260,37 +289,29 @@ hipError_t launch_attn_decode(q35m_ctx* c, int layer, const SeqBatch& sb, const 
     const AttnLayer& L = c->full[layer];
     int max_len = 0;
     for (int i = 0; i < sb.n; ++i) max_len = max(max_len, sb.pos[i] + 1);
-    const int P = pick_chunk(sb.n, d.nkv, max_len);
-    const int nchunks = (max_len + P - 1) / P;
+    const int nsub = pick_nsub(sb.n, d.nkv, max_len);
+    const int chunk = SUB * nsub;
+    const int nchunks = (max_len + chunk - 1) / chunk;
     float* part_o = c->work;
     float* part_ml = part_o + (size_t)sb.n * d.nkv * nchunks * kGqaGroup * kHd;
-    dim3 grid(nchunks, d.nkv, sb.n);
+    const dim3 grid(nchunks, d.nkv, sb.n);
     {
-    ProfScope ps_(c, K_ATTN_DECODE_PARTIAL);
-    switch (P) {
-        case 256:
-            hipLaunchKernelGGL(attn_decode_partial<256>, grid, dim3(NT), 0, c->stream, q_gate, k, v,
-                               L.q_norm, L.k_norm, L.k_cache, L.v_cache, c->rope_cos, c->rope_sin,
-                               part_o, part_ml, d.nkv, c->cap, nchunks, d.eps, sb);
-            break;
-        case 128:
-            hipLaunchKernelGGL(attn_decode_partial<128>, grid, dim3(NT), 0, c->stream, q_gate, k, v,
-                               L.q_norm, L.k_norm, L.k_cache, L.v_cache, c->rope_cos, c->rope_sin,
-                               part_o, part_ml, d.nkv, c->cap, nchunks, d.eps, sb);
-            break;
-        default:
-            hipLaunchKernelGGL(attn_decode_partial<64>, grid, dim3(NT), 0, c->stream, q_gate, k, v,
-                               L.q_norm, L.k_norm, L.k_cache, L.v_cache, c->rope_cos, c->rope_sin,
-                               part_o, part_ml, d.nkv, c->cap, nchunks, d.eps, sb);
-            break;
-    }
+        ProfScope ps_(c, K_ATTN_DECODE_PARTIAL);
+#define Q35_PARTIAL(NS)                                                                          \
+    hipLaunchKernelGGL(attn_decode_partial<NS>, grid, dim3(NT), 0, c->stream, q_gate, k, v,      \
+                       L.q_norm, L.k_norm, L.k_cache, L.v_cache, c->rope_cos, c->rope_sin,       \
+                       part_o, part_ml, d.nkv, c->cap, nchunks, d.eps, sb)
+        if (nsub == 4) Q35_PARTIAL(4);
+        else if (nsub == 2) Q35_PARTIAL(2);
+        else Q35_PARTIAL(1);
+#undef Q35_PARTIAL
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     {
         ProfScope ps_(c, K_ATTN_DECODE_MERGE);
-        hipLaunchKernelGGL(attn_decode_merge, dim3(d.nh, sb.n), dim3(kHd), 0, c->stream, part_o, part_ml,
-                           q_gate, out, d.nkv, nchunks, P, sb);
+        hipLaunchKernelGGL(attn_decode_merge, dim3(d.nh, sb.n), dim3(MT), 0, c->stream, part_o,
+                           part_ml, q_gate, out, d.nkv, nchunks, chunk, sb);
     }
     return hipGetLastError();
 }

@@ -18,41 +18,6 @@
 namespace q35 {
 namespace {
 
-__device__ __forceinline__ float4 rope_norm_row(float4 x, int lane, const float* __restrict__ cs,
-                                                const float* __restrict__ sn,
-                                                const float* __restrict__ w, float eps,
-                                                float post_scale) {
-    float4 p;
-    p.x = __shfl_xor(x.x, 8, kWave);
-    p.y = __shfl_xor(x.y, 8, kWave);
-    p.z = __shfl_xor(x.z, 8, kWave);
-    p.w = __shfl_xor(x.w, 8, kWave);
-    if (lane < 16) {
-        const int i0 = 4 * (lane & 7);
-        const float4 c = *reinterpret_cast<const float4*>(cs + i0);
-        const float4 s = *reinterpret_cast<const float4*>(sn + i0);
-        if (lane < 8) {
-            x.x = x.x * c.x - p.x * s.x;
-            x.y = x.y * c.y - p.y * s.y;
-            x.z = x.z * c.z - p.z * s.z;
-            x.w = x.w * c.w - p.w * s.w;
-        } else {
-            x.x = p.x * s.x + x.x * c.x;
-            x.y = p.y * s.y + x.y * c.y;
-            x.z = p.z * s.z + x.z * c.z;
-            x.w = p.w * s.w + x.w * c.w;
-        }
-    }
-    const float ss = wave_sum(x.x * x.x + x.y * x.y + x.z * x.z + x.w * x.w);
-    const float scale = 1.0f / sqrtf(ss / (float)kHd + eps);
-    const float4 ww = *reinterpret_cast<const float4*>(w + 4 * lane);
-    x.x = x.x * scale * (1.0f + ww.x) * post_scale;
-    x.y = x.y * scale * (1.0f + ww.y) * post_scale;
-    x.z = x.z * scale * (1.0f + ww.z) * post_scale;
-    x.w = x.w * scale * (1.0f + ww.w) * post_scale;
-    return x;
-}
-
 __global__ __launch_bounds__(kWave) void attn_prefill_prep(
     const float* __restrict__ q_gate, const float* __restrict__ knew,
     const float* __restrict__ vnew, const float* __restrict__ q_norm,

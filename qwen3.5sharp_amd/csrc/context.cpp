@@ -132,8 +132,9 @@ namespace q35 {
 const char* kernel_name(int id) {
     static const char* names[K_COUNT] = {
         "deltanet_decode_kernel", "deltanet_prefill_prep", "deltanet_conv_writeback",
-        "deltanet_prefill_scan",  "deltanet_gated_norm",   "attn_decode_partial",
-        "attn_decode_merge",      "attn_prefill_prep",     "attn_prefill_flash"};
+        "dn_chunk_prep",          "dn_chunk_scan",         "deltanet_gated_norm",
+        "attn_decode_partial",    "attn_decode_merge",     "attn_prefill_prep",
+        "attn_prefill_flash"};
     return (id >= 0 && id < K_COUNT) ? names[id] : nullptr;
 }
 
@@ -224,6 +225,8 @@ int q35m_create(const q35m_config* cfg, int n_seqs, int kv_capacity, q35m_ctx** 
         cfg->ssm_time_step_rank % cfg->ssm_group_count != 0)
         return fail(Q35M_ERR_INVALID, "ssm_time_step_rank must be a positive multiple of "
                                       "ssm_group_count");
+    if (cfg->ssm_time_step_rank / cfg->ssm_group_count > q35::kMaxVPerK)
+        return fail(Q35M_ERR_UNSUPPORTED, "at most %d v-heads per k-head", q35::kMaxVPerK);
     if (cfg->ssm_inner_size != cfg->ssm_time_step_rank * cfg->ssm_state_size)
         return fail(Q35M_ERR_INVALID, "ssm_inner_size must equal ssm_time_step_rank * "
                                       "ssm_state_size");
@@ -295,7 +298,6 @@ int q35m_create(const q35m_config* cfg, int n_seqs, int kv_capacity, q35m_ctx** 
             if (!r) r = alloc_zero(c, (void**)&L.k_norm, (size_t)q35::kHd * 4);
         }
     }
-    if (!r) r = alloc_zero(c, (void**)&c->counters, (size_t)q35::kMaxBatch * d.nk * sizeof(unsigned));
     if (!r) {
         c->rope_cap = kv_capacity > 4096 ? kv_capacity : 4096;
         std::vector<float> cs, sn;

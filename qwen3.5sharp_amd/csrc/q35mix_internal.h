@@ -20,6 +20,7 @@ constexpr int kRopeDim = 64;    // rotated dims
 constexpr int kRopeHalf = 32;
 constexpr int kGqaGroup = 4;    // q heads per kv head
 constexpr int kMaxBatch = 64;   // sequences per mixer launch
+constexpr int kMaxVPerK = 4;    // DeltaNet v-heads per k-head (one decode workgroup each)
 
 // Per-launch sequence batch, passed by value in the kernel arguments.
 struct SeqBatch {
@@ -53,7 +54,8 @@ enum KernelId {
     K_DN_DECODE = 0,
     K_DN_PREFILL_PREP,
     K_DN_CONV_WRITEBACK,
-    K_DN_PREFILL_SCAN,
+    K_DN_CHUNK_PREP,
+    K_DN_CHUNK_SCAN,
     K_DN_GATED_NORM,
     K_ATTN_DECODE_PARTIAL,
     K_ATTN_DECODE_MERGE,
@@ -88,7 +90,6 @@ struct q35m_ctx {
     float* rope_cos = nullptr;         // [rope_cap][32]
     float* rope_sin = nullptr;
     int rope_cap = 0;
-    unsigned* counters = nullptr;      // decode completion counters [kMaxBatch][nk]
     float* work = nullptr;             // scratch for split-K partials and prefill
     size_t work_bytes = 0;
     std::vector<void*> allocations;

@@ -286,3 +286,36 @@ def test_truncate_refuses_to_extend(ctx):
     with pytest.raises(q35mix.Q35Error) as ei:
         ctx.deltanet_decode(3, [0], *[ctx.array((1, 8))] * 5)   # layer 3 is full attention
     assert ei.value.code == q35mix.ERR_INVALID
+
+
+@pytest.mark.parametrize("lens", [[16383, 9000, 100, 16000], [8192, 8000, 5000, 7000]])
+def test_attn_decode_long_batch(lens):
+    """Four sequences at long contexts: exercises the multi-sub-chunk partial
+    kernel (4 and 2 sub-chunks of 64 rows per workgroup) and a long merge."""
+    n = len(lens)
+    with q35mix.Context(q35mix.qwen35_config(num_layers=1, is_recurrent=[0]), n_seqs=n,
+                        kv_capacity=16400) as c:
+        wts = synth.attn_weights(HD, salt=3)
+        c.set_attn_weights(0, wts)
+        caches = []
+        for s, L in enumerate(lens):
+            k, v = synth.kv_prefill(L, c.kv_dim, salt=70 + s)
+            c.state_write(0, s, q35mix.STATE_KEYS, k)
+            c.state_write(0, s, q35mix.STATE_VALUES, v)
+            c.advance(s, L)
+            caches.append((k, v))
+        x = synth.attn_inputs(n, NH, NKV, HD, salt=9)
+        qg, kk, vv = c.array((n, 2 * c.q_dim), x["q_gate"]), c.array((n, c.kv_dim), x["k"]), \
+            c.array((n, c.kv_dim), x["v"])
+        out = c.array((n, c.q_dim))
+        c.attn_decode(0, list(range(n)), qg, kk, vv, out)
+        got = out.download()
+        for s, L in enumerate(lens):
+            ck = np.zeros((L + 1, c.kv_dim), np.float32)
+            cv = np.zeros_like(ck)
+            ck[:L], cv[:L] = caches[s]
+            o_ref, _, _ = oracle.attn_decode(DIMS, L, x["q_gate"][s], x["k"][s], x["v"][s], wts,
+                                             ck, cv, n_threads=8)
+            e = rel(got[s], o_ref)
+            say(f"attn_decode long batch seq {s} len {L}: out rel err {e:.2e}")
+            assert e <= TOL
