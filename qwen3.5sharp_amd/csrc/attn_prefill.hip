@@ -9,9 +9,10 @@
 //
 //  1. attn_prefill_prep: rotate/norm q (scale folded in) into the workspace,
 //     rotate/norm K into the cache, copy V into the cache.
-//  2. attn_prefill_flash: causal flash attention, one workgroup per (q head,
-//     32-row query block), K/V streamed through LDS in 32-row tiles, online
-//     softmax; the [T][kvLen] score matrix is never materialised.
+//  2. attn_prefill_flash: causal flash attention on fp32 MFMA, one workgroup
+//     per (kv head, 16-row query block) with its 4 q heads, K/V streamed
+//     through LDS in 32-row tiles, online softmax; the [T][kvLen] score matrix
+//     is never materialised.
 #include "common.h"
 #include "q35mix_internal.h"
 
@@ -44,89 +45,154 @@ __global__ __launch_bounds__(kWave) void attn_prefill_prep(
     }
 }
 
-constexpr int QB = 32;   // query rows per workgroup
-constexpr int KT = 32;   // key rows per tile
-constexpr int KPAD = kHd + 4;
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-// Thread layout: row r = tid / 8 of the query block; sub = tid % 8 owns 32
-// interleaved dims.  Scores are reduced over the 8 lanes of a row.
-__global__ __launch_bounds__(256) void attn_prefill_flash(
+__device__ __forceinline__ f32x4 mfma16(float a, float b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+constexpr int QR = 16;          // query rows per workgroup (per head)
+constexpr int KT = 32;          // key rows per tile
+constexpr int LDKV = kHd + 4;   // padded LDS row stride of the K/V tiles
+
+// Causal flash attention on fp32 MFMA (v_mfma_f32_16x16x4f32).  Workgroup =
+// (kv head, 16 query rows); wave w is q head 4*kvh + w, so the 4 q heads of a
+// kv head share every K/V tile staged in LDS.  Per 32-row key tile a wave
+// computes S^T = K Q^T (positions x queries), so each lane's D column is one
+// query: the online-softmax max/sum and the rescale of O^T = V^T P^T are
+// per lane, and S^T's D tile feeds P^T = B operand register by register.
+// Lane l = 16g + c: Q operand holds Q[row c][64g + s], s < 64 (reduction index
+// of instruction s for lane group g), O^T register r of block db holds
+// O[row c][16 db + 4g + r].  The next K/V tile is loaded into registers while
+// the current one computes.  Heaviest query blocks are scheduled first.
+__global__ __launch_bounds__(256, 2) void attn_prefill_flash(
     const float* __restrict__ qbuf, const float* __restrict__ K, const float* __restrict__ V,
     const float* __restrict__ q_gate, float* __restrict__ out, int start, int T, int nh,
     int nkv) {
-    const int qb = blockIdx.x, h = blockIdx.y;
-    const int kvh = h / kGqaGroup;
+    const int qb = gridDim.x - 1 - blockIdx.x, kvh = blockIdx.y;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int g = lane >> 4, c16 = lane & 15;
+    const int h = kvh * kGqaGroup + wave;
     const int kv_dim = nkv * kHd;
-    const int tid = threadIdx.x, r = tid >> 3, sub = tid & 7;
-    const int t = qb * QB + r;
-    const bool valid = t < T;
-    const int my_len = start + (valid ? t : (T - 1)) + 1;   // visible rows of this query
-    const int blk_last = min(T - 1, qb * QB + QB - 1);
-    const int blk_len = start + blk_last + 1;                // rows the block must visit
+    const int r0 = qb * QR;
+    const int blk_len = start + min(T - 1, r0 + QR - 1) + 1;
+    const int my_t = min(r0 + c16, T - 1);
+    const int my_len = start + my_t + 1;
+    const float* Kh = K + (size_t)kvh * kHd;
+    const float* Vh = V + (size_t)kvh * kHd;
 
-    __shared__ float Ks[KT][KPAD];
-    __shared__ float Vs[KT][KPAD];
+    __shared__ float Ks[KT][LDKV];
+    __shared__ float Vs[KT][LDKV];
 
-    // Lane `sub` of a row owns dims sub, sub+8, ..., sub+248 (conflict-free LDS reads).
-    float q[32];
+    float qreg[64];
     {
-        const float* qrow = qbuf + ((size_t)(valid ? t : T - 1) * nh + h) * kHd + sub;
+        const float* qrow = qbuf + ((size_t)my_t * nh + h) * kHd + 64 * g;
 #pragma unroll
-        for (int d = 0; d < 32; ++d) q[d] = qrow[8 * d];
+        for (int u = 0; u < 16; ++u) {
+            const float4 x = *reinterpret_cast<const float4*>(qrow + 4 * u);
+            qreg[4 * u] = x.x; qreg[4 * u + 1] = x.y; qreg[4 * u + 2] = x.z; qreg[4 * u + 3] = x.w;
+        }
     }
-    float o[32];
+    f32x4 O[16];
 #pragma unroll
-    for (int d = 0; d < 32; ++d) o[d] = 0.0f;
-    float m = -INFINITY, l = 0.0f;
+    for (int db = 0; db < 16; ++db) O[db] = {0.f, 0.f, 0.f, 0.f};
+    float m_run = -INFINITY, l_run = 0.0f;
 
+    // Staging: thread loads float4 idx = tid + 256 i (i < 8) of the 32 x 64 float4 tile.
+    float4 sk[8], sv[8];
+    auto load_tile = [&](int p0) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int idx = tid + 256 * i, row = idx >> 6, c4 = idx & 63;
+            // Rows past blk_len read row 0 instead (finite data; their scores are
+            // masked), so no select waits on the loads before the next tile.
+            const int p = p0 + row;
+            const int pc = p < blk_len ? p : 0;
+            sk[i] = *reinterpret_cast<const float4*>(Kh + (size_t)pc * kv_dim + 4 * c4);
+            sv[i] = *reinterpret_cast<const float4*>(Vh + (size_t)pc * kv_dim + 4 * c4);
+        }
+    };
+    load_tile(0);
     for (int p0 = 0; p0 < blk_len; p0 += KT) {
-        __syncthreads();
-        // Stage K and V rows p0..p0+KT-1 (rows past blk_len are never used).
-        for (int idx = tid; idx < KT * (kHd / 4); idx += 256) {
-            const int pr = idx / (kHd / 4), c4 = idx % (kHd / 4);
-            const int p = p0 + pr;
-            float4 kx = make_float4(0.f, 0.f, 0.f, 0.f), vx = kx;
-            if (p < blk_len) {
-                kx = *reinterpret_cast<const float4*>(K + (size_t)p * kv_dim + kvh * kHd + 4 * c4);
-                vx = *reinterpret_cast<const float4*>(V + (size_t)p * kv_dim + kvh * kHd + 4 * c4);
+        lds_barrier();
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int idx = tid + 256 * i, row = idx >> 6, c4 = idx & 63;
+            *reinterpret_cast<float4*>(&Ks[row][4 * c4]) = sk[i];
+            *reinterpret_cast<float4*>(&Vs[row][4 * c4]) = sv[i];
+        }
+        lds_barrier();
+        if (p0 + KT < blk_len) load_tile(p0 + KT);
+
+        // S^T for positions p0 + 16 pb + (4g + r), queries c16.
+        f32x4 st[2];
+#pragma unroll
+        for (int pb = 0; pb < 2; ++pb) {
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int u = 0; u < 16; ++u) {
+                const float4 a = *reinterpret_cast<const float4*>(&Ks[16 * pb + c16][64 * g + 4 * u]);
+                acc = mfma16(a.x, qreg[4 * u], acc);
+                acc = mfma16(a.y, qreg[4 * u + 1], acc);
+                acc = mfma16(a.z, qreg[4 * u + 2], acc);
+                acc = mfma16(a.w, qreg[4 * u + 3], acc);
             }
-            *reinterpret_cast<float4*>(&Ks[pr][4 * c4]) = kx;
-            *reinterpret_cast<float4*>(&Vs[pr][4 * c4]) = vx;
+            st[pb] = acc;
         }
-        __syncthreads();
-        float s[KT];
+        // Online softmax down this lane's query column.
+        float mt = m_run;
 #pragma unroll
-        for (int pr = 0; pr < KT; ++pr) {
-            float a = 0.0f;
+        for (int pb = 0; pb < 2; ++pb)
 #pragma unroll
-            for (int d = 0; d < 32; ++d) a += q[d] * Ks[pr][sub + 8 * d];
-            s[pr] = group_sum<8>(a);
+            for (int r = 0; r < 4; ++r) {
+                const int p = p0 + 16 * pb + 4 * g + r;
+                if (p >= my_len) st[pb][r] = -INFINITY;
+                mt = fmaxf(mt, st[pb][r]);
+            }
+        mt = fmaxf(mt, __shfl_xor(mt, 16, kWave));
+        mt = fmaxf(mt, __shfl_xor(mt, 32, kWave));
+        const float alpha = __expf(m_run - mt);
+        float ls = 0.0f;
+#pragma unroll
+        for (int pb = 0; pb < 2; ++pb)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float e = __expf(st[pb][r] - mt);
+                st[pb][r] = e;
+                ls += e;
+            }
+        ls += __shfl_xor(ls, 16, kWave);
+        ls += __shfl_xor(ls, 32, kWave);
+        l_run = l_run * alpha + ls;
+        m_run = mt;
+        // O^T = alpha O^T + V^T P^T.
+#pragma unroll
+        for (int db = 0; db < 16; ++db) {
+            f32x4 acc = O[db] * alpha;
+#pragma unroll
+            for (int pb = 0; pb < 2; ++pb)
+#pragma unroll
+                for (int s2 = 0; s2 < 4; ++s2)
+                    acc = mfma16(Vs[16 * pb + 4 * g + s2][16 * db + c16], st[pb][s2], acc);
+            O[db] = acc;
         }
-        float mt = m;
-#pragma unroll
-        for (int pr = 0; pr < KT; ++pr) {
-            if (p0 + pr >= my_len) s[pr] = -INFINITY;
-            mt = fmaxf(mt, s[pr]);
-        }
-        const float alpha = m == -INFINITY ? 0.0f : __expf(m - mt);
-        l *= alpha;
-#pragma unroll
-        for (int d = 0; d < 32; ++d) o[d] *= alpha;
-#pragma unroll
-        for (int pr = 0; pr < KT; ++pr) {
-            const float e = s[pr] == -INFINITY ? 0.0f : __expf(s[pr] - mt);
-            l += e;
-#pragma unroll
-            for (int d = 0; d < 32; ++d) o[d] += e * Vs[pr][sub + 8 * d];
-        }
-        m = mt;
     }
-    if (!valid) return;
-    const float* grow = q_gate + (size_t)t * 2 * nh * kHd + (size_t)h * 2 * kHd + kHd + sub;
-    float* orow = out + ((size_t)t * nh + h) * kHd + sub;
-    const float inv = 1.0f / l;
+    const int t = r0 + c16;
+    if (t >= T) return;
+    const float inv = 1.0f / l_run;
+    const float* grow = q_gate + (size_t)t * 2 * nh * kHd + (size_t)h * 2 * kHd + kHd;
+    float* orow = out + ((size_t)t * nh + h) * kHd;
 #pragma unroll
-    for (int d = 0; d < 32; ++d) orow[8 * d] = o[d] * inv * (1.0f / (1.0f + expf(-grow[8 * d])));
+    for (int db = 0; db < 16; ++db) {
+        const int d0 = 16 * db + 4 * g;
+        const float4 gt = *reinterpret_cast<const float4*>(grow + d0);
+        float4 r;
+        r.x = O[db][0] * inv * (1.0f / (1.0f + expf(-gt.x)));
+        r.y = O[db][1] * inv * (1.0f / (1.0f + expf(-gt.y)));
+        r.z = O[db][2] * inv * (1.0f / (1.0f + expf(-gt.z)));
+        r.w = O[db][3] * inv * (1.0f / (1.0f + expf(-gt.w)));
+        *reinterpret_cast<float4*>(orow + d0) = r;
+    }
 }
 
 }  // namespace
@@ -152,8 +218,8 @@ hipError_t launch_attn_prefill(q35m_ctx* c, int layer, int seq, int start, int T
     if (e != hipSuccess) return e;
     {
         ProfScope ps_(c, K_ATTN_PREFILL_FLASH);
-        hipLaunchKernelGGL(attn_prefill_flash, dim3((T + QB - 1) / QB, d.nh), dim3(256), 0, c->stream,
-                           qbuf, K, V, q_gate, out, start, T, d.nh, d.nkv);
+        hipLaunchKernelGGL(attn_prefill_flash, dim3((T + QR - 1) / QR, d.nkv), dim3(256), 0,
+                           c->stream, qbuf, K, V, q_gate, out, start, T, d.nh, d.nkv);
     }
     return hipGetLastError();
 }

@@ -26,6 +26,14 @@ __device__ __forceinline__ float softplus_ref(float x) {
     return logf(1.0f + ex);
 }
 
+// Workgroup barrier for LDS exchange only: waits for this wave's LDS traffic
+// (lgkmcnt) and synchronises, but leaves global loads in flight, unlike
+// __syncthreads(), whose fence also drains vmcnt.  Prefetched operands of the
+// next step therefore keep streaming across the barrier.
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 // Butterfly sum over all 64 lanes of a wave.
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

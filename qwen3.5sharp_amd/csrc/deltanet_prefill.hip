@@ -68,77 +68,151 @@ __device__ __forceinline__ f32x4 mfma16x4(float4 a, f32x4 b, f32x4 acc) {
 }
 
 constexpr int CH = 64;        // chunk length
-constexpr int LDK = 132;      // padded LDS row stride of [64][128] tiles
+constexpr int CB = CH * kDk;  // floats in one [64 tokens][128] chunk block
 constexpr int LDA = 68;       // padded LDS row stride of [64][64] tiles
 
+// Operand layouts of one chunk block [64 tokens][128 dims], chosen so that
+// every MFMA operand is one coalesced float4 per lane (1 KiB per wave):
+//  A layout: lane (g, c) holds X[16 tb + c][16 kb + 4g + s], s = 0..3
+//            (the A operand of an MFMA whose reduction index is the dim).
+//  D layout: lane (g, c) holds X[16 tb + 4g + s][16 kb + c]
+//            (an MFMA D tile; also the A operand of a product reducing over
+//             tokens, e.g. K^T D).
+// Both are [4 tb][8 kb][64 lanes][4] inside the block.
+__device__ __forceinline__ int a_idx(int t, int d) {
+    return (((t >> 4) * 8 + (d >> 4)) * 64 + ((d >> 2) & 3) * 16 + (t & 15)) * 4 + (d & 3);
+}
+__device__ __forceinline__ const float4* blk4(const float* base, int tb, int kb, int lane) {
+    return reinterpret_cast<const float4*>(base + (size_t)((tb * 8 + kb) * 64 + lane) * 4);
+}
+
 struct PrefillWork {
-    float* qhat;   // [T][nk][dk]  L2-normed, scaled by 1/sqrt(dk)
-    float* khat;   // [T][nk][dk]
-    float* vv;     // [T][nv][dv]
+    float* qa;     // [nk][nch] chunk blocks, A layout: q^ (L2-normed, / sqrt(dk))
+    float* ka;     // [nk][nch] A layout: k^
+    float* kt;     // [nk][nch] D layout: k^
+    float* vd;     // [nv][nch] D layout: v
+    float* wa;     // [nv][nch] A layout: W
+    float* ud;     // [nv][nch] D layout: U
+    float* aqk;    // [nv][nch][4 rb][4 cb][64][4]: lane (g,c) holds (M o QK^T)[16rb+c][16cb+4g+s]
     float* beta;   // [T][nv]
     float* gl;     // [T][nv]   g (log decay)
-    float* core;   // [T][nv][dv] pre-norm recurrence output
-    float* W;      // [nv][nch][64][128]
-    float* U;      // [nv][nch][64][128]
-    float* Aqk;    // [nv][nch][64][64]
     float* gam;    // [nv][nch][64]   e^{G_i}
     float* gdec;   // [nv][nch][64]   e^{G_last - G_i}
+    float* core;   // [T][nv][dv] pre-norm recurrence output
 };
 
 size_t work_floats(const Dims& d, int T, int nch) {
-    return (size_t)T * (2 * d.key_dim + 2 * d.value_dim + 2 * d.nv) +
-           (size_t)d.nv * nch * (2 * CH * kDk + CH * CH + 2 * CH);
+    return (size_t)nch * CB * (3 * d.nk + 3 * d.nv) + (size_t)d.nv * nch * (CH * CH + 2 * CH) +
+           (size_t)T * (2 * d.nv + d.value_dim);
 }
 
 PrefillWork carve(float* w, const Dims& d, int T, int nch) {
     PrefillWork p;
-    p.qhat = w;
-    p.khat = p.qhat + (size_t)T * d.key_dim;
-    p.vv = p.khat + (size_t)T * d.key_dim;
-    p.beta = p.vv + (size_t)T * d.value_dim;
+    const size_t kblk = (size_t)d.nk * nch * CB, vblk = (size_t)d.nv * nch * CB;
+    p.qa = w;
+    p.ka = p.qa + kblk;
+    p.kt = p.ka + kblk;
+    p.vd = p.kt + kblk;
+    p.wa = p.vd + vblk;
+    p.ud = p.wa + vblk;
+    p.aqk = p.ud + vblk;
+    p.beta = p.aqk + (size_t)d.nv * nch * CH * CH;
     p.gl = p.beta + (size_t)T * d.nv;
-    p.core = p.gl + (size_t)T * d.nv;
-    p.W = p.core + (size_t)T * d.value_dim;
-    p.U = p.W + (size_t)d.nv * nch * CH * kDk;
-    p.Aqk = p.U + (size_t)d.nv * nch * CH * kDk;
-    p.gam = p.Aqk + (size_t)d.nv * nch * CH * CH;
+    p.gam = p.gl + (size_t)T * d.nv;
     p.gdec = p.gam + (size_t)d.nv * nch * CH;
+    p.core = p.gdec + (size_t)d.nv * nch * CH;
     return p;
 }
+
+// One workgroup per (16-token group, head block); a thread owns one channel
+// and slides the 4-tap window over the 16 tokens, so each qkv element is read
+// once.  Head blocks 0..nk-1 are q heads, nk..2nk-1 k heads, then v heads.
+// Groups past T (up to the end of the last chunk) write zeros.  The group's
+// 16 x 128 outputs are transposed through LDS and written as contiguous
+// 8 KiB runs of the chunk-block layouts.
+constexpr int PT = 16;
 
 __global__ __launch_bounds__(kDk) void deltanet_prefill_prep(
     const float* __restrict__ qkv, const float* __restrict__ bin, const float* __restrict__ ain,
     const float* __restrict__ conv_w, const float* __restrict__ ssm_a,
-    const float* __restrict__ dt_bias, PrefillWork w, int T, int nk, int nv, float eps) {
-    const int t = blockIdx.x, hb = blockIdx.y, tid = threadIdx.x;
+    const float* __restrict__ dt_bias, PrefillWork w, int T, int nk, int nv, int nch, float eps) {
+    const int tg = blockIdx.x, hb = blockIdx.y, tid = threadIdx.x;
+    const int t0 = tg * PT, n = tg >> 2, tb = tg & 3;
     const int key_dim = nk * kDk, conv_dim = 2 * key_dim + nv * kDk;
     int c;
     if (hb < nk) c = hb * kDk + tid;
     else if (hb < 2 * nk) c = key_dim + (hb - nk) * kDk + tid;
     else c = 2 * key_dim + (hb - 2 * nk) * kDk + tid;
-    float acc = 0.0f;
+    const float w0 = conv_w[c], w1 = conv_w[conv_dim + c], w2 = conv_w[2 * conv_dim + c],
+                w3 = conv_w[3 * conv_dim + c];
+    float x[PT + 3];
 #pragma unroll
-    for (int j = 0; j < kConvK; ++j)
-        if (t - j >= 0) acc += conv_w[(size_t)j * conv_dim + c] * qkv[(size_t)(t - j) * conv_dim + c];
-    const float y = silu(acc);
+    for (int j = 0; j < PT + 3; ++j) {
+        const int t = t0 - 3 + j;
+        const float xv = qkv[(size_t)min(max(t, 0), T - 1) * conv_dim + c];
+        x[j] = (t >= 0 && t < T) ? xv : 0.0f;
+    }
+    __shared__ float tile[PT][kDk + 4];
+    __shared__ float nrm[PT];
+    float y[PT];
+#pragma unroll
+    for (int j = 0; j < PT; ++j) {
+        // Taps in the reference's order: j = 0 (current) .. 3 (x[t-3]), zero pad.
+        float acc = w0 * x[j + 3];
+        acc += w1 * x[j + 2];
+        acc += w2 * x[j + 1];
+        acc += w3 * x[j];
+        y[j] = t0 + j < T ? silu(acc) : 0.0f;
+    }
+    float scale[PT];
     if (hb < 2 * nk) {
-        __shared__ float red[2];
-        const float ss = wave_sum(y * y);
-        if ((tid & 63) == 0) red[tid >> 6] = ss;
+        // Sum of squares per token: transpose through LDS, then thread
+        // (token tid/8, part tid%8) adds 16 channels and 8 lanes combine.
+#pragma unroll
+        for (int j = 0; j < PT; ++j) tile[j][tid] = y[j] * y[j];
         __syncthreads();
-        const float n2 = red[0] + red[1];
-        const int kh = hb < nk ? hb : hb - nk;
-        const size_t off = ((size_t)t * nk + kh) * kDk + tid;
-        if (hb < nk) w.qhat[off] = y * ((1.0f / sqrtf((float)kDk)) / sqrtf(n2 + eps));
-        else w.khat[off] = y * (1.0f / sqrtf(n2 + eps));
-    } else {
-        const int vh = hb - 2 * nk;
-        w.vv[((size_t)t * nv + vh) * kDk + tid] = y;
-        if (tid == 0) {
-            const size_t gi = (size_t)t * nv + vh;
-            w.beta[gi] = 1.0f / (1.0f + expf(-bin[gi]));
-            w.gl[gi] = ssm_a[vh] * softplus_ref(ain[gi] + dt_bias[vh]);
+        {
+            const int j = tid >> 3, part = tid & 7;
+            float a = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) a += tile[j][16 * part + e];
+            a = group_sum<8>(a);
+            if (part == 0) nrm[j] = a;
         }
+        __syncthreads();
+        const float pre = hb < nk ? 1.0f / sqrtf((float)kDk) : 1.0f;
+#pragma unroll
+        for (int j = 0; j < PT; ++j) scale[j] = pre / sqrtf(nrm[j] + eps);
+    } else {
+#pragma unroll
+        for (int j = 0; j < PT; ++j) scale[j] = 1.0f;
+    }
+#pragma unroll
+    for (int j = 0; j < PT; ++j) tile[j][tid] = y[j] * scale[j];
+    __syncthreads();
+    // Thread writes float4 o4 = tid + 128 i of the group's 512 (kb = o4/64, lane = o4%64).
+    const int head = hb < nk ? hb : (hb < 2 * nk ? hb - nk : hb - 2 * nk);
+    const size_t gbase = ((size_t)head * nch + n) * CB + (size_t)tb * 8 * 256;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int o4 = tid + 128 * i, kb = o4 >> 6, ln = o4 & 63, g = ln >> 4, cc = ln & 15;
+        const float4 av = *reinterpret_cast<const float4*>(&tile[cc][16 * kb + 4 * g]);
+        const float4 dv = make_float4(tile[4 * g][16 * kb + cc], tile[4 * g + 1][16 * kb + cc],
+                                      tile[4 * g + 2][16 * kb + cc], tile[4 * g + 3][16 * kb + cc]);
+        if (hb < nk) {
+            reinterpret_cast<float4*>(w.qa + gbase)[o4] = av;
+        } else if (hb < 2 * nk) {
+            reinterpret_cast<float4*>(w.ka + gbase)[o4] = av;
+            reinterpret_cast<float4*>(w.kt + gbase)[o4] = dv;
+        } else {
+            reinterpret_cast<float4*>(w.vd + gbase)[o4] = dv;
+        }
+    }
+    if (hb >= 2 * nk && tid < PT && t0 + tid < T) {
+        const int vh = hb - 2 * nk;
+        const size_t gi = (size_t)(t0 + tid) * nv + vh;
+        w.beta[gi] = 1.0f / (1.0f + expf(-bin[gi]));
+        w.gl[gi] = ssm_a[vh] * softplus_ref(ain[gi] + dt_bias[vh]);
     }
 }
 
@@ -176,8 +250,16 @@ __global__ void deltanet_conv_writeback(const float* __restrict__ qkv,
 __constant__ int kTriRb[10] = {0, 1, 1, 2, 2, 2, 3, 3, 3, 3};
 __constant__ int kTriCb[10] = {0, 0, 1, 0, 1, 2, 0, 1, 2, 3};
 
-__global__ __launch_bounds__(256) void dn_chunk_prep(PrefillWork w, int T, int nk, int nv,
-                                                     int nch) {
+// One workgroup per (k-head, chunk).  K K^T and (Q K^T)^T are formed once for
+// the R v-heads of the k-head (their 20 lower 16x16 blocks, 5 per wave, kept
+// in registers); every operand is a coalesced float4 of the chunk-block
+// layouts.  (Q K^T)^T = K Q^T comes out of the MFMA already in the A layout
+// of M o QK^T that dn_chunk_scan reads.  Per v-head: the decay masks, the
+// 16x16 diagonal-block inverses of I + A, and the blocked forward
+// substitution for W (written in the A layout through an LDS transpose) and
+// U (written in the D layout straight from the MFMA tile).
+__global__ __launch_bounds__(256, 2) void dn_chunk_prep(PrefillWork w, int T, int nk, int nv,
+                                                        int nch) {
     const int kh = blockIdx.x / nch, n = blockIdx.x % nch;
     const int R = nv / nk;
     const int t0 = n * CH;
@@ -185,48 +267,37 @@ __global__ __launch_bounds__(256) void dn_chunk_prep(PrefillWork w, int T, int n
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int g = lane >> 4, c16 = lane & 15;
 
-    __shared__ float Ks[CH][LDK];
-    __shared__ float QV[CH][LDK];    // Q^ of the chunk, then V of each v-head
-    __shared__ float KK[CH][LDA];
-    __shared__ float QK[CH][LDA];
-    __shared__ float Am[CH][LDA];    // -A (strictly lower)
-    __shared__ float Td[4][16][17];  // inverses of the 16x16 diagonal blocks of I + A
+    __shared__ float Am[CH][LDA];     // -A (strictly lower part of the lower blocks)
+    __shared__ float Td[4][16][17];   // inverses of the 16x16 diagonal blocks of I + A
+    __shared__ float tr[4][16][17];   // per-wave transpose scratch
     __shared__ double Gd[CH];
     __shared__ float bet[CH], gam[CH];
 
-    for (int idx = tid; idx < CH * (kDk / 4); idx += 256) {
-        const int r = idx / (kDk / 4), c4 = idx % (kDk / 4);
-        float4 kx = make_float4(0.f, 0.f, 0.f, 0.f), qx = kx;
-        if (r < tn) {
-            const size_t off = ((size_t)(t0 + r) * nk + kh) * kDk + 4 * c4;
-            kx = *reinterpret_cast<const float4*>(w.khat + off);
-            qx = *reinterpret_cast<const float4*>(w.qhat + off);
-        }
-        *reinterpret_cast<float4*>(&Ks[r][4 * c4]) = kx;
-        *reinterpret_cast<float4*>(&QV[r][4 * c4]) = qx;
-    }
-    __syncthreads();
+    const float* kA = w.ka + ((size_t)kh * nch + n) * CB;
+    const float* qA = w.qa + ((size_t)kh * nch + n) * CB;
+    const float* kD = w.kt + ((size_t)kh * nch + n) * CB;
 
-    // K K^T and Q K^T, lower 16x16 blocks only: 20 blocks, 5 per wave.
-    for (int bi = wave; bi < 20; bi += 4) {
-        const int mat = bi / 10, rb = kTriRb[bi % 10], cb = kTriCb[bi % 10];
-        const float(*src)[LDK] = mat ? QV : Ks;
-        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    // Block bi: bi < 10 -> K K^T block (rb, cb), rows 16rb + 4g + r, cols 16cb + c;
+    //           bi >= 10 -> (Q K^T)^T block: D rows = keys 16cb + 4g + r, cols = queries 16rb + c.
+    f32x4 blk[5];
 #pragma unroll
+    for (int m = 0; m < 5; ++m) {
+        const int bi = wave + 4 * m;
+        const int mat = bi / 10, rb = kTriRb[bi % 10], cb = kTriCb[bi % 10];
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll 2
         for (int q = 0; q < kDk / 16; ++q) {
-            const float4 a = *reinterpret_cast<const float4*>(&src[16 * rb + c16][16 * q + 4 * g]);
-            const float4 b = *reinterpret_cast<const float4*>(&Ks[16 * cb + c16][16 * q + 4 * g]);
+            const float4 a = mat ? *blk4(kA, cb, q, lane) : *blk4(kA, rb, q, lane);
+            const float4 b = mat ? *blk4(qA, rb, q, lane) : *blk4(kA, cb, q, lane);
             acc = mfma16(a.x, b.x, acc);
             acc = mfma16(a.y, b.y, acc);
             acc = mfma16(a.z, b.z, acc);
             acc = mfma16(a.w, b.w, acc);
         }
-        float(*dst)[LDA] = mat ? QK : KK;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) dst[16 * rb + 4 * g + r][16 * cb + c16] = acc[r];
+        blk[m] = acc;
     }
-    __syncthreads();
 
+#pragma unroll 1
     for (int rr = 0; rr < R; ++rr) {
         const int vh = kh * R + rr;
         const size_t cidx = (size_t)vh * nch + n;
@@ -235,7 +306,6 @@ __global__ __launch_bounds__(256) void dn_chunk_prep(PrefillWork w, int T, int n
             const int t = min(t0 + lane, T - 1);
             const bool valid = lane < tn;
             const float bv = w.beta[(size_t)t * nv + vh], gv = w.gl[(size_t)t * nv + vh];
-            const float b = valid ? bv : 0.0f;
             double G = valid ? (double)gv : 0.0;
 #pragma unroll
             for (int o = 1; o < 64; o <<= 1) {
@@ -243,61 +313,75 @@ __global__ __launch_bounds__(256) void dn_chunk_prep(PrefillWork w, int T, int n
                 if (lane >= o) G += up;
             }
             Gd[lane] = G;
-            bet[lane] = b;
-            gam[lane] = expf((float)G);
-            w.gam[cidx * CH + lane] = expf((float)G);
-        }
-        // V of this v-head (Q^ is no longer needed).
-        for (int idx = tid; idx < CH * (kDk / 4); idx += 256) {
-            const int r = idx / (kDk / 4), c4 = idx % (kDk / 4);
-            float4 vx = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (r < tn) vx = *reinterpret_cast<const float4*>(w.vv + ((size_t)(t0 + r) * nv + vh) * kDk + 4 * c4);
-            *reinterpret_cast<float4*>(&QV[r][4 * c4]) = vx;
+            bet[lane] = valid ? bv : 0.0f;
+            const float gm = expf((float)G);
+            gam[lane] = gm;
+            w.gam[cidx * CH + lane] = gm;
         }
         __syncthreads();
         if (wave == 1) w.gdec[cidx * CH + lane] = expf((float)(Gd[CH - 1] - Gd[lane]));
-        // Decay masks: -A (strictly lower) into LDS, M o QK^T to the workspace.
-        float* aqk = w.Aqk + cidx * CH * CH;
-        for (int idx = tid; idx < CH * CH; idx += 256) {
-            const int i = idx / CH, j = idx % CH;
-            const float dcy = j <= i ? expf((float)(Gd[i] - Gd[j])) : 0.0f;
-            Am[i][j] = j < i ? -bet[i] * dcy * KK[i][j] : 0.0f;
-            aqk[idx] = j <= i ? dcy * QK[i][j] : 0.0f;
+        // Decay masks on the register blocks: -A into LDS, M o QK^T to the workspace.
+        float* aqk = w.aqk + cidx * CH * CH;
+#pragma unroll
+        for (int m = 0; m < 5; ++m) {
+            const int bi = wave + 4 * m;
+            const int mat = bi / 10, rb = kTriRb[bi % 10], cb = kTriCb[bi % 10];
+            if (mat == 0) {
+                const int j = 16 * cb + c16;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int i = 16 * rb + 4 * g + r;
+                    Am[i][j] = j < i ? -bet[i] * expf((float)(Gd[i] - Gd[j])) * blk[m][r] : 0.0f;
+                }
+            } else {
+                const int iq = 16 * rb + c16;   // query token
+                float4 v;
+                float* vp = reinterpret_cast<float*>(&v);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int jk = 16 * cb + 4 * g + r;   // key token
+                    vp[r] = jk <= iq ? expf((float)(Gd[iq] - Gd[jk])) * blk[m][r] : 0.0f;
+                }
+                reinterpret_cast<float4*>(aqk)[(rb * 4 + cb) * 64 + lane] = v;
+            }
         }
         __syncthreads();
         // Inverse of each unit-lower 16x16 diagonal block of I + A by forward
-        // substitution: column j of the inverse, x_i = sum_{m<i} (-A)_im x_m.
+        // substitution: column j of the inverse, x_i = [i == j] + sum_{m<i} (-A)_im x_m.
         if (lane < 16) {
             const int j = lane, b0 = 16 * wave;
             float x[16];
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
-                float s = i == j ? 1.0f : 0.0f;
+                float acc = i == j ? 1.0f : 0.0f;
 #pragma unroll
-                for (int m = 0; m < i; ++m) s += Am[b0 + i][b0 + m] * x[m];
-                x[i] = i < j ? 0.0f : s;
+                for (int m = 0; m < i; ++m) acc += Am[b0 + i][b0 + m] * x[m];
+                x[i] = i < j ? 0.0f : acc;
             }
 #pragma unroll
             for (int i = 0; i < 16; ++i) Td[wave][i][j] = x[i];
         }
         __syncthreads();
         // Y = (I + A)^-1 X for X = diag(beta gamma) K^ (-> W) and diag(beta) V (-> U),
-        // block row by block row; wave takes column blocks wave + 4k of the 16.
+        // block row by block row; the wave takes column blocks wave + 4k of the 16.
+        const float* vD = w.vd + cidx * CB;
+        float* wA = w.wa + cidx * CB;
+        float* uD = w.ud + cidx * CB;
+#pragma unroll 1
         for (int k4 = 0; k4 < 4; ++k4) {
             const int cbk = wave + 4 * k4;
             const bool isV = cbk >= 8;
-            const int cc = (cbk & 7) * 16;
-            const float(*src)[LDK] = isV ? QV : Ks;
-            float* dst = (isV ? w.U : w.W) + cidx * CH * kDk;
+            const int kb = cbk & 7;
             f32x4 Y[4];
 #pragma unroll
             for (int ib = 0; ib < 4; ++ib) {
+                const float4 xv = isV ? *blk4(vD, ib, kb, lane) : *blk4(kD, ib, kb, lane);
+                const float* xp = reinterpret_cast<const float*>(&xv);
                 f32x4 acc;
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const int row = 16 * ib + 4 * g + r;
-                    const float sc = isV ? bet[row] : bet[row] * gam[row];
-                    acc[r] = src[row][cc + c16] * sc;
+                    acc[r] = xp[r] * (isV ? bet[row] : bet[row] * gam[row]);
                 }
 #pragma unroll
                 for (int jb = 0; jb < ib; ++jb) {
@@ -306,16 +390,72 @@ __global__ __launch_bounds__(256) void dn_chunk_prep(PrefillWork w, int T, int n
                 }
                 const float4 tdv = make_float4(Td[ib][c16][4 * g], Td[ib][c16][4 * g + 1],
                                                Td[ib][c16][4 * g + 2], Td[ib][c16][4 * g + 3]);
-                f32x4 y = {0.f, 0.f, 0.f, 0.f};
-                Y[ib] = mfma16x4(tdv, acc, y);
+                const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
+                Y[ib] = mfma16x4(tdv, acc, zero);
+                if (isV) {
+                    reinterpret_cast<float4*>(uD)[(ib * 8 + kb) * 64 + lane] =
+                        make_float4(Y[ib][0], Y[ib][1], Y[ib][2], Y[ib][3]);
+                } else {
+                    // D tile -> A layout: element (token 4g+r, dim c16) moves to
+                    // lane (dim/4 = c16/4, token) slot c16%4.
 #pragma unroll
-                for (int r = 0; r < 4; ++r) dst[(16 * ib + 4 * g + r) * kDk + cc + c16] = Y[ib][r];
+                    for (int r = 0; r < 4; ++r) tr[wave][4 * g + r][c16] = Y[ib][r];
+                    __builtin_amdgcn_wave_barrier();
+                    const float4 av = make_float4(tr[wave][c16][4 * g], tr[wave][c16][4 * g + 1],
+                                                  tr[wave][c16][4 * g + 2], tr[wave][c16][4 * g + 3]);
+                    __builtin_amdgcn_wave_barrier();
+                    reinterpret_cast<float4*>(wA)[(ib * 8 + kb) * 64 + lane] = av;
+                }
             }
         }
         __syncthreads();
     }
 }
 
+// Operands of one chunk for one wave of dn_chunk_scan, each a coalesced float4
+// per lane; none depends on the state, so the next chunk's set is loaded while
+// the current one computes.
+struct ScanOps {
+    float4 wa[4][2], qa[4][2];   // W, Q^ (A operands of W S and Q S)
+    float4 kt[4][2];             // K^ (A operand of K^T D)
+    float4 aa[4];                // M o QK^T row block `wave`, column blocks 0..3
+    float4 ut[4];                // U, all token blocks, this column tile
+    float4 gdv[4];               // e^{G_last - G}
+    float4 gmo;                  // gamma for token block `wave`
+    float glast;                 // gamma_last
+};
+
+__device__ __forceinline__ void load_scan_ops(const PrefillWork& w, ScanOps& o, int n, int vh,
+                                              int kh, int tl, int nch, int wave, int g,
+                                              int lane) {
+    const size_t cidx = (size_t)vh * nch + n, kidx = (size_t)kh * nch + n;
+    const float* wA = w.wa + cidx * CB;
+    const float* qA = w.qa + kidx * CB;
+    const float* kD = w.kt + kidx * CB;
+    const float* uD = w.ud + cidx * CB;
+    const float4* aq = reinterpret_cast<const float4*>(w.aqk + cidx * CH * CH);
+    const float* gm = w.gam + cidx * CH;
+    const float* gd = w.gdec + cidx * CH;
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb) {
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            o.wa[tb][b] = *blk4(wA, tb, 2 * wave + b, lane);
+            o.qa[tb][b] = *blk4(qA, tb, 2 * wave + b, lane);
+            o.kt[tb][b] = *blk4(kD, tb, 2 * wave + b, lane);
+        }
+        o.aa[tb] = aq[(wave * 4 + tb) * 64 + lane];
+        o.ut[tb] = *blk4(uD, tb, tl, lane);
+        o.gdv[tb] = *reinterpret_cast<const float4*>(gd + 16 * tb + 4 * g);
+    }
+    o.gmo = *reinterpret_cast<const float4*>(gm + 16 * wave + 4 * g);
+    o.glast = gm[CH - 1];
+}
+
+__device__ __forceinline__ f32x4 v4(float4 a) { return f32x4{a.x, a.y, a.z, a.w}; }
+
+// One workgroup per (v-head, 16-column tile); wave w owns state rows
+// 32w..32w+31 of the tile (two D-layout 16x16 tiles, kept across chunks).
 __global__ __launch_bounds__(256) void dn_chunk_scan(PrefillWork w, float* __restrict__ state,
                                                      int T, int nk, int nv, int nch) {
     const int L = xcd_remap(blockIdx.x, gridDim.x);
@@ -326,105 +466,67 @@ __global__ __launch_bounds__(256) void dn_chunk_scan(PrefillWork w, float* __res
     const int col = 16 * tl + c16;
     float* S = state + (size_t)vh * kDk * kDk;
 
-    // State rows 32*wave + 16b + 4g + r, column col, as two D-layout tiles.
     f32x4 Sb[2];
 #pragma unroll
     for (int b = 0; b < 2; ++b)
 #pragma unroll
         for (int r = 0; r < 4; ++r) Sb[b][r] = S[(size_t)(32 * wave + 16 * b + 4 * g + r) * kDk + col];
 
-    __shared__ f32x4 red[4][2][4][64];
-    __shared__ f32x4 dl[4][64];
+    // Partials of W S and Q S per wave, double-buffered by chunk parity so one
+    // barrier per chunk suffices.
+    __shared__ f32x4 red[2][4][2][4][64];
 
+    ScanOps cur, nxt;
+    load_scan_ops(w, cur, 0, vh, kh, tl, nch, wave, g, lane);
     for (int n = 0; n < nch; ++n) {
         const int t0 = n * CH;
-        const size_t cidx = (size_t)vh * nch + n;
-        const float* Wc = w.W + cidx * CH * kDk;
-        const float* Uc = w.U + cidx * CH * kDk;
-        const float* Ac = w.Aqk + cidx * CH * CH;
-        const float* gm = w.gam + cidx * CH;
-        const float* gd = w.gdec + cidx * CH;
-
-        // Loads that do not depend on the state go out first.
-        float kT[4][2][4];
-#pragma unroll
-        for (int tb = 0; tb < 4; ++tb)
-#pragma unroll
-            for (int s = 0; s < 4; ++s) {
-                const int t = min(t0 + 16 * tb + 4 * g + s, T - 1);
-                const float* kr = w.khat + ((size_t)t * nk + kh) * kDk + 32 * wave + c16;
-                kT[tb][0][s] = kr[0];
-                kT[tb][1][s] = kr[16];
-            }
-        f32x4 uu, gmo, gdv[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            uu[r] = Uc[(size_t)(16 * wave + 4 * g + r) * kDk + col];
-            gmo[r] = gm[16 * wave + 4 * g + r];
-        }
-#pragma unroll
-        for (int tb = 0; tb < 4; ++tb)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) gdv[tb][r] = gd[16 * tb + 4 * g + r];
-        const float glast = gm[CH - 1];
-
+        if (n + 1 < nch) load_scan_ops(w, nxt, n + 1, vh, kh, tl, nch, wave, g, lane);
+        const int par = n & 1;
         // Partial W S and Q S over this wave's 32 state rows, all 4 token blocks.
-        f32x4 pws[4], pqs[4];
 #pragma unroll
         for (int tb = 0; tb < 4; ++tb) {
-            pws[tb] = {0.f, 0.f, 0.f, 0.f};
-            pqs[tb] = {0.f, 0.f, 0.f, 0.f};
-            const int tq = min(t0 + 16 * tb + c16, T - 1);
+            f32x4 pws = {0.f, 0.f, 0.f, 0.f}, pqs = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int b = 0; b < 2; ++b) {
-                const int k0 = 32 * wave + 16 * b + 4 * g;
-                const float4 wa = *reinterpret_cast<const float4*>(Wc + (size_t)(16 * tb + c16) * kDk + k0);
-                const float4 qa = *reinterpret_cast<const float4*>(w.qhat + ((size_t)tq * nk + kh) * kDk + k0);
-                pws[tb] = mfma16x4(wa, Sb[b], pws[tb]);
-                pqs[tb] = mfma16x4(qa, Sb[b], pqs[tb]);
+                pws = mfma16x4(cur.wa[tb][b], Sb[b], pws);
+                pqs = mfma16x4(cur.qa[tb][b], Sb[b], pqs);
             }
-            red[wave][0][tb][lane] = pws[tb];
-            red[wave][1][tb][lane] = pqs[tb];
+            red[par][wave][0][tb][lane] = pws;
+            red[par][wave][1][tb][lane] = pqs;
         }
-        __syncthreads();
-        // Token block `wave`: D = U - W S, and the Q S rows of the output.
-        f32x4 ws = red[0][0][wave][lane], qs = red[0][1][wave][lane];
-#pragma unroll
-        for (int v = 1; v < 4; ++v) {
-            ws += red[v][0][wave][lane];
-            qs += red[v][1][wave][lane];
-        }
-        dl[wave][lane] = uu - ws;
-        __syncthreads();
+        lds_barrier();
+        // Every wave forms D = U - W S for all 4 token blocks (it needs them all
+        // for its rows of the state update), and Q S for its token block `wave`.
         f32x4 D[4];
 #pragma unroll
-        for (int tb = 0; tb < 4; ++tb) D[tb] = dl[tb][lane];
-
-        // O rows of token block `wave` = gamma Q S + (M o QK^T) D (causal: blocks <= wave).
-        f32x4 o = gmo * qs;
-        for (int tb = 0; tb <= wave; ++tb) {
-            const float4 aa = *reinterpret_cast<const float4*>(Ac + (size_t)(16 * wave + c16) * CH + 16 * tb + 4 * g);
-            o = mfma16x4(aa, D[tb], o);
+        for (int tb = 0; tb < 4; ++tb) {
+            f32x4 ws = red[par][0][0][tb][lane];
+#pragma unroll
+            for (int v = 1; v < 4; ++v) ws += red[par][v][0][tb][lane];
+            D[tb] = v4(cur.ut[tb]) - ws;
         }
+        f32x4 qs = red[par][0][1][wave][lane];
+#pragma unroll
+        for (int v = 1; v < 4; ++v) qs += red[par][v][1][wave][lane];
+        // S = gamma_last S + K^T (e^{G_last - G} D).
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+            f32x4 acc = Sb[b] * cur.glast;
+#pragma unroll
+            for (int tb = 0; tb < 4; ++tb) acc = mfma16x4(cur.kt[tb][b], D[tb] * v4(cur.gdv[tb]), acc);
+            Sb[b] = acc;
+        }
+        // O rows of token block `wave` = gamma Q S + (M o QK^T) D (causal: blocks <= wave).
+        f32x4 o = v4(cur.gmo) * qs;
+#pragma unroll
+        for (int tb = 0; tb < 4; ++tb)
+            if (tb <= wave) o = mfma16x4(cur.aa[tb], D[tb], o);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int t = t0 + 16 * wave + 4 * g + r;
             if (t < T) w.core[((size_t)t * nv + vh) * kDk + col] = o[r];
         }
-        // S = gamma_last S + K^T (e^{G_last - G} D).
-#pragma unroll
-        for (int b = 0; b < 2; ++b) {
-            f32x4 acc = Sb[b] * glast;
-#pragma unroll
-            for (int tb = 0; tb < 4; ++tb) {
-                const f32x4 dd = D[tb] * gdv[tb];
-                acc = mfma16(kT[tb][b][0], dd[0], acc);
-                acc = mfma16(kT[tb][b][1], dd[1], acc);
-                acc = mfma16(kT[tb][b][2], dd[2], acc);
-                acc = mfma16(kT[tb][b][3], dd[3], acc);
-            }
-            Sb[b] = acc;
-        }
+        cur = nxt;
     }
 #pragma unroll
     for (int b = 0; b < 2; ++b)
@@ -432,20 +534,24 @@ __global__ __launch_bounds__(256) void dn_chunk_scan(PrefillWork w, float* __res
         for (int r = 0; r < 4; ++r) S[(size_t)(32 * wave + 16 * b + 4 * g + r) * kDk + col] = Sb[b][r];
 }
 
-// Qwen35Ops.GatedRmsNorm (Qwen35Ops.cs:74-111) over rows of dv = 128.
-__global__ __launch_bounds__(kDk) void deltanet_gated_norm(const float* __restrict__ core,
+// Qwen35Ops.GatedRmsNorm (Qwen35Ops.cs:74-111) over rows of dv = 128: one
+// wave per row, two values per lane; four rows per workgroup.
+__global__ __launch_bounds__(256) void deltanet_gated_norm(const float* __restrict__ core,
                                                            const float* __restrict__ z,
                                                            const float* __restrict__ wnorm,
-                                                           float* __restrict__ out, float eps) {
-    const size_t row = blockIdx.x;
-    const int e = threadIdx.x;
-    const float x = core[row * kDk + e];
-    __shared__ float red[2];
-    const float ss = wave_sum(x * x);
-    if ((e & 63) == 0) red[e >> 6] = ss;
-    __syncthreads();
-    const float rs = 1.0f / sqrtf((red[0] + red[1]) / (float)kDk + eps);
-    out[row * kDk + e] = x * rs * wnorm[e] * silu(z[row * kDk + e]);
+                                                           float* __restrict__ out, float eps,
+                                                           size_t rows) {
+    const size_t row = (size_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    const float2 x = reinterpret_cast<const float2*>(core + row * kDk)[lane];
+    const float2 zz = reinterpret_cast<const float2*>(z + row * kDk)[lane];
+    const float2 ww = reinterpret_cast<const float2*>(wnorm)[lane];
+    const float rs = 1.0f / sqrtf(wave_sum(x.x * x.x + x.y * x.y) / (float)kDk + eps);
+    float2 r;
+    r.x = x.x * rs * ww.x * silu(zz.x);
+    r.y = x.y * rs * ww.y * silu(zz.y);
+    reinterpret_cast<float2*>(out + row * kDk)[lane] = r;
 }
 
 }  // namespace
@@ -465,9 +571,9 @@ hipError_t launch_deltanet_prefill(q35m_ctx* c, int layer, int seq, int T, const
     hipError_t e;
     {
         ProfScope ps_(c, K_DN_PREFILL_PREP);
-        hipLaunchKernelGGL(deltanet_prefill_prep, dim3(T, 2 * d.nk + d.nv), dim3(kDk), 0,
-                           c->stream, qkv, b, a, L.conv_w, L.ssm_a, L.dt_bias, w, T, d.nk, d.nv,
-                           d.eps);
+        hipLaunchKernelGGL(deltanet_prefill_prep, dim3(nch * (CH / PT), 2 * d.nk + d.nv), dim3(kDk),
+                           0, c->stream, qkv, b, a, L.conv_w, L.ssm_a, L.dt_bias, w, T, d.nk,
+                           d.nv, nch, d.eps);
     }
     if ((e = hipGetLastError()) != hipSuccess) return e;
     {
@@ -490,8 +596,9 @@ hipError_t launch_deltanet_prefill(q35m_ctx* c, int layer, int seq, int T, const
     if ((e = hipGetLastError()) != hipSuccess) return e;
     {
         ProfScope ps_(c, K_DN_GATED_NORM);
-        hipLaunchKernelGGL(deltanet_gated_norm, dim3((unsigned)T * d.nv), dim3(kDk), 0, c->stream,
-                           w.core, z, L.ssm_norm, out, d.eps);
+        const size_t rows = (size_t)T * d.nv;
+        hipLaunchKernelGGL(deltanet_gated_norm, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0,
+                           c->stream, w.core, z, L.ssm_norm, out, d.eps, rows);
     }
     return hipGetLastError();
 }
