@@ -17,6 +17,7 @@ timers in a second, separately timed pass.
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import sys
@@ -47,8 +48,26 @@ def attn_decode_bytes(kv_len: int) -> int:
 
 
 DN_PREFILL_FLOP = 11_811_160_064           # T=2048, chunked WY form (32 heads x 32 chunks)
-DN_SCAN_FLOP_PER_TOKEN = 7 * DK * DK * NV   # sequential delta rule: 7 dk dv per head-token
+# Per-kernel algorithmic FLOP of one T=2048 DeltaNet prefill (C = 64, 32 chunks, 32 v-heads):
+#  dn_chunk_scan: W S, Q S, K^T D (3 x 2 C dk dv) + (M o QK^T) D (2 C^2 dv) per chunk-head
+#  dn_chunk_prep: K K^T, Q K^T (2 x 2 C^2 dk, once per k-head) + W, U (2 x 2 C^2 dk per v-head)
+DN_SCAN_FLOP = 32 * 32 * (3 * 2 * 64 * DK * DK + 2 * 64 * 64 * DK)
+DN_CPREP_FLOP = 32 * 16 * 2 * 2 * 64 * 64 * DK + 32 * 32 * 2 * 2 * 64 * 64 * DK
 ATTN_PREFILL_FLOP = 4 * HD * NH * 2048 * 2049 // 2
+PROFILES = os.path.join(ROOT, "profiles")
+
+
+def measured_traffic(kernel: str):
+    """HBM bytes per launch of `kernel` from the committed PMC summary
+    (profiles/<kernel>_traffic.txt, line 'bytes_per_launch: N'), or None."""
+    path = os.path.join(PROFILES, f"{kernel}_traffic.txt")
+    try:
+        for line in open(path):
+            if line.startswith("bytes_per_launch:"):
+                return int(float(line.split(":", 1)[1]))
+    except OSError:
+        pass
+    return None
 
 
 def log(*a):
@@ -278,6 +297,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default="", help="comma list of: dn_prefill,dn_decode,attn_decode,"
                                                "attn_prefill,stack")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="also run one device-to-device copy of MIB MiB (a plain copy kernel "
+                         "of known traffic, to scale FETCH_SIZE/WRITE_SIZE counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one MI355X only; --gpus {args.gpus} is not supported "
@@ -293,19 +315,37 @@ def main():
     workloads = {}
     result = None
 
+    if args.copy_calibration:
+        nbytes = args.copy_calibration << 20
+        ctx = q35mix.Context(q35mix.qwen35_config(num_layers=1, is_recurrent=[1]), 1, 16)
+        src, dst = ctx.array((nbytes // 4,)), ctx.array((nbytes // 4,))
+        hip = q35mix.hip()
+        hip.hipMemcpyAsync.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t,
+                                       ctypes.c_int, ctypes.c_void_p]
+        r = hip.hipMemcpyAsync(ctypes.c_void_p(dst.ptr), ctypes.c_void_p(src.ptr), nbytes, 3,
+                               ctypes.c_void_p(ctx.stream))
+        if r != 0:
+            raise RuntimeError(f"hipMemcpyAsync failed: {r}")
+        ctx.sync()
+        log(f"[bench] calibration copy: {nbytes} bytes device to device")
+        ctx.close()
+
     if want("dn_prefill"):
         log("[bench] DeltaNet prefill T=2048 ...")
         ms, kt, x = bench_dn_prefill(K, W)
         tok_s = 2048 / (ms / 1e3)
         kname, kms = dominant(kt)
         log(f"[bench] DeltaNet prefill: {ms:.3f} ms/step, {tok_s:.0f} tok/s; kernels {kt}")
-        scan_flop = DN_SCAN_FLOP_PER_TOKEN * 2048
-        roof = {"bound": "mfma", "achieved": scan_flop / (kms / 1e3) / 1e12,
+        kflop = {"dn_chunk_scan": DN_SCAN_FLOP, "dn_chunk_prep": DN_CPREP_FLOP}.get(kname)
+        if kflop is None:
+            raise RuntimeError(f"no algorithmic FLOP count for dominant kernel {kname}")
+        roof = {"bound": "mfma", "achieved": kflop / (kms / 1e3) / 1e12,
                 "peak": FP32_PEAK / 1e12, "unit": "TFLOP/s",
-                "frac": scan_flop / (kms / 1e3) / FP32_PEAK, "traffic": None,
+                "frac": kflop / (kms / 1e3) / FP32_PEAK, "traffic": measured_traffic(kname),
                 "kernel": kname, "kernel_ms": kms,
-                "algorithmic": f"{scan_flop} FLOP per launch (7*dk*dv per head-token, 32 heads, "
-                               "2048 tokens)"}
+                "algorithmic": f"{kflop} FLOP per launch (fp32 MFMA products of one 2048-token "
+                               "layer: 32 v-heads x 32 chunks of 64)",
+                "kernels_ms": {k: v[0] for k, v in kt.items()}}
         cpu = None
         if not args.no_cpu:
             log("[bench] CPU restatement, one 2048-token DeltaNet prefill layer ...")
