@@ -146,7 +146,10 @@ int q35m_attn_prefill(q35m_ctx* ctx, int layer, int seq, int T, const float* q_g
 int q35m_state_read(q35m_ctx* ctx, int layer, int seq, int kind, void* host, size_t bytes);
 int q35m_state_write(q35m_ctx* ctx, int layer, int seq, int kind, const void* host,
                      size_t bytes);
-/* Device address and size of one state buffer, for zero-copy callers. */
+/* Device address and size of one state buffer, for zero-copy callers.  The
+ * conv window is double-buffered on the device (decode reads one buffer and
+ * writes the shifted window to the other), so the Q35M_STATE_CONV address is
+ * valid until the next q35m_deltanet_decode of that layer and sequence. */
 int q35m_state_device_ptr(q35m_ctx* ctx, int layer, int seq, int kind, void** dptr,
                           size_t* bytes);
 

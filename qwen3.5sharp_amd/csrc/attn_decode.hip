@@ -206,23 +206,28 @@ __global__ __launch_bounds__(NT, 2) void attn_decode_partial(
     }
 }
 
-// Merge of the chunk partials of one (sequence, q head): 512 threads; thread
-// holds 4 dims (d4 = t % 64) and merges chunks c = t / 64 (mod 8); the chunk
-// weights exp(m_c - M) come from one shared maximum M.
-constexpr int MT = 512;
+// Merge of the chunk partials of one (sequence, q head, 64-dim slice): 256
+// threads; thread holds 4 dims (d4 = t % 16) of the slice and merges chunks
+// c = t / 16 (mod 16); the chunk weights exp(m_c - M) come from one shared
+// maximum M over all chunks of the head.
+constexpr int MT = 256;
+constexpr int MSLICE = 64;                 // dims per merge workgroup
+constexpr int MD4 = MSLICE / 4;            // float4 columns per slice
+constexpr int MG = MT / MD4;               // chunk groups
 
 __global__ __launch_bounds__(MT) void attn_decode_merge(
     const float* __restrict__ part_o, const float* __restrict__ part_ml,
     const float* __restrict__ q_gate, float* __restrict__ out, int nkv, int nchunks, int chunk,
     SeqBatch sb) {
-    const int h = blockIdx.x, i = blockIdx.y, t = threadIdx.x;
+    const int h = blockIdx.x / (kHd / MSLICE), slice = blockIdx.x % (kHd / MSLICE);
+    const int i = blockIdx.y, t = threadIdx.x;
     const int nh = nkv * kGqaGroup;
     const int kvh = h / kGqaGroup, hl = h % kGqaGroup;
     const int nc = (sb.pos[i] + chunk) / chunk;
     const size_t base = ((size_t)i * nkv + kvh) * nchunks;
     __shared__ float red[MT / kWave];
-    __shared__ float4 obuf[MT / kWave][kHd / 4];
-    __shared__ float lbuf[MT / kWave];
+    __shared__ float4 obuf[MG][MD4];
+    __shared__ float lbuf[MG];
 
     float mx = -INFINITY;
     for (int c = t; c < nc; c += MT) mx = fmaxf(mx, part_ml[2 * ((base + c) * kGqaGroup + hl)]);
@@ -233,37 +238,39 @@ __global__ __launch_bounds__(MT) void attn_decode_merge(
 #pragma unroll
     for (int w = 1; w < MT / kWave; ++w) M = fmaxf(M, red[w]);
 
-    const int d4 = t & 63, g = t >> 6;
+    const int d4 = t % MD4, g = t / MD4;
+    const int col = slice * MD4 + d4;
     float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
     float l = 0.0f;
 #pragma unroll 4
-    for (int c = g; c < nc; c += MT / kWave) {
+    for (int c = g; c < nc; c += MG) {
         const size_t pidx = (base + c) * kGqaGroup + hl;
         const float wgt = __expf(part_ml[2 * pidx] - M);
-        const float4 oc = reinterpret_cast<const float4*>(part_o + pidx * kHd)[d4];
+        const float4 oc = reinterpret_cast<const float4*>(part_o + pidx * kHd)[col];
         l += wgt * part_ml[2 * pidx + 1];
         o.x += wgt * oc.x; o.y += wgt * oc.y; o.z += wgt * oc.z; o.w += wgt * oc.w;
     }
     obuf[g][d4] = o;
     if (d4 == 0) lbuf[g] = l;
     __syncthreads();
-    if (t < kHd / 4) {
+    if (t < MD4) {
         float4 s = obuf[0][t];
         float L = lbuf[0];
 #pragma unroll
-        for (int w = 1; w < MT / kWave; ++w) {
+        for (int w = 1; w < MG; ++w) {
             s.x += obuf[w][t].x; s.y += obuf[w][t].y; s.z += obuf[w][t].z; s.w += obuf[w][t].w;
             L += lbuf[w];
         }
         const float inv = 1.0f / L;
+        const int dim = slice * MSLICE + 4 * t;
         const float4 gt = *reinterpret_cast<const float4*>(
-            q_gate + (size_t)i * 2 * nh * kHd + (size_t)h * 2 * kHd + kHd + 4 * t);
+            q_gate + (size_t)i * 2 * nh * kHd + (size_t)h * 2 * kHd + kHd + dim);
         float4 r;
         r.x = s.x * inv * (1.0f / (1.0f + expf(-gt.x)));
         r.y = s.y * inv * (1.0f / (1.0f + expf(-gt.y)));
         r.z = s.z * inv * (1.0f / (1.0f + expf(-gt.z)));
         r.w = s.w * inv * (1.0f / (1.0f + expf(-gt.w)));
-        *reinterpret_cast<float4*>(out + (size_t)i * nh * kHd + (size_t)h * kHd + 4 * t) = r;
+        *reinterpret_cast<float4*>(out + (size_t)i * nh * kHd + (size_t)h * kHd + dim) = r;
     }
 }
 
@@ -310,7 +317,7 @@ hipError_t launch_attn_decode(q35m_ctx* c, int layer, const SeqBatch& sb, const 
     if (e != hipSuccess) return e;
     {
         ProfScope ps_(c, K_ATTN_DECODE_MERGE);
-        hipLaunchKernelGGL(attn_decode_merge, dim3(d.nh, sb.n), dim3(MT), 0, c->stream, part_o,
+        hipLaunchKernelGGL(attn_decode_merge, dim3(d.nh * (kHd / MSLICE), sb.n), dim3(MT), 0, c->stream, part_o,
                            part_ml, q_gate, out, d.nkv, nchunks, chunk, sb);
     }
     return hipGetLastError();

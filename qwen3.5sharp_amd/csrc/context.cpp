@@ -285,7 +285,8 @@ int q35m_create(const q35m_config* cfg, int n_seqs, int kv_capacity, q35m_ctx** 
         if (c->is_recurrent[l]) {
             q35::DeltaNetLayer& L = c->lin[l];
             r = alloc_zero(c, (void**)&L.state, state_bytes);
-            if (!r) r = alloc_zero(c, (void**)&L.conv, conv_bytes);
+            if (!r) r = alloc_zero(c, (void**)&L.conv, 2 * conv_bytes);
+            L.conv_cur.assign(n_seqs, 0);
             if (!r) r = alloc_zero(c, (void**)&L.conv_w, (size_t)q35::kConvK * d.conv_dim * 4);
             if (!r) r = alloc_zero(c, (void**)&L.ssm_a, (size_t)d.nv * 4);
             if (!r) r = alloc_zero(c, (void**)&L.dt_bias, (size_t)d.nv * 4);
@@ -342,7 +343,9 @@ int q35m_reset(q35m_ctx* ctx, int seq) {
     for (int l = 0; l < ctx->cfg.num_layers; l++) {
         if (!ctx->is_recurrent[l]) continue;
         HIP_TRY(hipMemsetAsync((char*)ctx->lin[l].state + sb * seq, 0, sb, ctx->stream), "reset");
-        HIP_TRY(hipMemsetAsync((char*)ctx->lin[l].conv + cb * seq, 0, cb, ctx->stream), "reset");
+        HIP_TRY(hipMemsetAsync(ctx->lin[l].conv_window(seq, ctx->n_seqs, d.conv_dim), 0, cb,
+                               ctx->stream),
+                "reset");
     }
     ctx->kv_len[seq] = 0;
     return Q35M_OK;
@@ -426,7 +429,11 @@ int q35m_deltanet_decode(q35m_ctx* ctx, int layer, int n, const int* seqs, const
     q35::SeqBatch sb;
     r = build_seq_batch(ctx, n, seqs, false, &sb);
     if (r) return r;
+    q35::DeltaNetLayer& L = ctx->lin[layer];
+    for (int i = 0; i < n; i++) sb.pos[i] = L.conv_cur[seqs[i]];
     HIP_TRY(q35::launch_deltanet_decode(ctx, layer, sb, qkv, z, b, a, out), "deltanet_decode");
+    // The step wrote the shifted windows into the other buffer.
+    for (int i = 0; i < n; i++) L.conv_cur[seqs[i]] ^= 1;
     return Q35M_OK;
 }
 
@@ -492,7 +499,7 @@ static int state_locate(q35m_ctx* ctx, int layer, int seq, int kind, char** base
             *base = (char*)ctx->lin[layer].state + *bytes * seq;
         } else {
             *bytes = (size_t)d.conv_dim * q35::kConvState * sizeof(float);
-            *base = (char*)ctx->lin[layer].conv + *bytes * seq;
+            *base = (char*)ctx->lin[layer].conv_window(seq, ctx->n_seqs, d.conv_dim);
         }
         return Q35M_OK;
     }

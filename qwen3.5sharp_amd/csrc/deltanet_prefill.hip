@@ -79,9 +79,6 @@ constexpr int LDA = 68;       // padded LDS row stride of [64][64] tiles
 //            (an MFMA D tile; also the A operand of a product reducing over
 //             tokens, e.g. K^T D).
 // Both are [4 tb][8 kb][64 lanes][4] inside the block.
-__device__ __forceinline__ int a_idx(int t, int d) {
-    return (((t >> 4) * 8 + (d >> 4)) * 64 + ((d >> 2) & 3) * 16 + (t & 15)) * 4 + (d & 3);
-}
 __device__ __forceinline__ const float4* blk4(const float* base, int tb, int kb, int lane) {
     return reinterpret_cast<const float4*>(base + (size_t)((tb * 8 + kb) * 64 + lane) * 4);
 }
@@ -567,7 +564,7 @@ hipError_t launch_deltanet_prefill(q35m_ctx* c, int layer, int seq, int T, const
     const int nch = (T + CH - 1) / CH;
     PrefillWork w = carve(c->work, d, T, nch);
     float* state = L.state + (size_t)seq * d.nv * kDk * kDk;
-    float* cs = L.conv + (size_t)seq * d.conv_dim * kConvState;
+    float* cs = L.conv_window(seq, c->n_seqs, d.conv_dim);
     hipError_t e;
     {
         ProfScope ps_(c, K_DN_PREFILL_PREP);

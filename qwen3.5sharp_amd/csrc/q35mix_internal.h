@@ -26,7 +26,8 @@ constexpr int kMaxVPerK = 4;    // DeltaNet v-heads per k-head (one decode workg
 struct SeqBatch {
     int n;
     int seq[kMaxBatch];
-    int pos[kMaxBatch];  // attention: row the new token is written to
+    int pos[kMaxBatch];  // attention: row the new token is written to;
+                         // DeltaNet decode: conv-window buffer holding the window
 };
 
 struct DeltaNetLayer {
@@ -35,7 +36,11 @@ struct DeltaNetLayer {
     float* dt_bias = nullptr;  // [H_v]
     float* ssm_norm = nullptr; // [dv]
     float* state = nullptr;    // [n_seqs][H_v][dk][dv]
-    float* conv = nullptr;     // [n_seqs][conv_dim][3]
+    float* conv = nullptr;     // [2][n_seqs][conv_dim][3], double-buffered windows
+    std::vector<unsigned char> conv_cur;  // [n_seqs] buffer holding the current window
+    float* conv_window(int seq, int n_seqs, int conv_dim) const {
+        return conv + ((size_t)conv_cur[seq] * n_seqs + seq) * conv_dim * kConvState;
+    }
     bool has_weights = false;
 };
 

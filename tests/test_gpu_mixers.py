@@ -319,3 +319,44 @@ def test_attn_decode_long_batch(lens):
             e = rel(got[s], o_ref)
             say(f"attn_decode long batch seq {s} len {L}: out rel err {e:.2e}")
             assert e <= TOL
+
+
+@pytest.mark.parametrize("n", [16, 32])
+def test_deltanet_decode_wide_batch(n):
+    """16 and 32 sequences in one launch (512 and 1024 workgroups), three
+    chained tokens, so the double-buffered conv windows flip three times."""
+    with q35mix.Context(q35mix.qwen35_config(num_layers=1, is_recurrent=[1]), n_seqs=n,
+                        kv_capacity=4) as c:
+        c.set_deltanet_weights(0, synth.deltanet_weights(NK, NV, 128, salt=0))
+        _dn_decode_case(c, 0, list(range(n))[::-1], salt0=300 + n, steps=3)
+
+
+def test_deltanet_prefill_then_decode(ctx):
+    """Prefill of 5 tokens, two decode steps, a second prefill (which ignores
+    the stored window but rewrites it) and one more decode step, on one
+    sequence: the window each step reads is the one the previous step left."""
+    layer, s = 0, 2
+    w = synth.deltanet_weights(NK, NV, 128, salt=layer)
+    st = synth.deltanet_state(NK, NV, 128, salt=77)
+    ctx.state_write(layer, s, q35mix.STATE_RECURRENT, st["state"])
+    ctx.state_write(layer, s, q35mix.STATE_CONV, st["conv_state"])
+    cs_ref, st_ref = st["conv_state"], st["state"]
+    for step, T in enumerate([5, 1, 1, 3, 1]):
+        x = synth.deltanet_inputs(T, NK, NV, 128, salt=900 + step)
+        qkv, z = ctx.array((T, ctx.conv_dim), x["qkv"]), ctx.array((T, ctx.value_dim), x["z"])
+        b, a = ctx.array((T, NV), x["b"]), ctx.array((T, NV), x["a"])
+        out = ctx.array((T, ctx.value_dim))
+        if step in (0, 3):
+            ctx.deltanet_prefill(layer, s, T, qkv, z, b, a, out)
+            o_ref, cs_ref, st_ref, _ = oracle.deltanet_prefill(DIMS, T, x["qkv"], x["z"], x["b"],
+                                                               x["a"], w, st_ref, cs_ref)
+        else:
+            ctx.deltanet_decode(layer, [s], qkv, z, b, a, out)
+            o_ref, cs_ref, st_ref, _ = oracle.deltanet_decode(DIMS, x["qkv"][0], x["z"][0],
+                                                              x["b"][0], x["a"][0], w, cs_ref,
+                                                              st_ref)
+        e = rel(out.download().reshape(np.shape(o_ref)), o_ref)
+        say(f"deltanet prefill/decode chain step {step} (T={T}): out rel err {e:.2e}")
+        assert e <= TOL
+        np.testing.assert_array_equal(ctx.state_read(layer, s, q35mix.STATE_CONV), cs_ref)
+    assert rel(ctx.state_read(layer, s, q35mix.STATE_RECURRENT), st_ref) <= TOL
