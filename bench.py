@@ -48,11 +48,22 @@ def attn_decode_bytes(kv_len: int) -> int:
 
 
 DN_PREFILL_FLOP = 11_811_160_064           # T=2048, chunked WY form (32 heads x 32 chunks)
-# Per-kernel algorithmic FLOP of one T=2048 DeltaNet prefill (C = 64, 32 chunks, 32 v-heads):
-#  dn_chunk_scan: W S, Q S, K^T D (3 x 2 C dk dv) + (M o QK^T) D (2 C^2 dv) per chunk-head
-#  dn_chunk_prep: K K^T, Q K^T (2 x 2 C^2 dk, once per k-head) + W, U (2 x 2 C^2 dk per v-head)
-DN_SCAN_FLOP = 32 * 32 * (3 * 2 * 64 * DK * DK + 2 * 64 * 64 * DK)
-DN_CPREP_FLOP = 32 * 16 * 2 * 2 * 64 * 64 * DK + 32 * 32 * 2 * 2 * 64 * 64 * DK
+# Per-kernel algorithmic work of one T=2048 DeltaNet prefill (C = 64, 32 chunks,
+# 16 k-heads, 32 v-heads), as (bound, amount, description):
+DN_PREFILL_KERNELS = {
+    "dn_chunk_scan": ("mfma", 32 * 32 * 2 * (2 * 64 * DK * DK),
+                      "W S and K^T D, 2 x 2*64*128*128 FLOP per (v-head, chunk), 32 x 32"),
+    "dn_chunk_out": ("mfma", 32 * 32 * (2 * 64 * DK * DK + 10 * 2 * 16 * 16 * DK),
+                     "Q S (2*64*128*128) + the 10 causal 16x16 blocks of (M o QK^T) D "
+                     "(10 x 2*16*16*128) FLOP per (v-head, chunk), 32 x 32"),
+    "dn_chunk_prep": ("mfma", 32 * 16 * 2 * 2 * 64 * 64 * DK + 32 * 32 * 2 * 2 * 64 * 64 * DK,
+                      "K K^T, Q K^T (2 x 2*64*64*128 per k-head chunk) + W, U (2 x 2*64*64*128 "
+                      "per v-head chunk)"),
+    "deltanet_prefill_prep": ("hbm", 4 * (2048 * CONV_DIM + 2 * 2048 * NV) +
+                              4 * (3 * 2048 * NK * DK + 2048 * NV * DK + 2 * 2048 * NV),
+                              "qkv, b, a read once; q, k (two layouts), v chunk blocks and "
+                              "beta, g written once"),
+}
 ATTN_PREFILL_FLOP = 4 * HD * NH * 2048 * 2049 // 2
 PROFILES = os.path.join(ROOT, "profiles")
 
@@ -336,16 +347,22 @@ def main():
         tok_s = 2048 / (ms / 1e3)
         kname, kms = dominant(kt)
         log(f"[bench] DeltaNet prefill: {ms:.3f} ms/step, {tok_s:.0f} tok/s; kernels {kt}")
-        kflop = {"dn_chunk_scan": DN_SCAN_FLOP, "dn_chunk_prep": DN_CPREP_FLOP}.get(kname)
-        if kflop is None:
-            raise RuntimeError(f"no algorithmic FLOP count for dominant kernel {kname}")
-        roof = {"bound": "mfma", "achieved": kflop / (kms / 1e3) / 1e12,
-                "peak": FP32_PEAK / 1e12, "unit": "TFLOP/s",
-                "frac": kflop / (kms / 1e3) / FP32_PEAK, "traffic": measured_traffic(kname),
-                "kernel": kname, "kernel_ms": kms,
-                "algorithmic": f"{kflop} FLOP per launch (fp32 MFMA products of one 2048-token "
-                               "layer: 32 v-heads x 32 chunks of 64)",
-                "kernels_ms": {k: v[0] for k, v in kt.items()}}
+        if kname not in DN_PREFILL_KERNELS:
+            raise RuntimeError(f"no algorithmic work count for dominant kernel {kname}")
+        bound, work, what = DN_PREFILL_KERNELS[kname]
+        if bound == "mfma":
+            achieved, peak, unit = work / (kms / 1e3) / 1e12, FP32_PEAK / 1e12, "TFLOP/s"
+            algo = f"{work} FLOP per launch: {what}"
+        else:
+            achieved, peak, unit = work / (kms / 1e3) / 1e9, HBM_PEAK / 1e9, "GB/s"
+            algo = f"{work} bytes per launch: {what}"
+        roof = {"bound": bound, "achieved": achieved, "peak": peak, "unit": unit,
+                "frac": achieved / peak, "traffic": measured_traffic(kname),
+                "kernel": kname, "kernel_ms": kms, "algorithmic": algo,
+                "kernels_ms": {k: v[0] for k, v in kt.items()},
+                "kernels_frac": {k: (DN_PREFILL_KERNELS[k][1] / (v[0] / 1e3) /
+                                     (FP32_PEAK if DN_PREFILL_KERNELS[k][0] == "mfma" else HBM_PEAK))
+                                 for k, v in kt.items() if k in DN_PREFILL_KERNELS}}
         cpu = None
         if not args.no_cpu:
             log("[bench] CPU restatement, one 2048-token DeltaNet prefill layer ...")

@@ -35,12 +35,15 @@
 //     inverted in registers, off-diagonal blocks applied on MFMA), then
 //     W and U on MFMA.  Emits W, U, M o QK^T, gamma, e^{G_last - G}.
 //  4. dn_chunk_scan (one workgroup per v-head and 16-column tile of the
-//     state): walks the chunks in order with the state tile in MFMA
-//     accumulators: D = U - W S, O = gamma Q S + (M o QK^T) D,
+//     state): the only sequential part.  Walks the chunks in order with the
+//     state tile in MFMA accumulators, records the entry state S and
+//     D = U - W S of every chunk, and applies
 //     S = gamma_last S + K^T (e^{G_last-G} D).  Column tiles are independent
 //     (the rule is separable over dv), so 8 workgroups per head run in
-//     parallel; the 8 tiles of a head share an XCD so W, Q, K stay in its L2.
-//  5. deltanet_gated_norm: gated RMSNorm per (token, v-head) row.
+//     parallel; the 8 tiles of a head share an XCD so W and K stay in its L2.
+//  5. dn_chunk_out (one workgroup per v-head and chunk, all in parallel):
+//     O = gamma Q S + (M o QK^T) D from the recorded S and D, with the gated
+//     RMSNorm fused into the epilogue.
 //
 // MFMA: v_mfma_f32_16x16x4f32.  Lane l = 16g + c holds A[c][g] and B[g][c];
 // D register r holds D[4g + r][c].  A 16-deep product is 4 instructions; in
@@ -95,12 +98,13 @@ struct PrefillWork {
     float* gl;     // [T][nv]   g (log decay)
     float* gam;    // [nv][nch][64]   e^{G_i}
     float* gdec;   // [nv][nch][64]   e^{G_last - G_i}
-    float* core;   // [T][nv][dv] pre-norm recurrence output
+    float* sh;     // [nv][nch][8 rb][8 cb][64][4] D layout: state on entry to each chunk
+    float* dh;     // [nv][nch] chunk blocks, D layout: D = U - W S of each chunk
 };
 
 size_t work_floats(const Dims& d, int T, int nch) {
-    return (size_t)nch * CB * (3 * d.nk + 3 * d.nv) + (size_t)d.nv * nch * (CH * CH + 2 * CH) +
-           (size_t)T * (2 * d.nv + d.value_dim);
+    return (size_t)nch * CB * (3 * d.nk + 4 * d.nv) + (size_t)d.nv * nch * (CH * CH + 2 * CH) +
+           (size_t)T * 2 * d.nv + (size_t)d.nv * nch * kDk * kDk;
 }
 
 PrefillWork carve(float* w, const Dims& d, int T, int nch) {
@@ -117,7 +121,8 @@ PrefillWork carve(float* w, const Dims& d, int T, int nch) {
     p.gl = p.beta + (size_t)T * d.nv;
     p.gam = p.gl + (size_t)T * d.nv;
     p.gdec = p.gam + (size_t)d.nv * nch * CH;
-    p.core = p.gdec + (size_t)d.nv * nch * CH;
+    p.sh = p.gdec + (size_t)d.nv * nch * CH;
+    p.dh = p.sh + (size_t)d.nv * nch * kDk * kDk;
     return p;
 }
 
@@ -413,12 +418,10 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep(PrefillWork w, int T, in
 // per lane; none depends on the state, so the next chunk's set is loaded while
 // the current one computes.
 struct ScanOps {
-    float4 wa[4][2], qa[4][2];   // W, Q^ (A operands of W S and Q S)
-    float4 kt[4][2];             // K^ (A operand of K^T D)
-    float4 aa[4];                // M o QK^T row block `wave`, column blocks 0..3
+    float4 wa[4][2];             // W (A operand of W S), this wave's 32 state rows
+    float4 kt[4][2];             // K^ (A operand of K^T D), same rows
     float4 ut[4];                // U, all token blocks, this column tile
     float4 gdv[4];               // e^{G_last - G}
-    float4 gmo;                  // gamma for token block `wave`
     float glast;                 // gamma_last
 };
 
@@ -427,34 +430,32 @@ __device__ __forceinline__ void load_scan_ops(const PrefillWork& w, ScanOps& o, 
                                               int lane) {
     const size_t cidx = (size_t)vh * nch + n, kidx = (size_t)kh * nch + n;
     const float* wA = w.wa + cidx * CB;
-    const float* qA = w.qa + kidx * CB;
     const float* kD = w.kt + kidx * CB;
     const float* uD = w.ud + cidx * CB;
-    const float4* aq = reinterpret_cast<const float4*>(w.aqk + cidx * CH * CH);
-    const float* gm = w.gam + cidx * CH;
     const float* gd = w.gdec + cidx * CH;
 #pragma unroll
     for (int tb = 0; tb < 4; ++tb) {
 #pragma unroll
         for (int b = 0; b < 2; ++b) {
             o.wa[tb][b] = *blk4(wA, tb, 2 * wave + b, lane);
-            o.qa[tb][b] = *blk4(qA, tb, 2 * wave + b, lane);
             o.kt[tb][b] = *blk4(kD, tb, 2 * wave + b, lane);
         }
-        o.aa[tb] = aq[(wave * 4 + tb) * 64 + lane];
         o.ut[tb] = *blk4(uD, tb, tl, lane);
         o.gdv[tb] = *reinterpret_cast<const float4*>(gd + 16 * tb + 4 * g);
     }
-    o.gmo = *reinterpret_cast<const float4*>(gm + 16 * wave + 4 * g);
-    o.glast = gm[CH - 1];
+    o.glast = w.gam[cidx * CH + CH - 1];
 }
 
 __device__ __forceinline__ f32x4 v4(float4 a) { return f32x4{a.x, a.y, a.z, a.w}; }
 
-// One workgroup per (v-head, 16-column tile); wave w owns state rows
-// 32w..32w+31 of the tile (two D-layout 16x16 tiles, kept across chunks).
+// The sequential part: one workgroup per (v-head, 16-column tile); wave w owns
+// state rows 32w..32w+31 of the tile (two D-layout 16x16 tiles, kept in MFMA
+// accumulators across chunks).  Per chunk it records the entry state S and
+// D = U - W S for dn_chunk_out, then S = gamma_last S + K^T (e^{G_last-G} D).
+// Column tiles are independent (the rule is separable over dv), so 8
+// workgroups per head run in parallel, on one XCD so W and K stay in its L2.
 __global__ __launch_bounds__(256) void dn_chunk_scan(PrefillWork w, float* __restrict__ state,
-                                                     int T, int nk, int nv, int nch) {
+                                                     int nk, int nv, int nch) {
     const int L = xcd_remap(blockIdx.x, gridDim.x);
     const int vh = L / 8, tl = L % 8;
     const int kh = vh / (nv / nk);
@@ -469,61 +470,64 @@ __global__ __launch_bounds__(256) void dn_chunk_scan(PrefillWork w, float* __res
 #pragma unroll
         for (int r = 0; r < 4; ++r) Sb[b][r] = S[(size_t)(32 * wave + 16 * b + 4 * g + r) * kDk + col];
 
-    // Partials of W S and Q S per wave, double-buffered by chunk parity so one
+    // Partials of W S per wave, double-buffered by chunk parity so one
     // barrier per chunk suffices.
-    __shared__ f32x4 red[2][4][2][4][64];
+    __shared__ f32x4 red[2][4][4][64];
 
-    ScanOps cur, nxt;
-    load_scan_ops(w, cur, 0, vh, kh, tl, nch, wave, g, lane);
-    for (int n = 0; n < nch; ++n) {
-        const int t0 = n * CH;
-        if (n + 1 < nch) load_scan_ops(w, nxt, n + 1, vh, kh, tl, nch, wave, g, lane);
+    // One chunk: record S and D, then the state update.
+    auto chunk = [&](const ScanOps& cur, int n) {
         const int par = n & 1;
-        // Partial W S and Q S over this wave's 32 state rows, all 4 token blocks.
+        const size_t cidx = (size_t)vh * nch + n;
+        float* sh = w.sh + cidx * kDk * kDk;
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+            *reinterpret_cast<f32x4*>(sh + (size_t)(((2 * wave + b) * 8 + tl) * 64 + lane) * 4) = Sb[b];
+        // Partial W S over this wave's 32 state rows, all 4 token blocks.
 #pragma unroll
         for (int tb = 0; tb < 4; ++tb) {
-            f32x4 pws = {0.f, 0.f, 0.f, 0.f}, pqs = {0.f, 0.f, 0.f, 0.f};
+            f32x4 pws = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int b = 0; b < 2; ++b) {
-                pws = mfma16x4(cur.wa[tb][b], Sb[b], pws);
-                pqs = mfma16x4(cur.qa[tb][b], Sb[b], pqs);
-            }
-            red[par][wave][0][tb][lane] = pws;
-            red[par][wave][1][tb][lane] = pqs;
+            for (int b = 0; b < 2; ++b) pws = mfma16x4(cur.wa[tb][b], Sb[b], pws);
+            red[par][wave][tb][lane] = pws;
         }
         lds_barrier();
-        // Every wave forms D = U - W S for all 4 token blocks (it needs them all
-        // for its rows of the state update), and Q S for its token block `wave`.
+        // Every wave forms D = U - W S for all 4 token blocks (its rows of the
+        // update need them all) and records token block `wave`.
         f32x4 D[4];
 #pragma unroll
         for (int tb = 0; tb < 4; ++tb) {
-            f32x4 ws = red[par][0][0][tb][lane];
+            f32x4 ws = red[par][0][tb][lane];
 #pragma unroll
-            for (int v = 1; v < 4; ++v) ws += red[par][v][0][tb][lane];
+            for (int v = 1; v < 4; ++v) ws += red[par][v][tb][lane];
             D[tb] = v4(cur.ut[tb]) - ws;
+            if (tb == wave)
+                *reinterpret_cast<f32x4*>(w.dh + cidx * CB + (size_t)((tb * 8 + tl) * 64 + lane) * 4) = D[tb];
         }
-        f32x4 qs = red[par][0][1][wave][lane];
-#pragma unroll
-        for (int v = 1; v < 4; ++v) qs += red[par][v][1][wave][lane];
         // S = gamma_last S + K^T (e^{G_last - G} D).
+#pragma unroll
+        for (int tb = 0; tb < 4; ++tb) D[tb] *= v4(cur.gdv[tb]);
 #pragma unroll
         for (int b = 0; b < 2; ++b) {
             f32x4 acc = Sb[b] * cur.glast;
 #pragma unroll
-            for (int tb = 0; tb < 4; ++tb) acc = mfma16x4(cur.kt[tb][b], D[tb] * v4(cur.gdv[tb]), acc);
+            for (int tb = 0; tb < 4; ++tb) acc = mfma16x4(cur.kt[tb][b], D[tb], acc);
             Sb[b] = acc;
         }
-        // O rows of token block `wave` = gamma Q S + (M o QK^T) D (causal: blocks <= wave).
-        f32x4 o = v4(cur.gmo) * qs;
-#pragma unroll
-        for (int tb = 0; tb < 4; ++tb)
-            if (tb <= wave) o = mfma16x4(cur.aa[tb], D[tb], o);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int t = t0 + 16 * wave + 4 * g + r;
-            if (t < T) w.core[((size_t)t * nv + vh) * kDk + col] = o[r];
-        }
-        cur = nxt;
+    };
+    // Operands run two chunks ahead (they come from other XCDs' writes, so
+    // mostly from HBM): three register sets in rotation, no copies.
+    ScanOps o0, o1, o2;
+    load_scan_ops(w, o0, 0, vh, kh, tl, nch, wave, g, lane);
+    if (nch > 1) load_scan_ops(w, o1, 1, vh, kh, tl, nch, wave, g, lane);
+    for (int n = 0; n < nch; n += 3) {
+        if (n + 2 < nch) load_scan_ops(w, o2, n + 2, vh, kh, tl, nch, wave, g, lane);
+        chunk(o0, n);
+        if (n + 1 >= nch) break;
+        if (n + 3 < nch) load_scan_ops(w, o0, n + 3, vh, kh, tl, nch, wave, g, lane);
+        chunk(o1, n + 1);
+        if (n + 2 >= nch) break;
+        if (n + 4 < nch) load_scan_ops(w, o1, n + 4, vh, kh, tl, nch, wave, g, lane);
+        chunk(o2, n + 2);
     }
 #pragma unroll
     for (int b = 0; b < 2; ++b)
@@ -531,24 +535,133 @@ __global__ __launch_bounds__(256) void dn_chunk_scan(PrefillWork w, float* __res
         for (int r = 0; r < 4; ++r) S[(size_t)(32 * wave + 16 * b + 4 * g + r) * kDk + col] = Sb[b][r];
 }
 
-// Qwen35Ops.GatedRmsNorm (Qwen35Ops.cs:74-111) over rows of dv = 128: one
-// wave per row, two values per lane; four rows per workgroup.
-__global__ __launch_bounds__(256) void deltanet_gated_norm(const float* __restrict__ core,
-                                                           const float* __restrict__ z,
-                                                           const float* __restrict__ wnorm,
-                                                           float* __restrict__ out, float eps,
-                                                           size_t rows) {
-    const size_t row = (size_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    const int lane = threadIdx.x & 63;
-    if (row >= rows) return;
-    const float2 x = reinterpret_cast<const float2*>(core + row * kDk)[lane];
-    const float2 zz = reinterpret_cast<const float2*>(z + row * kDk)[lane];
-    const float2 ww = reinterpret_cast<const float2*>(wnorm)[lane];
-    const float rs = 1.0f / sqrtf(wave_sum(x.x * x.x + x.y * x.y) / (float)kDk + eps);
-    float2 r;
-    r.x = x.x * rs * ww.x * silu(zz.x);
-    r.y = x.y * rs * ww.y * silu(zz.y);
-    reinterpret_cast<float2*>(out + row * kDk)[lane] = r;
+// Chunk outputs, in parallel over (v-head, chunk), with the gated RMSNorm
+// (Qwen35Ops.GatedRmsNorm, Qwen35Ops.cs:74-111) fused:
+//   O = diag(gamma) Q S + (M o Q K^T) D,  out = O * rms(O)^-1 * w * SiLU(z).
+// Wave w computes column tiles 2w, 2w+1 of all 4 token blocks: its S columns
+// (16 KiB) and D columns stay in registers.  The A operands shared by the 4
+// waves -- gamma-scaled Q (32 KiB) and the 10 causal blocks of M o QK^T --
+// are loaded once per workgroup into LDS.  The RMS spans the 4 waves' columns
+// of a row: one LDS exchange.  The epilogue goes row-major through LDS, so z
+// (prefetched at the start) and out move as coalesced float4 rows.
+__global__ __launch_bounds__(256) void dn_chunk_out(PrefillWork w, const float* __restrict__ z,
+                                                    const float* __restrict__ wnorm,
+                                                    float* __restrict__ out, int T, int nk,
+                                                    int nv, int nch, float eps) {
+    const int L = xcd_remap(blockIdx.x, gridDim.x);
+    const int vh = L / nch, n = L % nch;
+    const int kh = vh / (nv / nk);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int g = lane >> 4, c16 = lane & 15;
+    const size_t cidx = (size_t)vh * nch + n, kidx = (size_t)kh * nch + n;
+    const float* sh = w.sh + cidx * kDk * kDk;
+    const float* dD = w.dh + cidx * CB;
+    const float4* qA = reinterpret_cast<const float4*>(w.qa + kidx * CB);
+    const float4* aq = reinterpret_cast<const float4*>(w.aqk + cidx * CH * CH);
+    const float* gm = w.gam + cidx * CH;
+
+    __shared__ float4 q_s[4 * 8][64];     // [tb][kb] A-layout blocks of gamma Q
+    __shared__ float4 a_s[10][64];        // causal blocks (tb, j <= tb) of M o QK^T
+    __shared__ float ssq[4][CH];
+    __shared__ float o_s[CH][kDk + 4];
+
+    f32x4 Sc[8][2];           // S[16 kb .. +15][16 (2w + cc) .. +15], D layout
+    f32x4 Dc[4][2];           // D[16 tb .. +15][same columns]
+#pragma unroll
+    for (int kb = 0; kb < 8; ++kb)
+#pragma unroll
+        for (int cc = 0; cc < 2; ++cc) Sc[kb][cc] = v4(*blk4(sh, kb, 2 * wave + cc, lane));
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb)
+#pragma unroll
+        for (int cc = 0; cc < 2; ++cc) Dc[tb][cc] = v4(*blk4(dD, tb, 2 * wave + cc, lane));
+    {
+        // Q: 2048 float4, 8 per thread; block = o4 / 64 = tb * 8 + kb, and the
+        // lane's row within the block is its c16 (A layout).
+        float4 qv[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) qv[i] = qA[tid + 256 * i];
+        float4 av[3];
+#pragma unroll
+        for (int i = 0; i < 3; ++i) {
+            const int o4 = min(tid + 256 * i, 10 * 64 - 1);
+            const int blk = o4 >> 6, tb = blk < 1 ? 0 : blk < 3 ? 1 : blk < 6 ? 2 : 3;
+            const int j = blk - tb * (tb + 1) / 2;
+            av[i] = aq[(tb * 4 + j) * 64 + (o4 & 63)];
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int o4 = tid + 256 * i, tb = o4 >> 9;
+            const float gr = gm[16 * tb + (o4 & 15)];
+            q_s[o4 >> 6][o4 & 63] = make_float4(qv[i].x * gr, qv[i].y * gr, qv[i].z * gr, qv[i].w * gr);
+        }
+#pragma unroll
+        for (int i = 0; i < 3; ++i) {
+            const int o4 = tid + 256 * i;
+            if (o4 < 10 * 64) a_s[o4 >> 6][o4 & 63] = av[i];
+        }
+    }
+    // z rows of this (chunk, v-head): float4 o4 = tid + 256 i is row o4 / 32,
+    // columns 4 (o4 % 32) ..; rows past T read row T - 1 and are not stored.
+    const int t0 = n * CH;
+    float4 zr[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int o4 = tid + 256 * i, t = min(t0 + (o4 >> 5), T - 1);
+        zr[i] = reinterpret_cast<const float4*>(z + ((size_t)t * nv + vh) * kDk)[o4 & 31];
+    }
+    __syncthreads();
+
+    f32x4 O[4][2];
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb) {
+        f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kb = 0; kb < 8; ++kb) {
+            const float4 q = q_s[tb * 8 + kb][lane];
+            acc0 = mfma16x4(q, Sc[kb][0], acc0);
+            acc1 = mfma16x4(q, Sc[kb][1], acc1);
+        }
+#pragma unroll
+        for (int j = 0; j <= tb; ++j) {
+            const float4 a = a_s[tb * (tb + 1) / 2 + j][lane];
+            acc0 = mfma16x4(a, Dc[j][0], acc0);
+            acc1 = mfma16x4(a, Dc[j][1], acc1);
+        }
+        O[tb][0] = acc0;
+        O[tb][1] = acc1;
+        // Sum of squares of rows 16 tb + 4g + r over this wave's 32 columns.
+        f32x4 sq = acc0 * acc0 + acc1 * acc1;
+#pragma unroll
+        for (int m = 1; m < 16; m <<= 1)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) sq[r] += __shfl_xor(sq[r], m, kWave);
+        if (c16 == 0)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) ssq[wave][16 * tb + 4 * g + r] = sq[r];
+    }
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb)
+#pragma unroll
+        for (int cc = 0; cc < 2; ++cc)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) o_s[16 * tb + 4 * g + r][16 * (2 * wave + cc) + c16] = O[tb][cc][r];
+    lds_barrier();
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int o4 = tid + 256 * i, row = o4 >> 5, c4 = o4 & 31, t = t0 + row;
+        if (t >= T) continue;
+        const float rs = 1.0f / sqrtf((ssq[0][row] + ssq[1][row] + ssq[2][row] + ssq[3][row]) /
+                                          (float)kDk + eps);
+        const float4 o = *reinterpret_cast<const float4*>(&o_s[row][4 * c4]);
+        const float4 wn = reinterpret_cast<const float4*>(wnorm)[c4];
+        float4 r;
+        r.x = o.x * rs * wn.x * silu(zr[i].x);
+        r.y = o.y * rs * wn.y * silu(zr[i].y);
+        r.z = o.z * rs * wn.z * silu(zr[i].z);
+        r.w = o.w * rs * wn.w * silu(zr[i].w);
+        reinterpret_cast<float4*>(out + ((size_t)t * nv + vh) * kDk)[c4] = r;
+    }
 }
 
 }  // namespace
@@ -587,15 +700,14 @@ hipError_t launch_deltanet_prefill(q35m_ctx* c, int layer, int seq, int T, const
     if ((e = hipGetLastError()) != hipSuccess) return e;
     {
         ProfScope ps_(c, K_DN_CHUNK_SCAN);
-        hipLaunchKernelGGL(dn_chunk_scan, dim3(d.nv * 8), dim3(256), 0, c->stream, w, state, T,
-                           d.nk, d.nv, nch);
+        hipLaunchKernelGGL(dn_chunk_scan, dim3(d.nv * 8), dim3(256), 0, c->stream, w, state, d.nk,
+                           d.nv, nch);
     }
     if ((e = hipGetLastError()) != hipSuccess) return e;
     {
-        ProfScope ps_(c, K_DN_GATED_NORM);
-        const size_t rows = (size_t)T * d.nv;
-        hipLaunchKernelGGL(deltanet_gated_norm, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0,
-                           c->stream, w.core, z, L.ssm_norm, out, d.eps, rows);
+        ProfScope ps_(c, K_DN_CHUNK_OUT);
+        hipLaunchKernelGGL(dn_chunk_out, dim3(d.nv * nch), dim3(256), 0, c->stream, w, z,
+                           L.ssm_norm, out, T, d.nk, d.nv, nch, d.eps);
     }
     return hipGetLastError();
 }

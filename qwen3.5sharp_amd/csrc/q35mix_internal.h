@@ -61,7 +61,7 @@ enum KernelId {
     K_DN_CONV_WRITEBACK,
     K_DN_CHUNK_PREP,
     K_DN_CHUNK_SCAN,
-    K_DN_GATED_NORM,
+    K_DN_CHUNK_OUT,
     K_ATTN_DECODE_PARTIAL,
     K_ATTN_DECODE_MERGE,
     K_ATTN_PREFILL_PREP,
