@@ -420,8 +420,8 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep(PrefillWork w, int T, in
 struct ScanOps {
     float4 wa[4][2];             // W (A operand of W S), this wave's 32 state rows
     float4 kt[4][2];             // K^ (A operand of K^T D), same rows
-    float4 ut[4];                // U, all token blocks, this column tile
-    float4 gdv[4];               // e^{G_last - G}
+    float4 ut;                   // U, token block `wave`, this column tile
+    float4 gdv;                  // e^{G_last - G}, token block `wave`
     float glast;                 // gamma_last
 };
 
@@ -440,9 +440,9 @@ __device__ __forceinline__ void load_scan_ops(const PrefillWork& w, ScanOps& o, 
             o.wa[tb][b] = *blk4(wA, tb, 2 * wave + b, lane);
             o.kt[tb][b] = *blk4(kD, tb, 2 * wave + b, lane);
         }
-        o.ut[tb] = *blk4(uD, tb, tl, lane);
-        o.gdv[tb] = *reinterpret_cast<const float4*>(gd + 16 * tb + 4 * g);
     }
+    o.ut = *blk4(uD, wave, tl, lane);
+    o.gdv = *reinterpret_cast<const float4*>(gd + 16 * wave + 4 * g);
     o.glast = w.gam[cidx * CH + CH - 1];
 }
 
@@ -470,18 +470,23 @@ __global__ __launch_bounds__(256) void dn_chunk_scan(PrefillWork w, float* __res
 #pragma unroll
         for (int r = 0; r < 4; ++r) Sb[b][r] = S[(size_t)(32 * wave + 16 * b + 4 * g + r) * kDk + col];
 
-    // Partials of W S per wave, double-buffered by chunk parity so one
-    // barrier per chunk suffices.
+    // Partials of W S per wave and the decayed D blocks, double-buffered by
+    // chunk parity.
     __shared__ f32x4 red[2][4][4][64];
+    __shared__ f32x4 dg[2][4][64];
 
-    // One chunk: record S and D, then the state update.
-    auto chunk = [&](const ScanOps& cur, int n) {
+    // One chunk: record S and D, then the state update.  The operands of
+    // chunk `pf` (two ahead; clamped, so the last chunks reload the final one)
+    // are loaded into `nxt`, their 18 loads interleaved with the 32 MFMAs of
+    // W S so the memory pipe runs beside the matrix pipe.
+    auto chunk = [&](const ScanOps& cur, ScanOps& nxt, int n, int pf) {
         const int par = n & 1;
         const size_t cidx = (size_t)vh * nch + n;
         float* sh = w.sh + cidx * kDk * kDk;
 #pragma unroll
         for (int b = 0; b < 2; ++b)
             *reinterpret_cast<f32x4*>(sh + (size_t)(((2 * wave + b) * 8 + tl) * 64 + lane) * 4) = Sb[b];
+        load_scan_ops(w, nxt, min(pf, nch - 1), vh, kh, tl, nch, wave, g, lane);
         // Partial W S over this wave's 32 state rows, all 4 token blocks.
 #pragma unroll
         for (int tb = 0; tb < 4; ++tb) {
@@ -490,22 +495,29 @@ __global__ __launch_bounds__(256) void dn_chunk_scan(PrefillWork w, float* __res
             for (int b = 0; b < 2; ++b) pws = mfma16x4(cur.wa[tb][b], Sb[b], pws);
             red[par][wave][tb][lane] = pws;
         }
+#pragma unroll
+        for (int i = 0; i < 18; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);   // one VMEM read
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one MFMA
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, 14, 0);
         lds_barrier();
-        // Every wave forms D = U - W S for all 4 token blocks (its rows of the
-        // update need them all) and records token block `wave`.
+        // Wave w forms D = U - W S of token block w, records it, and shares
+        // e^{G_last - G} D with the other waves (each needs all 4 blocks for
+        // its rows of the update).
+        {
+            f32x4 ws = red[par][0][wave][lane];
+#pragma unroll
+            for (int v = 1; v < 4; ++v) ws += red[par][v][wave][lane];
+            const f32x4 dw = v4(cur.ut) - ws;
+            *reinterpret_cast<f32x4*>(w.dh + cidx * CB + (size_t)((wave * 8 + tl) * 64 + lane) * 4) = dw;
+            dg[par][wave][lane] = dw * v4(cur.gdv);
+        }
+        lds_barrier();
         f32x4 D[4];
 #pragma unroll
-        for (int tb = 0; tb < 4; ++tb) {
-            f32x4 ws = red[par][0][tb][lane];
-#pragma unroll
-            for (int v = 1; v < 4; ++v) ws += red[par][v][tb][lane];
-            D[tb] = v4(cur.ut[tb]) - ws;
-            if (tb == wave)
-                *reinterpret_cast<f32x4*>(w.dh + cidx * CB + (size_t)((tb * 8 + tl) * 64 + lane) * 4) = D[tb];
-        }
+        for (int tb = 0; tb < 4; ++tb) D[tb] = dg[par][tb][lane];
         // S = gamma_last S + K^T (e^{G_last - G} D).
-#pragma unroll
-        for (int tb = 0; tb < 4; ++tb) D[tb] *= v4(cur.gdv[tb]);
 #pragma unroll
         for (int b = 0; b < 2; ++b) {
             f32x4 acc = Sb[b] * cur.glast;
@@ -518,16 +530,13 @@ __global__ __launch_bounds__(256) void dn_chunk_scan(PrefillWork w, float* __res
     // mostly from HBM): three register sets in rotation, no copies.
     ScanOps o0, o1, o2;
     load_scan_ops(w, o0, 0, vh, kh, tl, nch, wave, g, lane);
-    if (nch > 1) load_scan_ops(w, o1, 1, vh, kh, tl, nch, wave, g, lane);
+    load_scan_ops(w, o1, min(1, nch - 1), vh, kh, tl, nch, wave, g, lane);
     for (int n = 0; n < nch; n += 3) {
-        if (n + 2 < nch) load_scan_ops(w, o2, n + 2, vh, kh, tl, nch, wave, g, lane);
-        chunk(o0, n);
+        chunk(o0, o2, n, n + 2);
         if (n + 1 >= nch) break;
-        if (n + 3 < nch) load_scan_ops(w, o0, n + 3, vh, kh, tl, nch, wave, g, lane);
-        chunk(o1, n + 1);
+        chunk(o1, o0, n + 1, n + 3);
         if (n + 2 >= nch) break;
-        if (n + 4 < nch) load_scan_ops(w, o1, n + 4, vh, kh, tl, nch, wave, g, lane);
-        chunk(o2, n + 2);
+        chunk(o2, o1, n + 2, n + 4);
     }
 #pragma unroll
     for (int b = 0; b < 2; ++b)
