@@ -26,9 +26,10 @@
 //     straight from the token-major qkv (no transpose); q/k L2 norm (q also
 //     scaled by 1/sqrt(dk)); beta = sigmoid(b), g = ssm_a * softplus(a +
 //     dt_bias) (Prefill.cs:239-248).
-//  2. deltanet_conv_writeback: conv window <- last K-1 raw inputs
-//     (Prefill.cs:192-204), reproducing the reference's read past the channel
-//     row when T < K-1.
+//     For T >= K-1 it also writes the conv window <- last K-1 raw inputs
+//     (Prefill.cs:192-204).
+//  2. deltanet_conv_writeback (T < K-1 only): the conv window write-back
+//     reproducing the reference's read past the channel row.
 //  3. dn_chunk_prep (one workgroup per k-head and chunk; the R v-heads of the
 //     k-head share K K^T and Q K^T): K K^T and Q K^T on MFMA, the decay masks,
 //     T = (I+A)^-1 by blocked forward substitution (16x16 diagonal blocks
@@ -137,7 +138,8 @@ constexpr int PT = 16;
 __global__ __launch_bounds__(kDk) void deltanet_prefill_prep(
     const float* __restrict__ qkv, const float* __restrict__ bin, const float* __restrict__ ain,
     const float* __restrict__ conv_w, const float* __restrict__ ssm_a,
-    const float* __restrict__ dt_bias, PrefillWork w, int T, int nk, int nv, int nch, float eps) {
+    const float* __restrict__ dt_bias, PrefillWork w, float* __restrict__ cs, int T, int nk,
+    int nv, int nch, float eps) {
     const int tg = blockIdx.x, hb = blockIdx.y, tid = threadIdx.x;
     const int t0 = tg * PT, n = tg >> 2, tb = tg & 3;
     const int key_dim = nk * kDk, conv_dim = 2 * key_dim + nv * kDk;
@@ -153,6 +155,18 @@ __global__ __launch_bounds__(kDk) void deltanet_prefill_prep(
         const int t = t0 - 3 + j;
         const float xv = qkv[(size_t)min(max(t, 0), T - 1) * conv_dim + c];
         x[j] = (t >= 0 && t < T) ? xv : 0.0f;
+    }
+    // Conv window write-back (T >= 3): the group holding token T - 1 also holds
+    // the raw inputs T-3 .. T-1, at x[T - t0 + j].
+    if (T >= kConvState && t0 <= T - 1 && T - 1 < t0 + PT) {
+#pragma unroll
+        for (int j = 0; j < kConvState; ++j) {
+            float v = 0.0f;
+#pragma unroll
+            for (int jj = 0; jj < PT + 3; ++jj)
+                if (jj == T - t0 + j) v = x[jj];
+            cs[(size_t)c * kConvState + j] = v;
+        }
     }
     __shared__ float tile[PT][kDk + 4];
     __shared__ float nrm[PT];
@@ -531,13 +545,17 @@ __global__ __launch_bounds__(256) void dn_chunk_scan(PrefillWork w, float* __res
     ScanOps o0, o1, o2;
     load_scan_ops(w, o0, 0, vh, kh, tl, nch, wave, g, lane);
     load_scan_ops(w, o1, min(1, nch - 1), vh, kh, tl, nch, wave, g, lane);
-    for (int n = 0; n < nch; n += 3) {
+    // Whole triples in a branch-free body, then the 0-2 remaining chunks.
+    const int ntrip = nch / 3;
+    for (int it = 0; it < ntrip; ++it) {
+        const int n = 3 * it;
         chunk(o0, o2, n, n + 2);
-        if (n + 1 >= nch) break;
         chunk(o1, o0, n + 1, n + 3);
-        if (n + 2 >= nch) break;
         chunk(o2, o1, n + 2, n + 4);
     }
+    const int nt = 3 * ntrip;
+    if (nt < nch) chunk(o0, o2, nt, nt + 2);
+    if (nt + 1 < nch) chunk(o1, o0, nt + 1, nt + 3);
 #pragma unroll
     for (int b = 0; b < 2; ++b)
 #pragma unroll
@@ -691,11 +709,11 @@ hipError_t launch_deltanet_prefill(q35m_ctx* c, int layer, int seq, int T, const
     {
         ProfScope ps_(c, K_DN_PREFILL_PREP);
         hipLaunchKernelGGL(deltanet_prefill_prep, dim3(nch * (CH / PT), 2 * d.nk + d.nv), dim3(kDk),
-                           0, c->stream, qkv, b, a, L.conv_w, L.ssm_a, L.dt_bias, w, T, d.nk,
+                           0, c->stream, qkv, b, a, L.conv_w, L.ssm_a, L.dt_bias, w, cs, T, d.nk,
                            d.nv, nch, d.eps);
     }
-    if ((e = hipGetLastError()) != hipSuccess) return e;
-    {
+    if (T < kConvState) {
+        if ((e = hipGetLastError()) != hipSuccess) return e;
         ProfScope ps_(c, K_DN_CONV_WRITEBACK);
         hipLaunchKernelGGL(deltanet_conv_writeback, dim3((d.conv_dim + 255) / 256), dim3(256), 0,
                            c->stream, qkv, L.conv_w, cs, T, d.conv_dim);
