@@ -568,10 +568,10 @@ __global__ __launch_bounds__(256) void dn_chunk_scan(PrefillWork w, float* __res
 // Wave w computes column tiles 2w, 2w+1 of all 4 token blocks: its S columns
 // (16 KiB) and D columns stay in registers.  The A operands shared by the 4
 // waves -- gamma-scaled Q (32 KiB) and the 10 causal blocks of M o QK^T --
-// are loaded once per workgroup into LDS.  The RMS spans the 4 waves' columns
-// of a row: one LDS exchange.  The epilogue goes row-major through LDS, so z
-// (prefetched at the start) and out move as coalesced float4 rows.
-__global__ __launch_bounds__(256) void dn_chunk_out(PrefillWork w, const float* __restrict__ z,
+// are loaded once per workgroup into LDS.  O goes row-major through LDS (in
+// the space Q used), so the RMS of a row is a 32-lane reduction and z and out
+// move as coalesced float4 rows.
+__global__ __launch_bounds__(256, 3) void dn_chunk_out(PrefillWork w, const float* __restrict__ z,
                                                     const float* __restrict__ wnorm,
                                                     float* __restrict__ out, int T, int nk,
                                                     int nv, int nch, float eps) {
@@ -587,10 +587,12 @@ __global__ __launch_bounds__(256) void dn_chunk_out(PrefillWork w, const float* 
     const float4* aq = reinterpret_cast<const float4*>(w.aqk + cidx * CH * CH);
     const float* gm = w.gam + cidx * CH;
 
-    __shared__ float4 q_s[4 * 8][64];     // [tb][kb] A-layout blocks of gamma Q
+    // q_s: [tb][kb] A-layout blocks of gamma Q; reused as o_s, the row-major
+    // output tile [64][128 + 4], once every wave is past its last Q read.
+    __shared__ float4 qo_s[CH * (kDk + 4) / 4];
     __shared__ float4 a_s[10][64];        // causal blocks (tb, j <= tb) of M o QK^T
-    __shared__ float ssq[4][CH];
-    __shared__ float o_s[CH][kDk + 4];
+    float4 (*q_s)[64] = reinterpret_cast<float4 (*)[64]>(qo_s);
+    float (*o_s)[kDk + 4] = reinterpret_cast<float (*)[kDk + 4]>(qo_s);
 
     f32x4 Sc[8][2];           // S[16 kb .. +15][16 (2w + cc) .. +15], D layout
     f32x4 Dc[4][2];           // D[16 tb .. +15][same columns]
@@ -628,15 +630,6 @@ __global__ __launch_bounds__(256) void dn_chunk_out(PrefillWork w, const float* 
             if (o4 < 10 * 64) a_s[o4 >> 6][o4 & 63] = av[i];
         }
     }
-    // z rows of this (chunk, v-head): float4 o4 = tid + 256 i is row o4 / 32,
-    // columns 4 (o4 % 32) ..; rows past T read row T - 1 and are not stored.
-    const int t0 = n * CH;
-    float4 zr[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const int o4 = tid + 256 * i, t = min(t0 + (o4 >> 5), T - 1);
-        zr[i] = reinterpret_cast<const float4*>(z + ((size_t)t * nv + vh) * kDk)[o4 & 31];
-    }
     __syncthreads();
 
     f32x4 O[4][2];
@@ -657,30 +650,35 @@ __global__ __launch_bounds__(256) void dn_chunk_out(PrefillWork w, const float* 
         }
         O[tb][0] = acc0;
         O[tb][1] = acc1;
-        // Sum of squares of rows 16 tb + 4g + r over this wave's 32 columns.
-        f32x4 sq = acc0 * acc0 + acc1 * acc1;
-#pragma unroll
-        for (int m = 1; m < 16; m <<= 1)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) sq[r] += __shfl_xor(sq[r], m, kWave);
-        if (c16 == 0)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) ssq[wave][16 * tb + 4 * g + r] = sq[r];
     }
+    // z rows of this (chunk, v-head): float4 o4 = tid + 256 i is row o4 / 32,
+    // columns 4 (o4 % 32) ..; rows past T read row T - 1 and are not stored.
+    const int t0 = n * CH;
+    float4 zr[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int o4 = tid + 256 * i, t = min(t0 + (o4 >> 5), T - 1);
+        zr[i] = reinterpret_cast<const float4*>(z + ((size_t)t * nv + vh) * kDk)[o4 & 31];
+    }
+    lds_barrier();
 #pragma unroll
     for (int tb = 0; tb < 4; ++tb)
 #pragma unroll
-        for (int cc = 0; cc < 2; ++cc)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) o_s[16 * tb + 4 * g + r][16 * (2 * wave + cc) + c16] = O[tb][cc][r];
+        for (int r = 0; r < 4; ++r) {
+            o_s[16 * tb + 4 * g + r][32 * wave + c16] = O[tb][0][r];
+            o_s[16 * tb + 4 * g + r][32 * wave + 16 + c16] = O[tb][1][r];
+        }
     lds_barrier();
+    // Row-major epilogue: lanes 0-31 of a wave hold one row, 32-63 the next.
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
         const int o4 = tid + 256 * i, row = o4 >> 5, c4 = o4 & 31, t = t0 + row;
-        if (t >= T) continue;
-        const float rs = 1.0f / sqrtf((ssq[0][row] + ssq[1][row] + ssq[2][row] + ssq[3][row]) /
-                                          (float)kDk + eps);
         const float4 o = *reinterpret_cast<const float4*>(&o_s[row][4 * c4]);
+        float ss = o.x * o.x + o.y * o.y + o.z * o.z + o.w * o.w;
+#pragma unroll
+        for (int m = 1; m < 32; m <<= 1) ss += __shfl_xor(ss, m, kWave);
+        if (t >= T) continue;
+        const float rs = 1.0f / sqrtf(ss / (float)kDk + eps);
         const float4 wn = reinterpret_cast<const float4*>(wnorm)[c4];
         float4 r;
         r.x = o.x * rs * wn.x * silu(zr[i].x);
