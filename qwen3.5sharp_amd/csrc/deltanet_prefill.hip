@@ -140,7 +140,10 @@ __global__ __launch_bounds__(kDk) void deltanet_prefill_prep(
     const float* __restrict__ conv_w, const float* __restrict__ ssm_a,
     const float* __restrict__ dt_bias, PrefillWork w, float* __restrict__ cs, int T, int nk,
     int nv, int nch, float eps) {
-    const int tg = blockIdx.x, hb = blockIdx.y, tid = threadIdx.x;
+    // Head blocks vary fastest over the launch, so the workgroups in flight
+    // read whole 32 KiB token rows of qkv rather than one 512-byte column of
+    // many rows (which would fall on few HBM channels).
+    const int hb = blockIdx.x, tg = blockIdx.y, tid = threadIdx.x;
     const int t0 = tg * PT, n = tg >> 2, tb = tg & 3;
     const int key_dim = nk * kDk, conv_dim = 2 * key_dim + nv * kDk;
     int c;
@@ -149,12 +152,19 @@ __global__ __launch_bounds__(kDk) void deltanet_prefill_prep(
     else c = 2 * key_dim + (hb - 2 * nk) * kDk + tid;
     const float w0 = conv_w[c], w1 = conv_w[conv_dim + c], w2 = conv_w[2 * conv_dim + c],
                 w3 = conv_w[3 * conv_dim + c];
+    // All 19 loads issue back to back from clamped rows; the zero padding is a
+    // multiply by 0/1 (a select on the uniform row test would become a branch
+    // around each load and serialise them).
     float x[PT + 3];
 #pragma unroll
     for (int j = 0; j < PT + 3; ++j) {
         const int t = t0 - 3 + j;
-        const float xv = qkv[(size_t)min(max(t, 0), T - 1) * conv_dim + c];
-        x[j] = (t >= 0 && t < T) ? xv : 0.0f;
+        x[j] = qkv[(size_t)min(max(t, 0), T - 1) * conv_dim + c];
+    }
+#pragma unroll
+    for (int j = 0; j < PT + 3; ++j) {
+        const int t = t0 - 3 + j;
+        x[j] *= (t >= 0 && t < T) ? 1.0f : 0.0f;
     }
     // Conv window write-back (T >= 3): the group holding token T - 1 also holds
     // the raw inputs T-3 .. T-1, at x[T - t0 + j].
@@ -576,7 +586,9 @@ __global__ __launch_bounds__(256, 3) void dn_chunk_out(PrefillWork w, const floa
                                                     float* __restrict__ out, int T, int nk,
                                                     int nv, int nch, float eps) {
     const int L = xcd_remap(blockIdx.x, gridDim.x);
-    const int vh = L / nch, n = L % nch;
+    // v-heads vary fastest, so the z rows and output rows in flight are whole
+    // token rows (16 KiB) rather than one 512-byte column of many rows.
+    const int vh = L % nv, n = L / nv;
     const int kh = vh / (nv / nk);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int g = lane >> 4, c16 = lane & 15;
@@ -706,7 +718,7 @@ hipError_t launch_deltanet_prefill(q35m_ctx* c, int layer, int seq, int T, const
     hipError_t e;
     {
         ProfScope ps_(c, K_DN_PREFILL_PREP);
-        hipLaunchKernelGGL(deltanet_prefill_prep, dim3(nch * (CH / PT), 2 * d.nk + d.nv), dim3(kDk),
+        hipLaunchKernelGGL(deltanet_prefill_prep, dim3(2 * d.nk + d.nv, nch * (CH / PT)), dim3(kDk),
                            0, c->stream, qkv, b, a, L.conv_w, L.ssm_a, L.dt_bias, w, cs, T, d.nk,
                            d.nv, nch, d.eps);
     }
