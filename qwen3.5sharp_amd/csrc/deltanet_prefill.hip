@@ -305,16 +305,29 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep(PrefillWork w, int T, in
 
     // Block bi: bi < 10 -> K K^T block (rb, cb), rows 16rb + 4g + r, cols 16cb + c;
     //           bi >= 10 -> (Q K^T)^T block: D rows = keys 16cb + 4g + r, cols = queries 16rb + c.
+    // The 16 operand loads of block m + 1 are in flight while block m's 32
+    // MFMAs run.
     f32x4 blk[5];
-#pragma unroll
-    for (int m = 0; m < 5; ++m) {
+    float4 oa[2][8], ob[2][8];
+    auto load_blk = [&](int m, float4 (&a)[8], float4 (&b)[8]) {
         const int bi = wave + 4 * m;
         const int mat = bi / 10, rb = kTriRb[bi % 10], cb = kTriCb[bi % 10];
-        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll 2
+        const float* pa = kA + (size_t)(mat ? cb : rb) * 8 * 256;
+        const float* pb = (mat ? qA : kA) + (size_t)(mat ? rb : cb) * 8 * 256;
+#pragma unroll
         for (int q = 0; q < kDk / 16; ++q) {
-            const float4 a = mat ? *blk4(kA, cb, q, lane) : *blk4(kA, rb, q, lane);
-            const float4 b = mat ? *blk4(qA, rb, q, lane) : *blk4(kA, cb, q, lane);
+            a[q] = *blk4(pa, 0, q, lane);
+            b[q] = *blk4(pb, 0, q, lane);
+        }
+    };
+    load_blk(0, oa[0], ob[0]);
+#pragma unroll
+    for (int m = 0; m < 5; ++m) {
+        if (m + 1 < 5) load_blk(m + 1, oa[(m + 1) & 1], ob[(m + 1) & 1]);
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int q = 0; q < kDk / 16; ++q) {
+            const float4 a = oa[m & 1][q], b = ob[m & 1][q];
             acc = mfma16(a.x, b.x, acc);
             acc = mfma16(a.y, b.y, acc);
             acc = mfma16(a.z, b.z, acc);
@@ -327,6 +340,18 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep(PrefillWork w, int T, in
     for (int rr = 0; rr < R; ++rr) {
         const int vh = kh * R + rr;
         const size_t cidx = (size_t)vh * nch + n;
+        // Right-hand sides of the solve, one column block (k^ blocks 0..7, v
+        // blocks 8..15) ahead: the first is issued now, so its latency hides
+        // behind the gates, masks and diagonal inverses.
+        const float* vD = w.vd + cidx * CB;
+        auto load_rhs = [&](int k4, float4 (&x)[4]) {
+            const int cbk = wave + 4 * k4;
+            const float* src = cbk >= 8 ? vD : kD;
+#pragma unroll
+            for (int ib = 0; ib < 4; ++ib) x[ib] = *blk4(src, ib, cbk & 7, lane);
+        };
+        float4 xc[4];
+        load_rhs(0, xc);
         // Gates and the fp64 running sum of g; padded tokens get beta = g = 0.
         if (wave == 0) {
             const int t = min(t0 + lane, T - 1);
@@ -390,7 +415,6 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep(PrefillWork w, int T, in
         __syncthreads();
         // Y = (I + A)^-1 X for X = diag(beta gamma) K^ (-> W) and diag(beta) V (-> U),
         // block row by block row; the wave takes column blocks wave + 4k of the 16.
-        const float* vD = w.vd + cidx * CB;
         float* wA = w.wa + cidx * CB;
         float* uD = w.ud + cidx * CB;
 #pragma unroll 1
@@ -398,16 +422,19 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep(PrefillWork w, int T, in
             const int cbk = wave + 4 * k4;
             const bool isV = cbk >= 8;
             const int kb = cbk & 7;
+            float4 xn[4];
+            load_rhs(min(k4 + 1, 3), xn);
             f32x4 Y[4];
 #pragma unroll
             for (int ib = 0; ib < 4; ++ib) {
-                const float4 xv = isV ? *blk4(vD, ib, kb, lane) : *blk4(kD, ib, kb, lane);
+                const float4 xv = xc[ib];
                 const float* xp = reinterpret_cast<const float*>(&xv);
                 f32x4 acc;
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const int row = 16 * ib + 4 * g + r;
-                    acc[r] = xp[r] * (isV ? bet[row] : bet[row] * gam[row]);
+                    const float gm = gam[row];
+                    acc[r] = xp[r] * bet[row] * (isV ? 1.0f : gm);
                 }
 #pragma unroll
                 for (int jb = 0; jb < ib; ++jb) {
@@ -433,6 +460,8 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep(PrefillWork w, int T, in
                     reinterpret_cast<float4*>(wA)[(ib * 8 + kb) * 64 + lane] = av;
                 }
             }
+#pragma unroll
+            for (int ib = 0; ib < 4; ++ib) xc[ib] = xn[ib];
         }
         __syncthreads();
     }
