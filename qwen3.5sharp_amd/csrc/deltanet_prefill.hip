@@ -298,6 +298,15 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep(PrefillWork w, int T, in
     __shared__ float tr[4][16][17];   // per-wave transpose scratch
     __shared__ double Gd[CH];
     __shared__ float bet[CH], gam[CH];
+    __shared__ float pre_b[kMaxVPerK][CH], pre_g[kMaxVPerK][CH];
+
+    // beta and g of the R v-heads, fetched up front (thread = (v-head, token)).
+    if (tid < R * CH) {
+        const int rr = tid / CH, j = tid % CH;
+        const int t = min(t0 + j, T - 1);
+        pre_b[rr][j] = w.beta[(size_t)t * nv + kh * R + rr];
+        pre_g[rr][j] = w.gl[(size_t)t * nv + kh * R + rr];
+    }
 
     const float* kA = w.ka + ((size_t)kh * nch + n) * CB;
     const float* qA = w.qa + ((size_t)kh * nch + n) * CB;
@@ -335,6 +344,7 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep(PrefillWork w, int T, in
         }
         blk[m] = acc;
     }
+    __syncthreads();
 
 #pragma unroll 1
     for (int rr = 0; rr < R; ++rr) {
@@ -354,9 +364,8 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep(PrefillWork w, int T, in
         load_rhs(0, xc);
         // Gates and the fp64 running sum of g; padded tokens get beta = g = 0.
         if (wave == 0) {
-            const int t = min(t0 + lane, T - 1);
             const bool valid = lane < tn;
-            const float bv = w.beta[(size_t)t * nv + vh], gv = w.gl[(size_t)t * nv + vh];
+            const float bv = pre_b[rr][lane], gv = pre_g[rr][lane];
             double G = valid ? (double)gv : 0.0;
 #pragma unroll
             for (int o = 1; o < 64; o <<= 1) {

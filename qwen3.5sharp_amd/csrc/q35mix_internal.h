@@ -20,7 +20,7 @@ constexpr int kRopeDim = 64;    // rotated dims
 constexpr int kRopeHalf = 32;
 constexpr int kGqaGroup = 4;    // q heads per kv head
 constexpr int kMaxBatch = 64;   // sequences per mixer launch
-constexpr int kMaxVPerK = 4;    // DeltaNet v-heads per k-head (one decode workgroup each)
+constexpr int kMaxVPerK = 4;    // DeltaNet v-heads per k-head (chunk prep stages their gates)
 
 // Per-launch sequence batch, passed by value in the kernel arguments.
 struct SeqBatch {
