@@ -344,6 +344,9 @@ def main():
     if want("dn_prefill"):
         log("[bench] DeltaNet prefill T=2048 ...")
         ms, kt, x = bench_dn_prefill(K, W)
+        # Per-step kernel time (the scan and output pass run in segments, the
+        # output segments on a second stream beside the scan).
+        kt = {k: (v[0] * v[1] / K, 1) for k, v in kt.items()}
         tok_s = 2048 / (ms / 1e3)
         kname, kms = dominant(kt)
         log(f"[bench] DeltaNet prefill: {ms:.3f} ms/step, {tok_s:.0f} tok/s; kernels {kt}")
