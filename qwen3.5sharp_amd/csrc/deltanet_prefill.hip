@@ -644,62 +644,74 @@ __global__ __launch_bounds__(256, 3) void dn_chunk_out(PrefillWork w, const floa
     float4 (*q_s)[64] = reinterpret_cast<float4 (*)[64]>(qo_s);
     float (*o_s)[kDk + 4] = reinterpret_cast<float (*)[kDk + 4]>(qo_s);
 
-    f32x4 Sc[8][2];           // S[16 kb .. +15][16 (2w + cc) .. +15], D layout
-    f32x4 Dc[4][2];           // D[16 tb .. +15][same columns]
-#pragma unroll
-    for (int kb = 0; kb < 8; ++kb)
-#pragma unroll
-        for (int cc = 0; cc < 2; ++cc) Sc[kb][cc] = v4(*blk4(sh, kb, 2 * wave + cc, lane));
-#pragma unroll
-    for (int tb = 0; tb < 4; ++tb)
-#pragma unroll
-        for (int cc = 0; cc < 2; ++cc) Dc[tb][cc] = v4(*blk4(dD, tb, 2 * wave + cc, lane));
+    // Load order: Q and M o QK^T first (staged into LDS), then S and D, whose
+    // blocks the MFMAs consume in arrival order (kb outer), so the products
+    // start while most of S is still in flight.
+    f32x4 O[4][2];
     {
         // Q: 2048 float4, 8 per thread; block = o4 / 64 = tb * 8 + kb, and the
         // lane's row within the block is its c16 (A layout).
         float4 qv[8];
 #pragma unroll
         for (int i = 0; i < 8; ++i) qv[i] = qA[tid + 256 * i];
-        float4 av[3];
-#pragma unroll
-        for (int i = 0; i < 3; ++i) {
+        // M o QK^T: the 640 float4 of the causal blocks, up to 3 per thread.
+        auto aload = [&](int i) {
             const int o4 = min(tid + 256 * i, 10 * 64 - 1);
             const int blk = o4 >> 6, tb = blk < 1 ? 0 : blk < 3 ? 1 : blk < 6 ? 2 : 3;
             const int j = blk - tb * (tb + 1) / 2;
-            av[i] = aq[(tb * 4 + j) * 64 + (o4 & 63)];
-        }
+            return aq[(tb * 4 + j) * 64 + (o4 & 63)];
+        };
+        const float4 av0 = aload(0), av1 = aload(1), av2 = aload(2);
+        float grr[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) grr[i] = gm[16 * ((tid + 256 * i) >> 9) + (tid & 15)];
+        __builtin_amdgcn_sched_barrier(0);     // keep the loads above ahead of S and D
+        f32x4 Sc[8][2];           // S[16 kb .. +15][16 (2w + cc) .. +15], D layout
+#pragma unroll
+        for (int kb = 0; kb < 8; ++kb)
+#pragma unroll
+            for (int cc = 0; cc < 2; ++cc) Sc[kb][cc] = v4(*blk4(sh, kb, 2 * wave + cc, lane));
+        f32x4 Dc[4][2];           // D[16 tb .. +15][same columns]
+#pragma unroll
+        for (int tb = 0; tb < 4; ++tb)
+#pragma unroll
+            for (int cc = 0; cc < 2; ++cc) Dc[tb][cc] = v4(*blk4(dD, tb, 2 * wave + cc, lane));
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            const int o4 = tid + 256 * i, tb = o4 >> 9;
-            const float gr = gm[16 * tb + (o4 & 15)];
+            const int o4 = tid + 256 * i;
+            const float gr = grr[i];
             q_s[o4 >> 6][o4 & 63] = make_float4(qv[i].x * gr, qv[i].y * gr, qv[i].z * gr, qv[i].w * gr);
         }
-#pragma unroll
-        for (int i = 0; i < 3; ++i) {
-            const int o4 = tid + 256 * i;
-            if (o4 < 10 * 64) a_s[o4 >> 6][o4 & 63] = av[i];
+        // Threads past the 640 float4 rewrite the last one with the same value
+        // (an unconditional store keeps these loads ahead of S and D).
+        a_s[tid >> 6][tid & 63] = av0;
+        a_s[(tid + 256) >> 6][tid & 63] = av1;
+        {
+            const int o4 = min(tid + 512, 10 * 64 - 1);
+            a_s[o4 >> 6][o4 & 63] = av2;
         }
-    }
-    __syncthreads();
+        lds_barrier();
 
-    f32x4 O[4][2];
 #pragma unroll
-    for (int tb = 0; tb < 4; ++tb) {
-        f32x4 acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+        for (int tb = 0; tb < 4; ++tb)
 #pragma unroll
-        for (int kb = 0; kb < 8; ++kb) {
-            const float4 q = q_s[tb * 8 + kb][lane];
-            acc0 = mfma16x4(q, Sc[kb][0], acc0);
-            acc1 = mfma16x4(q, Sc[kb][1], acc1);
-        }
+            for (int cc = 0; cc < 2; ++cc) O[tb][cc] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int j = 0; j <= tb; ++j) {
-            const float4 a = a_s[tb * (tb + 1) / 2 + j][lane];
-            acc0 = mfma16x4(a, Dc[j][0], acc0);
-            acc1 = mfma16x4(a, Dc[j][1], acc1);
-        }
-        O[tb][0] = acc0;
-        O[tb][1] = acc1;
+        for (int kb = 0; kb < 8; ++kb)
+#pragma unroll
+            for (int tb = 0; tb < 4; ++tb) {
+                const float4 q = q_s[tb * 8 + kb][lane];
+                O[tb][0] = mfma16x4(q, Sc[kb][0], O[tb][0]);
+                O[tb][1] = mfma16x4(q, Sc[kb][1], O[tb][1]);
+            }
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int tb = j; tb < 4; ++tb) {
+                const float4 a = a_s[tb * (tb + 1) / 2 + j][lane];
+                O[tb][0] = mfma16x4(a, Dc[j][0], O[tb][0]);
+                O[tb][1] = mfma16x4(a, Dc[j][1], O[tb][1]);
+            }
     }
     // z rows of this (chunk, v-head): float4 o4 = tid + 256 i is row o4 / 32,
     // columns 4 (o4 % 32) ..; rows past T read row T - 1 and are not stored.
