@@ -98,31 +98,36 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_flash(
     for (int db = 0; db < 16; ++db) O[db] = {0.f, 0.f, 0.f, 0.f};
     float m_run = -INFINITY, l_run = 0.0f;
 
-    // Staging: thread loads float4 idx = tid + 256 i (i < 8) of the 32 x 64 float4 tile.
-    float4 sk[8], sv[8];
-    auto load_tile = [&](int p0) {
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int idx = tid + 256 * i, row = idx >> 6, c4 = idx & 63;
-            // Rows past blk_len read row 0 instead (finite data; their scores are
-            // masked), so no select waits on the loads before the next tile.
-            const int p = p0 + row;
-            const int pc = p < blk_len ? p : 0;
-            sk[i] = *reinterpret_cast<const float4*>(Kh + (size_t)pc * kv_dim + 4 * c4);
-            sv[i] = *reinterpret_cast<const float4*>(Vh + (size_t)pc * kv_dim + 4 * c4);
-        }
-    };
-    load_tile(0);
+    // Staging: thread loads float4 idx = tid + 256 i (i < 8) of the 32 x 64
+    // float4 tile, i.e. row 4 i + tid / 64, float4 column tid % 64.  Rows past
+    // blk_len read row 0 instead (finite data; their scores are masked), so
+    // no select waits on the loads, and the refill is unconditional.
+    const int srow = tid >> 6, sc4 = tid & 63;
+    float4 sk0, sk1, sk2, sk3, sk4, sk5, sk6, sk7;
+    float4 sv0, sv1, sv2, sv3, sv4, sv5, sv6, sv7;
+#define Q35_LOAD_ROW(i, p0)                                                                  \
+    {                                                                                      \
+        const int p = (p0) + 4 * (i) + srow;                                               \
+        const size_t off = (size_t)(p < blk_len ? p : 0) * kv_dim + 4 * sc4;               \
+        sk##i = *reinterpret_cast<const float4*>(Kh + off);                                \
+        sv##i = *reinterpret_cast<const float4*>(Vh + off);                                \
+    }
+#define Q35_LOAD_TILE(p0)                                                                    \
+    Q35_LOAD_ROW(0, p0) Q35_LOAD_ROW(1, p0) Q35_LOAD_ROW(2, p0) Q35_LOAD_ROW(3, p0)            \
+    Q35_LOAD_ROW(4, p0) Q35_LOAD_ROW(5, p0) Q35_LOAD_ROW(6, p0) Q35_LOAD_ROW(7, p0)
+#define Q35_STORE_ROW(i)                                                                     \
+    *reinterpret_cast<float4*>(&Ks[4 * (i) + srow][4 * sc4]) = sk##i;                       \
+    *reinterpret_cast<float4*>(&Vs[4 * (i) + srow][4 * sc4]) = sv##i;
+    Q35_LOAD_TILE(0)
     for (int p0 = 0; p0 < blk_len; p0 += KT) {
         lds_barrier();
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            const int idx = tid + 256 * i, row = idx >> 6, c4 = idx & 63;
-            *reinterpret_cast<float4*>(&Ks[row][4 * c4]) = sk[i];
-            *reinterpret_cast<float4*>(&Vs[row][4 * c4]) = sv[i];
-        }
+        Q35_STORE_ROW(0) Q35_STORE_ROW(1) Q35_STORE_ROW(2) Q35_STORE_ROW(3)
+        Q35_STORE_ROW(4) Q35_STORE_ROW(5) Q35_STORE_ROW(6) Q35_STORE_ROW(7)
         lds_barrier();
-        if (p0 + KT < blk_len) load_tile(p0 + KT);
+        Q35_LOAD_TILE(p0 + KT)
+#undef Q35_LOAD_ROW
+#undef Q35_LOAD_TILE
+#undef Q35_STORE_ROW
 
         // S^T for positions p0 + 16 pb + (4g + r), queries c16.
         f32x4 st[2];
