@@ -305,7 +305,7 @@ hipError_t launch_attn_decode(q35m_ctx* c, int layer, const SeqBatch& sb, const 
     {
         ProfScope ps_(c, K_ATTN_DECODE_PARTIAL);
 #define Q35_PARTIAL(NS)                                                                          \
-    hipLaunchKernelGGL(attn_decode_partial<NS>, grid, dim3(NT), 0, c->stream, q_gate, k, v,      \
+    hipExtLaunchKernelGGL(attn_decode_partial<NS>, grid, dim3(NT), 0, c->stream, ps_.a, ps_.b, 0, q_gate, k, v,      \
                        L.q_norm, L.k_norm, L.k_cache, L.v_cache, c->rope_cos, c->rope_sin,       \
                        part_o, part_ml, d.nkv, c->cap, nchunks, d.eps, sb)
         if (nsub == 4) Q35_PARTIAL(4);
@@ -317,7 +317,7 @@ hipError_t launch_attn_decode(q35m_ctx* c, int layer, const SeqBatch& sb, const 
     if (e != hipSuccess) return e;
     {
         ProfScope ps_(c, K_ATTN_DECODE_MERGE);
-        hipLaunchKernelGGL(attn_decode_merge, dim3(d.nh * (kHd / MSLICE), sb.n), dim3(MT), 0, c->stream, part_o,
+        hipExtLaunchKernelGGL(attn_decode_merge, dim3(d.nh * (kHd / MSLICE), sb.n), dim3(MT), 0, c->stream, ps_.a, ps_.b, 0, part_o,
                            part_ml, q_gate, out, d.nkv, nchunks, chunk, sb);
     }
     return hipGetLastError();

@@ -215,7 +215,7 @@ hipError_t launch_attn_prefill(q35m_ctx* c, int layer, int seq, int start, int T
     float* qbuf = c->work;
     {
         ProfScope ps_(c, K_ATTN_PREFILL_PREP);
-        hipLaunchKernelGGL(attn_prefill_prep, dim3(T, d.nh + d.nkv), dim3(kWave), 0, c->stream, q_gate,
+        hipExtLaunchKernelGGL(attn_prefill_prep, dim3(T, d.nh + d.nkv), dim3(kWave), 0, c->stream, ps_.a, ps_.b, 0, q_gate,
                            k, v, L.q_norm, L.k_norm, K, V, c->rope_cos, c->rope_sin, qbuf, start, d.nh,
                            d.nkv, d.eps);
     }
@@ -223,8 +223,8 @@ hipError_t launch_attn_prefill(q35m_ctx* c, int layer, int seq, int start, int T
     if (e != hipSuccess) return e;
     {
         ProfScope ps_(c, K_ATTN_PREFILL_FLASH);
-        hipLaunchKernelGGL(attn_prefill_flash, dim3((T + QR - 1) / QR, d.nkv), dim3(256), 0,
-                           c->stream, qbuf, K, V, q_gate, out, start, T, d.nh, d.nkv);
+        hipExtLaunchKernelGGL(attn_prefill_flash, dim3((T + QR - 1) / QR, d.nkv), dim3(256), 0,
+                           c->stream, ps_.a, ps_.b, 0, qbuf, K, V, q_gate, out, start, T, d.nh, d.nkv);
     }
     return hipGetLastError();
 }

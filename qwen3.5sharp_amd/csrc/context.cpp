@@ -152,15 +152,15 @@ static hipEvent_t take_event(q35m_ctx* c) {
 ProfScope::ProfScope(q35m_ctx* ctx, int id) : c(ctx), kid(id) {
     if (!c->profile) return;
     a = take_event(c);
-    if (a) (void)hipEventRecord(a, c->stream);
+    b = a ? take_event(c) : nullptr;
+    if (!b && a) {
+        c->event_pool.push_back(a);
+        a = nullptr;
+    }
 }
 
 ProfScope::~ProfScope() {
-    if (!c->profile || !a) return;
-    hipEvent_t b = take_event(c);
-    if (!b) return;
-    (void)hipEventRecord(b, c->stream);
-    c->pending.push_back({a, b, kid});
+    if (a && b) c->pending.push_back({a, b, kid});
 }
 
 // Folds finished event pairs into the per-kernel totals.

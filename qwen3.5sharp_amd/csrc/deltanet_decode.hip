@@ -221,7 +221,7 @@ hipError_t launch_deltanet_decode(q35m_ctx* c, int layer, const SeqBatch& sb, co
     const Dims& d = c->d;
     const DeltaNetLayer& L = c->lin[layer];
     ProfScope ps_(c, K_DN_DECODE);
-    hipLaunchKernelGGL(deltanet_decode_kernel, dim3(sb.n * d.nv), dim3(NT), 0, c->stream, qkv, z,
+    hipExtLaunchKernelGGL(deltanet_decode_kernel, dim3(sb.n * d.nv), dim3(NT), 0, c->stream, ps_.a, ps_.b, 0, qkv, z,
                        b, a, out, L.conv_w, L.ssm_a, L.dt_bias, L.ssm_norm, L.state, L.conv, d.nk,
                        d.nv, c->n_seqs, d.eps, sb);
     return hipGetLastError();

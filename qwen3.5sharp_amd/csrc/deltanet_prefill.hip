@@ -768,32 +768,32 @@ hipError_t launch_deltanet_prefill(q35m_ctx* c, int layer, int seq, int T, const
     hipError_t e;
     {
         ProfScope ps_(c, K_DN_PREFILL_PREP);
-        hipLaunchKernelGGL(deltanet_prefill_prep, dim3(2 * d.nk + d.nv, nch * (CH / PT)), dim3(kDk),
-                           0, c->stream, qkv, b, a, L.conv_w, L.ssm_a, L.dt_bias, w, cs, T, d.nk,
+        hipExtLaunchKernelGGL(deltanet_prefill_prep, dim3(2 * d.nk + d.nv, nch * (CH / PT)), dim3(kDk),
+                           0, c->stream, ps_.a, ps_.b, 0, qkv, b, a, L.conv_w, L.ssm_a, L.dt_bias, w, cs, T, d.nk,
                            d.nv, nch, d.eps);
     }
     if (T < kConvState) {
         if ((e = hipGetLastError()) != hipSuccess) return e;
         ProfScope ps_(c, K_DN_CONV_WRITEBACK);
-        hipLaunchKernelGGL(deltanet_conv_writeback, dim3((d.conv_dim + 255) / 256), dim3(256), 0,
-                           c->stream, qkv, L.conv_w, cs, T, d.conv_dim);
+        hipExtLaunchKernelGGL(deltanet_conv_writeback, dim3((d.conv_dim + 255) / 256), dim3(256), 0,
+                           c->stream, ps_.a, ps_.b, 0, qkv, L.conv_w, cs, T, d.conv_dim);
     }
     if ((e = hipGetLastError()) != hipSuccess) return e;
     {
         ProfScope ps_(c, K_DN_CHUNK_PREP);
-        hipLaunchKernelGGL(dn_chunk_prep, dim3(d.nk * nch), dim3(256), 0, c->stream, w, T, d.nk,
+        hipExtLaunchKernelGGL(dn_chunk_prep, dim3(d.nk * nch), dim3(256), 0, c->stream, ps_.a, ps_.b, 0, w, T, d.nk,
                            d.nv, nch);
     }
     if ((e = hipGetLastError()) != hipSuccess) return e;
     {
         ProfScope ps_(c, K_DN_CHUNK_SCAN);
-        hipLaunchKernelGGL(dn_chunk_scan, dim3(d.nv * 8), dim3(256), 0, c->stream, w, state, d.nk,
+        hipExtLaunchKernelGGL(dn_chunk_scan, dim3(d.nv * 8), dim3(256), 0, c->stream, ps_.a, ps_.b, 0, w, state, d.nk,
                            d.nv, nch);
     }
     if ((e = hipGetLastError()) != hipSuccess) return e;
     {
         ProfScope ps_(c, K_DN_CHUNK_OUT);
-        hipLaunchKernelGGL(dn_chunk_out, dim3(d.nv * nch), dim3(256), 0, c->stream, w, z,
+        hipExtLaunchKernelGGL(dn_chunk_out, dim3(d.nv * nch), dim3(256), 0, c->stream, ps_.a, ps_.b, 0, w, z,
                            L.ssm_norm, out, T, d.nk, d.nv, nch, d.eps);
     }
     return hipGetLastError();

@@ -1,6 +1,7 @@
 // Internal declarations shared by the host ABI (context.cpp) and the kernels.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <cstddef>
@@ -126,10 +127,14 @@ size_t attn_prefill_work_bytes(const Dims& d, int T);
 hipError_t ensure_work(q35m_ctx* c, size_t bytes);
 
 // Event timer bracketing one kernel launch when profiling is on.
+// Per-kernel timer: when profiling is on, a and b are bound to the dispatch of
+// the kernel launched in the scope (hipExtLaunchKernelGGL start/stop events),
+// so they time its execution and not the gaps around it; otherwise both are
+// null and the launch is a plain one.
 struct ProfScope {
     q35m_ctx* c;
     int kid;
-    hipEvent_t a = nullptr;
+    hipEvent_t a = nullptr, b = nullptr;
     ProfScope(q35m_ctx* ctx, int id);
     ~ProfScope();
 };
