@@ -275,9 +275,9 @@ __global__ __launch_bounds__(MT) void attn_decode_merge(
 }
 
 // Sub-chunks per workgroup: as many as keep >= 1024 workgroups (4 per CU),
-// at most 4, so partials stay small next to the cache they summarise.
+// at most 8, so partials stay small next to the cache they summarise.
 int pick_nsub(int n, int nkv, int max_len) {
-    for (int ns = 4; ns > 1; ns >>= 1)
+    for (int ns = 8; ns > 1; ns >>= 1)
         if ((long)n * nkv * ((max_len + SUB * ns - 1) / (SUB * ns)) >= 1024) return ns;
     return 1;
 }
@@ -308,7 +308,8 @@ hipError_t launch_attn_decode(q35m_ctx* c, int layer, const SeqBatch& sb, const 
     hipExtLaunchKernelGGL(attn_decode_partial<NS>, grid, dim3(NT), 0, c->stream, ps_.a, ps_.b, 0, q_gate, k, v,      \
                        L.q_norm, L.k_norm, L.k_cache, L.v_cache, c->rope_cos, c->rope_sin,       \
                        part_o, part_ml, d.nkv, c->cap, nchunks, d.eps, sb)
-        if (nsub == 4) Q35_PARTIAL(4);
+        if (nsub == 8) Q35_PARTIAL(8);
+        else if (nsub == 4) Q35_PARTIAL(4);
         else if (nsub == 2) Q35_PARTIAL(2);
         else Q35_PARTIAL(1);
 #undef Q35_PARTIAL
