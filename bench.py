@@ -216,8 +216,10 @@ def bench_stack(n_steps=128, warmup=4, n_seqs=8, ctx_len=32768, n_layers=32):
             ctx.set_attn_weights(layer, wa)
             for s in range(n_seqs):
                 for kind in (q35mix.STATE_KEYS, q35mix.STATE_VALUES):
+                    # The whole head-major [kv_heads][capacity][256] block of the
+                    # (layer, seq) gets data (rows past `start` are rewritten by decode).
                     ptr, nbytes = ctx.state_device_ptr(layer, s, kind)
-                    fill = start * KV_DIM * 4
+                    fill = nbytes
                     off = 0
                     while off < fill:
                         n = min(block.nbytes, fill - off)

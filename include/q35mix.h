@@ -7,9 +7,10 @@
  * (between the projections and the output projection).  It owns, in HBM, the
  * state the reference keeps in Qwen35Model fields: the DeltaNet recurrent
  * state [H_v][dk][dv] and conv state [conv_dim][K-1] of every linear layer,
- * and the K/V cache [capacity][kv_heads*head_dim] of every full-attention
- * layer, per sequence.  Paths in citations are relative to the reference
- * repository root.
+ * and the K/V cache of every full-attention layer (the reference's
+ * [capacity][kv_heads*head_dim] rows, held head-major on the device), per
+ * sequence.  Paths in citations are relative to the reference repository
+ * root.
  *
  * Conventions
  *  - Every entry point returns an int status: Q35M_OK (0) or a negative
@@ -74,6 +75,9 @@ typedef struct q35m_ctx q35m_ctx;
                                   GatedDeltaNetOps.cs:76 (code layout)                    */
 #define Q35M_STATE_KEYS 2      /* K cache rows [len][kv_heads*head_dim], post-RoPE/norm */
 #define Q35M_STATE_VALUES 3    /* V cache rows [len][kv_heads*head_dim]                 */
+/* State read/write move the reference layouts above (K/V: whole rows only).
+ * On the device the K and V caches are head-major, [kv_heads][capacity]
+ * [head_dim] per (layer, seq), which is what q35m_state_device_ptr exposes. */
 
 /* ---- lifecycle -------------------------------------------------------- */
 

@@ -48,7 +48,8 @@ __global__ __launch_bounds__(NT, 2) void attn_decode_partial(
     if (p0 > pos) return;
     const int nh = nkv * kGqaGroup;
     const int kv_dim = nkv * kHd;
-    const size_t seq_off = (size_t)sb.seq[i] * cap * kv_dim + (size_t)kvh * kHd;
+    // Cache of one (sequence, kv head): [cap][256], head-major.
+    const size_t seq_off = ((size_t)sb.seq[i] * nkv + kvh) * cap * kHd;
     float* K = k_cache + seq_off;
     float* V = v_cache + seq_off;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -74,11 +75,11 @@ __global__ __launch_bounds__(NT, 2) void attn_decode_partial(
             float4 x = *reinterpret_cast<const float4*>(knew + (size_t)i * kv_dim + kvh * kHd + 4 * lane);
             x = rope_norm_row(x, lane, cs, sn, k_norm, eps, 1.0f);
             knew_s[lane] = x;
-            *reinterpret_cast<float4*>(K + (size_t)pos * kv_dim + 4 * lane) = x;
+            *reinterpret_cast<float4*>(K + (size_t)pos * kHd + 4 * lane) = x;
         } else if (wave == 1) {
             const float4 x = *reinterpret_cast<const float4*>(vnew + (size_t)i * kv_dim + kvh * kHd + 4 * lane);
             vnew_s[lane] = x;
-            *reinterpret_cast<float4*>(V + (size_t)pos * kv_dim + 4 * lane) = x;
+            *reinterpret_cast<float4*>(V + (size_t)pos * kHd + 4 * lane) = x;
         }
     }
     __syncthreads();
@@ -110,7 +111,7 @@ __global__ __launch_bounds__(NT, 2) void attn_decode_partial(
             const int pp = team + 16 * m;
             const int pabs = s0 + pp;
             const bool live = pp < np && pabs != pos;
-            const float4* krow = reinterpret_cast<const float4*>(K + (size_t)(live ? pabs : 0) * kv_dim);
+            const float4* krow = reinterpret_cast<const float4*>(K + (size_t)(live ? pabs : 0) * kHd);
 #pragma unroll
             for (int j = 0; j < 4; ++j)
                 kk[m][j] = live ? krow[l16 + 16 * j] : make_float4(0.f, 0.f, 0.f, 0.f);
@@ -120,7 +121,7 @@ __global__ __launch_bounds__(NT, 2) void attn_decode_partial(
             const int pp = ps + 4 * m;
             const int pabs = s0 + pp;
             const bool live = pp < np && pabs != pos;
-            const float4* vrow = reinterpret_cast<const float4*>(V + (size_t)(live ? pabs : 0) * kv_dim);
+            const float4* vrow = reinterpret_cast<const float4*>(V + (size_t)(live ? pabs : 0) * kHd);
             vv[m] = live ? vrow[d4] : make_float4(0.f, 0.f, 0.f, 0.f);
         }
         // The new row comes from LDS.

@@ -24,7 +24,7 @@ __global__ __launch_bounds__(kWave) void attn_prefill_prep(
     const float* __restrict__ vnew, const float* __restrict__ q_norm,
     const float* __restrict__ k_norm, float* __restrict__ K, float* __restrict__ V,
     const float* __restrict__ rope_cos, const float* __restrict__ rope_sin,
-    float* __restrict__ qbuf, int start, int nh, int nkv, float eps) {
+    float* __restrict__ qbuf, int start, int nh, int nkv, int cap, float eps) {
     const int t = blockIdx.x, r = blockIdx.y, lane = threadIdx.x;
     const int pos = start + t;
     const int kv_dim = nkv * kHd;
@@ -39,9 +39,11 @@ __global__ __launch_bounds__(kWave) void attn_prefill_prep(
         const int kvh = r - nh;
         float4 x = *reinterpret_cast<const float4*>(knew + (size_t)t * kv_dim + kvh * kHd + 4 * lane);
         x = rope_norm_row(x, lane, cs, sn, k_norm, eps, 1.0f);
-        *reinterpret_cast<float4*>(K + (size_t)pos * kv_dim + kvh * kHd + 4 * lane) = x;
+        // Head-major cache: row pos of kv head kvh at (kvh * cap + pos) * 256.
+        const size_t row = ((size_t)kvh * cap + pos) * kHd;
+        *reinterpret_cast<float4*>(K + row + 4 * lane) = x;
         const float4 v = *reinterpret_cast<const float4*>(vnew + (size_t)t * kv_dim + kvh * kHd + 4 * lane);
-        *reinterpret_cast<float4*>(V + (size_t)pos * kv_dim + kvh * kHd + 4 * lane) = v;
+        *reinterpret_cast<float4*>(V + row + 4 * lane) = v;
     }
 }
 
@@ -68,18 +70,18 @@ constexpr int LDKV = kHd + 4;   // padded LDS row stride of the K/V tiles
 __global__ __launch_bounds__(256, 2) void attn_prefill_flash(
     const float* __restrict__ qbuf, const float* __restrict__ K, const float* __restrict__ V,
     const float* __restrict__ q_gate, float* __restrict__ out, int start, int T, int nh,
-    int nkv) {
+    int nkv, int cap) {
     const int qb = gridDim.x - 1 - blockIdx.x, kvh = blockIdx.y;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int g = lane >> 4, c16 = lane & 15;
     const int h = kvh * kGqaGroup + wave;
-    const int kv_dim = nkv * kHd;
     const int r0 = qb * QR;
     const int blk_len = start + min(T - 1, r0 + QR - 1) + 1;
     const int my_t = min(r0 + c16, T - 1);
     const int my_len = start + my_t + 1;
-    const float* Kh = K + (size_t)kvh * kHd;
-    const float* Vh = V + (size_t)kvh * kHd;
+    // Head-major cache: kv head kvh's rows are [cap][256] from kvh * cap * 256.
+    const float* Kh = K + (size_t)kvh * cap * kHd;
+    const float* Vh = V + (size_t)kvh * cap * kHd;
 
     __shared__ float Ks[KT][LDKV];
     __shared__ float Vs[KT][LDKV];
@@ -108,7 +110,7 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_flash(
 #define Q35_LOAD_ROW(i, p0)                                                                  \
     {                                                                                      \
         const int p = (p0) + 4 * (i) + srow;                                               \
-        const size_t off = (size_t)(p < blk_len ? p : 0) * kv_dim + 4 * sc4;               \
+        const size_t off = (size_t)(p < blk_len ? p : 0) * kHd + 4 * sc4;                  \
         sk##i = *reinterpret_cast<const float4*>(Kh + off);                                \
         sv##i = *reinterpret_cast<const float4*>(Vh + off);                                \
     }
@@ -217,14 +219,15 @@ hipError_t launch_attn_prefill(q35m_ctx* c, int layer, int seq, int start, int T
         ProfScope ps_(c, K_ATTN_PREFILL_PREP);
         hipExtLaunchKernelGGL(attn_prefill_prep, dim3(T, d.nh + d.nkv), dim3(kWave), 0, c->stream, ps_.a, ps_.b, 0, q_gate,
                            k, v, L.q_norm, L.k_norm, K, V, c->rope_cos, c->rope_sin, qbuf, start, d.nh,
-                           d.nkv, d.eps);
+                           d.nkv, c->cap, d.eps);
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     {
         ProfScope ps_(c, K_ATTN_PREFILL_FLASH);
         hipExtLaunchKernelGGL(attn_prefill_flash, dim3((T + QR - 1) / QR, d.nkv), dim3(256), 0,
-                           c->stream, ps_.a, ps_.b, 0, qbuf, K, V, q_gate, out, start, T, d.nh, d.nkv);
+                           c->stream, ps_.a, ps_.b, 0, qbuf, K, V, q_gate, out, start, T, d.nh, d.nkv,
+                           c->cap);
     }
     return hipGetLastError();
 }

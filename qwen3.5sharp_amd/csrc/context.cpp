@@ -514,6 +514,28 @@ static int state_locate(q35m_ctx* ctx, int layer, int seq, int kind, char** base
     return fail(Q35M_ERR_INVALID, "unknown state kind %d", kind);
 }
 
+// K/V caches are head-major on the device ([kv_heads][cap][head_dim] per
+// (layer, seq)); state I/O moves whole rows in the reference layout
+// [rows][kv_heads * head_dim], one strided 2-D copy per kv head.
+static hipError_t kv_copy(q35m_ctx* ctx, char* dev, void* host, size_t bytes, bool to_host) {
+    const q35::Dims& d = ctx->d;
+    const size_t row_bytes = (size_t)d.kv_dim * sizeof(float), head_bytes = q35::kHd * sizeof(float);
+    const size_t rows = bytes / row_bytes;
+    if (rows == 0) return hipSuccess;
+    for (int h = 0; h < d.nkv; h++) {
+        char* dh = dev + (size_t)h * ctx->cap * head_bytes;
+        char* hh = static_cast<char*>(host) + (size_t)h * head_bytes;
+        hipError_t e = to_host ? hipMemcpy2DAsync(hh, row_bytes, dh, head_bytes, head_bytes, rows,
+                                                  hipMemcpyDeviceToHost, ctx->stream)
+                               : hipMemcpy2DAsync(dh, head_bytes, hh, row_bytes, head_bytes, rows,
+                                                  hipMemcpyHostToDevice, ctx->stream);
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
+static bool is_kv(int kind) { return kind == Q35M_STATE_KEYS || kind == Q35M_STATE_VALUES; }
+
 int q35m_state_read(q35m_ctx* ctx, int layer, int seq, int kind, void* host, size_t bytes) {
     char* base;
     size_t cap_bytes;
@@ -522,7 +544,13 @@ int q35m_state_read(q35m_ctx* ctx, int layer, int seq, int kind, void* host, siz
     if (!host) return fail(Q35M_ERR_INVALID, "null host buffer");
     if (bytes > cap_bytes)
         return fail(Q35M_ERR_INVALID, "read of %zu bytes exceeds the %zu-byte state", bytes, cap_bytes);
-    HIP_TRY(hipMemcpyAsync(host, base, bytes, hipMemcpyDeviceToHost, ctx->stream), "state_read");
+    if (is_kv(kind)) {
+        if (bytes % ((size_t)ctx->d.kv_dim * sizeof(float)))
+            return fail(Q35M_ERR_INVALID, "K/V reads move whole rows of %d floats", ctx->d.kv_dim);
+        HIP_TRY(kv_copy(ctx, base, host, bytes, true), "state_read");
+    } else {
+        HIP_TRY(hipMemcpyAsync(host, base, bytes, hipMemcpyDeviceToHost, ctx->stream), "state_read");
+    }
     HIP_TRY(hipStreamSynchronize(ctx->stream), "state_read");
     return Q35M_OK;
 }
@@ -537,7 +565,13 @@ int q35m_state_write(q35m_ctx* ctx, int layer, int seq, int kind, const void* ho
     if (bytes > cap_bytes)
         return fail(Q35M_ERR_INVALID, "write of %zu bytes exceeds the %zu-byte state", bytes,
                     cap_bytes);
-    HIP_TRY(hipMemcpyAsync(base, host, bytes, hipMemcpyHostToDevice, ctx->stream), "state_write");
+    if (is_kv(kind)) {
+        if (bytes % ((size_t)ctx->d.kv_dim * sizeof(float)))
+            return fail(Q35M_ERR_INVALID, "K/V writes move whole rows of %d floats", ctx->d.kv_dim);
+        HIP_TRY(kv_copy(ctx, base, const_cast<void*>(host), bytes, false), "state_write");
+    } else {
+        HIP_TRY(hipMemcpyAsync(base, host, bytes, hipMemcpyHostToDevice, ctx->stream), "state_write");
+    }
     HIP_TRY(hipStreamSynchronize(ctx->stream), "state_write");
     return Q35M_OK;
 }
