@@ -290,6 +290,26 @@ def cpu_baseline_prefill(x, T=2048):
     return T / dt, dt
 
 
+def measured_peaks():
+    """Ceilings measured on this GPU by libq35probe.so (plain streaming-read and
+    copy kernels, an fp32 MFMA loop), reported beside the datasheet peaks."""
+    path = os.path.join(ROOT, "qwen3.5sharp_amd", "libq35probe.so")
+    if not os.path.exists(path):
+        raise FileNotFoundError(f"{path} is not built (run __graft_entry__.build())")
+    lib = ctypes.CDLL(path)
+    out = {}
+    for name, fn, args in (("hbm_read_GBps", lib.q35p_hbm_read_gbs, (ctypes.c_size_t(1 << 31), 10)),
+                           ("hbm_copy_rw_GBps", lib.q35p_hbm_copy_gbs, (ctypes.c_size_t(1 << 30), 10)),
+                           ("mfma_f32_TFLOPs", lib.q35p_mfma_f32_tflops, (20000,))):
+        v = ctypes.c_double(0.0)
+        r = fn(*args, ctypes.byref(v))
+        if r != 0:
+            raise RuntimeError(f"{name} probe failed ({r})")
+        out[name] = v.value
+    out["datasheet"] = {"hbm_GBps": HBM_PEAK / 1e9, "mfma_f32_TFLOPs": FP32_PEAK / 1e12}
+    return out
+
+
 def cpu_info():
     model = "unknown"
     try:
@@ -309,7 +329,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default="", help="comma list of: dn_prefill,dn_decode,attn_decode,"
-                                               "attn_prefill,stack")
+                                               "attn_prefill,stack,peaks")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="also run one device-to-device copy of MIB MiB (a plain copy kernel "
                          "of known traffic, to scale FETCH_SIZE/WRITE_SIZE counters)")
@@ -430,6 +450,10 @@ def main():
                   "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
                   "dtype": "f32", "data": "synthetic", "config": {"workload": "partial run"}}
     result["workloads"] = workloads
+    if not only or "peaks" in only:
+        log("[bench] measured device ceilings ...")
+        result["measured_peaks"] = measured_peaks()
+        log(f"[bench] measured: {result['measured_peaks']}")
     print(json.dumps(result), flush=True)
 
 

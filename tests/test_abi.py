@@ -80,3 +80,12 @@ def test_no_device_here_is_an_error_not_a_fallback():
     assert h.value is None
     p = ctypes.c_void_p()
     assert q35mix.lib().q35m_malloc(ctypes.byref(p), 64) == q35mix.ERR_NO_DEVICE
+
+
+def test_probe_library_exports():
+    """bench.py's device-ceiling probes (a separate library, not the mixer ABI)."""
+    lib = ctypes.CDLL(os.path.join(ROOT, "qwen3.5sharp_amd", "libq35probe.so"))
+    for name in ("q35p_hbm_read_gbs", "q35p_hbm_copy_gbs", "q35p_mfma_f32_tflops"):
+        assert hasattr(lib, name), name
+    v = ctypes.c_double(0.0)
+    assert lib.q35p_mfma_f32_tflops(0, ctypes.byref(v)) == -1      # rejected before any device call
