@@ -66,12 +66,20 @@ constexpr int LDKV = kHd + 4;   // padded LDS row stride of the K/V tiles
 // Lane l = 16g + c: Q operand holds Q[row c][64g + s], s < 64 (reduction index
 // of instruction s for lane group g), O^T register r of block db holds
 // O[row c][16 db + 4g + r].  The next K/V tile is loaded into registers while
-// the current one computes.  Heaviest query blocks are scheduled first.
+// the current one computes.  Heavy and light query blocks are paired per CU.
 __global__ __launch_bounds__(256, 2) void attn_prefill_flash(
     const float* __restrict__ qbuf, const float* __restrict__ K, const float* __restrict__ V,
     const float* __restrict__ q_gate, float* __restrict__ out, int start, int T, int nh,
     int nkv, int cap) {
-    const int qb = gridDim.x - 1 - blockIdx.x, kvh = blockIdx.y;
+    // Work items ranked by cost (query block, heaviest first; kv heads
+    // innermost).  Workgroup L < half takes rank L and workgroup half + m
+    // takes rank total-1-m, so the two workgroups the dispatcher places on one
+    // CU when the whole grid is resident (L and L + half) carry a heavy and a
+    // light query block: causal work is balanced per CU, not per workgroup.
+    const int nqb = (T + QR - 1) / QR;
+    const int total = nqb * nkv, half = (total + 1) / 2, L = blockIdx.x;
+    const int rank = L < half ? L : total - 1 - (L - half);
+    const int qb = nqb - 1 - rank / nkv, kvh = rank % nkv;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int g = lane >> 4, c16 = lane & 15;
     const int h = kvh * kGqaGroup + wave;
@@ -225,7 +233,7 @@ hipError_t launch_attn_prefill(q35m_ctx* c, int layer, int seq, int start, int T
     if (e != hipSuccess) return e;
     {
         ProfScope ps_(c, K_ATTN_PREFILL_FLASH);
-        hipExtLaunchKernelGGL(attn_prefill_flash, dim3((T + QR - 1) / QR, d.nkv), dim3(256), 0,
+        hipExtLaunchKernelGGL(attn_prefill_flash, dim3((T + QR - 1) / QR * d.nkv), dim3(256), 0,
                            c->stream, ps_.a, ps_.b, 0, qbuf, K, V, q_gate, out, start, T, d.nh, d.nkv,
                            c->cap);
     }
