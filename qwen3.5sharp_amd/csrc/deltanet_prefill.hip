@@ -716,6 +716,8 @@ __global__ __launch_bounds__(256, 3) void dn_chunk_out(PrefillWork w, const floa
     // z rows of this (chunk, v-head): float4 o4 = tid + 256 i is row o4 / 32,
     // columns 4 (o4 % 32) ..; rows past T read row T - 1 and are not stored.
     const int t0 = n * CH;
+    // A thread's columns are the same in every row it handles (4 (tid % 32)).
+    const float4 wn = reinterpret_cast<const float4*>(wnorm)[tid & 31];
     float4 zr[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
@@ -741,7 +743,6 @@ __global__ __launch_bounds__(256, 3) void dn_chunk_out(PrefillWork w, const floa
         for (int m = 1; m < 32; m <<= 1) ss += __shfl_xor(ss, m, kWave);
         if (t >= T) continue;
         const float rs = 1.0f / sqrtf(ss / (float)kDk + eps);
-        const float4 wn = reinterpret_cast<const float4*>(wnorm)[c4];
         float4 r;
         r.x = o.x * rs * wn.x * silu(zr[i].x);
         r.y = o.y * rs * wn.y * silu(zr[i].y);
