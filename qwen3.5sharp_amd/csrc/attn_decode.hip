@@ -57,7 +57,10 @@ __global__ __launch_bounds__(NT, 2) void attn_decode_partial(
     __shared__ float4 q_s[kGqaGroup][kHd / 4];
     __shared__ float4 knew_s[kHd / 4];
     __shared__ float4 vnew_s[kHd / 4];
-    __shared__ float sc[kGqaGroup][SUB];
+    // Scores / weights and the rescale factors, double-buffered by sub-chunk
+    // parity so two barriers per sub-chunk suffice.
+    __shared__ float sc[2][kGqaGroup][SUB];
+    __shared__ float al_s[2][kGqaGroup];
     __shared__ float ml_s[kGqaGroup][2];
     __shared__ float4 obuf[4][kGqaGroup][kHd / 4];
 
@@ -103,6 +106,7 @@ __global__ __launch_bounds__(NT, 2) void attn_decode_partial(
     for (int sub = 0; sub < NSUB; ++sub) {
         const int s0 = p0 + sub * SUB;
         if (s0 > pos) break;                    // uniform across the workgroup
+        const int par = sub & 1;
         const int np = min(SUB, pos + 1 - s0);
         float4 kk[4][4];
         float4 vv[16];
@@ -148,24 +152,24 @@ __global__ __launch_bounds__(NT, 2) void attn_decode_partial(
             }
             if (l16 == 0)
 #pragma unroll
-                for (int h = 0; h < kGqaGroup; ++h) sc[h][team + 16 * m] = a[h];
+                for (int h = 0; h < kGqaGroup; ++h) sc[par][h][team + 16 * m] = a[h];
         }
-        __syncthreads();
+        lds_barrier();
         // Online softmax over the sub-chunk: wave h owns head h, lane = position.
         {
-            const float s = lane < np ? sc[wave][lane] : -INFINITY;
+            const float s = lane < np ? sc[par][wave][lane] : -INFINITY;
             const float mx = fmaxf(m_run, wave_max(s));
             const float e = lane < np ? __expf(s - mx) : 0.0f;
             const float alpha = __expf(m_run - mx);     // 0 on the first sub-chunk
             l_run = l_run * alpha + wave_sum(e);
             m_run = mx;
-            sc[wave][lane] = e;
-            if (lane == 0) ml_s[wave][0] = alpha;
+            sc[par][wave][lane] = e;
+            if (lane == 0) al_s[par][wave] = alpha;
         }
-        __syncthreads();
+        lds_barrier();
 #pragma unroll
         for (int h = 0; h < kGqaGroup; ++h) {
-            const float alpha = ml_s[h][0];
+            const float alpha = al_s[par][h];
             acc[h].x *= alpha; acc[h].y *= alpha; acc[h].z *= alpha; acc[h].w *= alpha;
         }
 #pragma unroll
@@ -173,14 +177,13 @@ __global__ __launch_bounds__(NT, 2) void attn_decode_partial(
             const int pp = ps + 4 * m;
 #pragma unroll
             for (int h = 0; h < kGqaGroup; ++h) {
-                const float e = sc[h][pp];
+                const float e = sc[par][h][pp];
                 acc[h].x += e * vv[m].x;
                 acc[h].y += e * vv[m].y;
                 acc[h].z += e * vv[m].z;
                 acc[h].w += e * vv[m].w;
             }
         }
-        __syncthreads();
     }
 
 #pragma unroll
