@@ -9,16 +9,19 @@
 // Ops.cs:281-357), causal softmax (Ops.SoftmaxCausal, Ops.cs:163-252),
 // P.V (Ops.AttentionCombine, Ops.cs:360-415), times sigmoid(gate).
 //
-// Pass 1 (attn_decode_partial): one workgroup per (sequence, kv head, chunk of
-// NSUB x 64 positions).  The 4 q heads of the kv head share every K/V row it
-// reads, so each cache byte is read once per token.  A 64-row sub-chunk is
-// processed with every K and V load issued before any arithmetic (64 KiB of
-// K and 64 KiB of V in flight per workgroup), which is what keeps HBM busy.
-// Each workgroup recomputes the 4 rotated, normed q rows (4 KiB of input); the
-// workgroup whose chunk holds the new position also rotates/norms the new K
-// row and writes K and V into the cache (single writer) and takes them from
-// LDS.  It emits, per q head, the chunk's max score m, sum of exp l and
-// unnormalised o = sum exp(s - m) v.
+// Pass 1 (attn_decode_partial): one workgroup per (sequence, kv head, chunk c
+// of NSUB 64-row sub-chunks).  Chunk c holds the sub-chunks c, c + nchunks,
+// c + 2 nchunks, ... so the workgroups of one cache that run together stream
+// adjacent rows.  The 4 q heads of the kv head share every K/V row it reads,
+// so each cache byte is read once per token.  A sub-chunk is processed with
+// every K and V load issued before any arithmetic (64 KiB of K and 64 KiB of
+// V in flight per workgroup), which is what keeps HBM busy; the first
+// sub-chunk's loads go out before the q preparation, so that preparation
+// (each workgroup rotates and norms the 4 q rows, 4 KiB of input) costs no
+// memory round trip of its own.  The workgroup that holds the new position
+// also rotates/norms the new K row, writes K and V into the cache (single
+// writer) and takes them from LDS.  It emits, per q head, the chunk's max
+// score m, sum of exp l and unnormalised o = sum exp(s - m) v.
 // Pass 2 (attn_decode_merge): per (sequence, q head) the chunks are merged by
 // log-sum-exp rescaling and the sigmoid gate is applied.
 //
@@ -34,6 +37,10 @@ namespace {
 constexpr int NT = 256;
 constexpr int SUB = 64;   // positions per sub-chunk
 
+__device__ __forceinline__ float4 sel4(bool c, float4 a, float4 b) {
+    return make_float4(c ? a.x : b.x, c ? a.y : b.y, c ? a.z : b.z, c ? a.w : b.w);
+}
+
 template <int NSUB>
 __global__ __launch_bounds__(NT, 2) void attn_decode_partial(
     const float* __restrict__ q_gate, const float* __restrict__ knew,
@@ -44,8 +51,9 @@ __global__ __launch_bounds__(NT, 2) void attn_decode_partial(
     float eps, SeqBatch sb) {
     const int c = blockIdx.x, kvh = blockIdx.y, i = blockIdx.z;
     const int pos = sb.pos[i];
-    const int p0 = c * SUB * NSUB;
-    if (p0 > pos) return;
+    // Workgroup c takes the sub-chunks c, c + nchunks, c + 2 nchunks, ...: the
+    // workgroups of one cache that run together read adjacent rows.
+    if (c * SUB > pos) return;
     const int nh = nkv * kGqaGroup;
     const int kv_dim = nkv * kHd;
     // Cache of one (sequence, kv head): [cap][256], head-major.
@@ -64,127 +72,148 @@ __global__ __launch_bounds__(NT, 2) void attn_decode_partial(
     __shared__ float ml_s[kGqaGroup][2];
     __shared__ float4 obuf[4][kGqaGroup][kHd / 4];
 
-    const float* cs = rope_cos + (size_t)pos * kRopeHalf;
-    const float* sn = rope_sin + (size_t)pos * kRopeHalf;
-    {
-        // q of head kvh*4 + wave; the attention scale 1/sqrt(256) is folded in.
-        const int h = kvh * kGqaGroup + wave;
-        const float* qrow = q_gate + (size_t)i * 2 * nh * kHd + (size_t)h * 2 * kHd;
-        const float4 x = *reinterpret_cast<const float4*>(qrow + 4 * lane);
-        q_s[wave][lane] = rope_norm_row(x, lane, cs, sn, q_norm, eps, 1.0f / sqrtf((float)kHd));
-    }
-    if (pos < p0 + SUB * NSUB) {
-        if (wave == 0) {
-            float4 x = *reinterpret_cast<const float4*>(knew + (size_t)i * kv_dim + kvh * kHd + 4 * lane);
-            x = rope_norm_row(x, lane, cs, sn, k_norm, eps, 1.0f);
-            knew_s[lane] = x;
-            *reinterpret_cast<float4*>(K + (size_t)pos * kHd + 4 * lane) = x;
-        } else if (wave == 1) {
-            const float4 x = *reinterpret_cast<const float4*>(vnew + (size_t)i * kv_dim + kvh * kHd + 4 * lane);
-            vnew_s[lane] = x;
-            *reinterpret_cast<float4*>(V + (size_t)pos * kHd + 4 * lane) = x;
-        }
-    }
-    __syncthreads();
-
     // Score layout: 16 teams of 16 lanes, team t scores positions t + 16m
     // (m < 4); lane l16 holds dims {4*l16 + 64*j .. +3}, j < 4.
     // P.V layout: thread holds dims 4*d4..+3 of all 4 heads, positions ps + 4m.
     const int team = tid >> 4, l16 = tid & 15;
     const int d4 = tid & 63, ps = tid >> 6;
-    float4 qr[kGqaGroup][4];
-#pragma unroll
-    for (int h = 0; h < kGqaGroup; ++h)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) qr[h][j] = q_s[h][l16 + 16 * j];
+    const bool owner = (pos / SUB) % nchunks == c;   // holds the new position
+
+    // Operands of the q / new-row preparation, loaded before the first
+    // sub-chunk's K/V so that their latency hides behind it: wave w prepares
+    // q of head 4 kvh + w; waves 0 and 1 also take the new K and V rows.
+    const int hq = kvh * kGqaGroup + wave;
+    const float4 xq = *reinterpret_cast<const float4*>(
+        q_gate + (size_t)i * 2 * nh * kHd + (size_t)hq * 2 * kHd + 4 * lane);
+    const float4 xn = *reinterpret_cast<const float4*>(
+        (wave == 1 ? vnew : knew) + (size_t)i * kv_dim + kvh * kHd + 4 * lane);
+    const float4 rc = *reinterpret_cast<const float4*>(rope_cos + (size_t)pos * kRopeHalf + 4 * (lane & 7));
+    const float4 rs = *reinterpret_cast<const float4*>(rope_sin + (size_t)pos * kRopeHalf + 4 * (lane & 7));
+    const float4 wq = *reinterpret_cast<const float4*>(q_norm + 4 * lane);
+    const float4 wk = *reinterpret_cast<const float4*>(k_norm + 4 * lane);
+
+    // K/V rows of sub-chunk `S0` into kk / vv, all loads unconditional: rows
+    // past pos read row pos instead (its scores are masked, its V rows are
+    // zeroed before P.V), and row pos itself, which this launch writes, is
+    // replaced by the new row from LDS.
+#define Q35_LOAD_SUB(S0)                                                                         \
+    {                                                                                            \
+        _Pragma("unroll") for (int m = 0; m < 4; ++m) {                                          \
+            const float4* krow = reinterpret_cast<const float4*>(                                \
+                K + (size_t)min((S0) + team + 16 * m, pos) * kHd);                               \
+            _Pragma("unroll") for (int j = 0; j < 4; ++j) kk[m][j] = krow[l16 + 16 * j];         \
+        }                                                                                        \
+        _Pragma("unroll") for (int m = 0; m < 16; ++m) {                                         \
+            const float4* vrow = reinterpret_cast<const float4*>(                                \
+                V + (size_t)min((S0) + ps + 4 * m, pos) * kHd);                                  \
+            vv[m] = vrow[d4];                                                                    \
+        }                                                                                        \
+    }
+
+    // One sub-chunk at s0 from kk / vv: scores (q re-read from LDS per head,
+    // so its 64 registers per thread are not held across the K/V loads), the
+    // online softmax (wave h owns head h, lane = position) and P.V.  Score and
+    // weight buffers alternate by sub-chunk parity PAR.
+#define Q35_SUB_BODY(PAR)                                                                        \
+    {                                                                                            \
+        const int np = min(SUB, pos + 1 - s0);                                                   \
+        if (owner) {                           /* uniform: the new K row from LDS */             \
+            _Pragma("unroll") for (int j = 0; j < 4; ++j) {                                      \
+                const float4 kn = knew_s[l16 + 16 * j];                                          \
+                _Pragma("unroll") for (int m = 0; m < 4; ++m)                                    \
+                    kk[m][j] = sel4(s0 + team + 16 * m == pos, kn, kk[m][j]);                    \
+            }                                                                                    \
+        }                                                                                        \
+        float a[4][kGqaGroup];                                                                   \
+        _Pragma("unroll") for (int h = 0; h < kGqaGroup; ++h) {                                  \
+            float4 qh[4];                                                                        \
+            _Pragma("unroll") for (int j = 0; j < 4; ++j) qh[j] = q_s[h][l16 + 16 * j];          \
+            _Pragma("unroll") for (int m = 0; m < 4; ++m) {                                      \
+                float t = 0.0f;                                                                  \
+                _Pragma("unroll") for (int j = 0; j < 4; ++j)                                    \
+                    t += qh[j].x * kk[m][j].x + qh[j].y * kk[m][j].y + qh[j].z * kk[m][j].z +    \
+                         qh[j].w * kk[m][j].w;                                                   \
+                a[m][h] = group_sum<16>(t);                                                      \
+            }                                                                                    \
+        }                                                                                        \
+        if (l16 == 0)                                                                            \
+            _Pragma("unroll") for (int m = 0; m < 4; ++m)                                        \
+                _Pragma("unroll") for (int h = 0; h < kGqaGroup; ++h)                            \
+                    sc[PAR][h][team + 16 * m] = a[m][h];                                         \
+        lds_barrier();                                                                           \
+        {                                                                                        \
+            const float s = lane < np ? sc[PAR][wave][lane] : -INFINITY;                         \
+            const float mx = fmaxf(m_run, wave_max(s));                                          \
+            const float e = lane < np ? __expf(s - mx) : 0.0f;                                   \
+            const float alpha = __expf(m_run - mx);     /* 0 on the first sub-chunk */           \
+            l_run = l_run * alpha + wave_sum(e);                                                 \
+            m_run = mx;                                                                          \
+            sc[PAR][wave][lane] = e;                                                             \
+            if (lane == 0) al_s[PAR][wave] = alpha;                                              \
+        }                                                                                        \
+        lds_barrier();                                                                           \
+        _Pragma("unroll") for (int h = 0; h < kGqaGroup; ++h) {                                  \
+            const float alpha = al_s[PAR][h];                                                    \
+            acc[h].x *= alpha; acc[h].y *= alpha; acc[h].z *= alpha; acc[h].w *= alpha;          \
+        }                                                                                        \
+        if (owner || np < SUB) {               /* uniform: rows past pos, the new V row */        \
+            const float4 vn = vnew_s[d4];                                                        \
+            _Pragma("unroll") for (int m = 0; m < 16; ++m) {                                     \
+                const int pp = ps + 4 * m;                                                       \
+                vv[m] = sel4(pp >= np, make_float4(0.f, 0.f, 0.f, 0.f),                          \
+                             sel4(s0 + pp == pos, vn, vv[m]));                                   \
+            }                                                                                    \
+        }                                                                                        \
+        _Pragma("unroll") for (int m = 0; m < 16; ++m) {                                         \
+            const int pp = ps + 4 * m;                                                           \
+            _Pragma("unroll") for (int h = 0; h < kGqaGroup; ++h) {                              \
+                const float e = sc[PAR][h][pp];                                                  \
+                acc[h].x += e * vv[m].x;                                                         \
+                acc[h].y += e * vv[m].y;                                                         \
+                acc[h].z += e * vv[m].z;                                                         \
+                acc[h].w += e * vv[m].w;                                                         \
+            }                                                                                    \
+        }                                                                                        \
+    }
 
     float m_run = -INFINITY, l_run = 0.0f;     // per head (wave = head in the softmax step)
     float4 acc[kGqaGroup];
 #pragma unroll
     for (int h = 0; h < kGqaGroup; ++h) acc[h] = make_float4(0.f, 0.f, 0.f, 0.f);
 
-    for (int sub = 0; sub < NSUB; ++sub) {
-        const int s0 = p0 + sub * SUB;
-        if (s0 > pos) break;                    // uniform across the workgroup
-        const int par = sub & 1;
-        const int np = min(SUB, pos + 1 - s0);
+    int s0 = c * SUB;
+    {
+        // The first sub-chunk's loads go out before the q preparation.
         float4 kk[4][4];
         float4 vv[16];
-#pragma unroll
-        for (int m = 0; m < 4; ++m) {
-            const int pp = team + 16 * m;
-            const int pabs = s0 + pp;
-            const bool live = pp < np && pabs != pos;
-            const float4* krow = reinterpret_cast<const float4*>(K + (size_t)(live ? pabs : 0) * kHd);
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                kk[m][j] = live ? krow[l16 + 16 * j] : make_float4(0.f, 0.f, 0.f, 0.f);
-        }
-#pragma unroll
-        for (int m = 0; m < 16; ++m) {
-            const int pp = ps + 4 * m;
-            const int pabs = s0 + pp;
-            const bool live = pp < np && pabs != pos;
-            const float4* vrow = reinterpret_cast<const float4*>(V + (size_t)(live ? pabs : 0) * kHd);
-            vv[m] = live ? vrow[d4] : make_float4(0.f, 0.f, 0.f, 0.f);
-        }
-        // The new row comes from LDS.
-#pragma unroll
-        for (int m = 0; m < 4; ++m)
-            if (s0 + team + 16 * m == pos)
-#pragma unroll
-                for (int j = 0; j < 4; ++j) kk[m][j] = knew_s[l16 + 16 * j];
-#pragma unroll
-        for (int m = 0; m < 16; ++m)
-            if (s0 + ps + 4 * m == pos) vv[m] = vnew_s[d4];
-
-#pragma unroll
-        for (int m = 0; m < 4; ++m) {
-            float a[kGqaGroup];
-#pragma unroll
-            for (int h = 0; h < kGqaGroup; ++h) {
-                float t = 0.0f;
-#pragma unroll
-                for (int j = 0; j < 4; ++j)
-                    t += qr[h][j].x * kk[m][j].x + qr[h][j].y * kk[m][j].y +
-                         qr[h][j].z * kk[m][j].z + qr[h][j].w * kk[m][j].w;
-                a[h] = group_sum<16>(t);
-            }
-            if (l16 == 0)
-#pragma unroll
-                for (int h = 0; h < kGqaGroup; ++h) sc[par][h][team + 16 * m] = a[h];
-        }
-        lds_barrier();
-        // Online softmax over the sub-chunk: wave h owns head h, lane = position.
-        {
-            const float s = lane < np ? sc[par][wave][lane] : -INFINITY;
-            const float mx = fmaxf(m_run, wave_max(s));
-            const float e = lane < np ? __expf(s - mx) : 0.0f;
-            const float alpha = __expf(m_run - mx);     // 0 on the first sub-chunk
-            l_run = l_run * alpha + wave_sum(e);
-            m_run = mx;
-            sc[par][wave][lane] = e;
-            if (lane == 0) al_s[par][wave] = alpha;
-        }
-        lds_barrier();
-#pragma unroll
-        for (int h = 0; h < kGqaGroup; ++h) {
-            const float alpha = al_s[par][h];
-            acc[h].x *= alpha; acc[h].y *= alpha; acc[h].z *= alpha; acc[h].w *= alpha;
-        }
-#pragma unroll
-        for (int m = 0; m < 16; ++m) {
-            const int pp = ps + 4 * m;
-#pragma unroll
-            for (int h = 0; h < kGqaGroup; ++h) {
-                const float e = sc[par][h][pp];
-                acc[h].x += e * vv[m].x;
-                acc[h].y += e * vv[m].y;
-                acc[h].z += e * vv[m].z;
-                acc[h].w += e * vv[m].w;
+        Q35_LOAD_SUB(s0)
+        // q rows (the attention scale 1/sqrt(256) folded in); the owner also
+        // rotates/norms the new K row and writes K and V into the cache.
+        q_s[wave][lane] = rope_norm_regs(xq, rc, rs, wq, lane, eps, 1.0f / sqrtf((float)kHd));
+        if (owner && wave < 2) {
+            float4* dst = reinterpret_cast<float4*>((wave == 0 ? K : V) + (size_t)pos * kHd) + lane;
+            if (wave == 0) {
+                const float4 x = rope_norm_regs(xn, rc, rs, wk, lane, eps, 1.0f);
+                knew_s[lane] = x;
+                *dst = x;
+            } else {
+                vnew_s[lane] = xn;
+                *dst = xn;
             }
         }
+        lds_barrier();
+        Q35_SUB_BODY(0)
     }
+    for (int sub = 1; sub < NSUB; ++sub) {
+        s0 += nchunks * SUB;
+        if (s0 > pos) break;                    // uniform across the workgroup
+        float4 kk[4][4];
+        float4 vv[16];
+        Q35_LOAD_SUB(s0)
+        Q35_SUB_BODY(sub & 1)
+    }
+#undef Q35_LOAD_SUB
+#undef Q35_SUB_BODY
 
 #pragma unroll
     for (int h = 0; h < kGqaGroup; ++h) obuf[ps][h][d4] = acc[h];
@@ -221,13 +250,12 @@ constexpr int MG = MT / MD4;               // chunk groups
 
 __global__ __launch_bounds__(MT) void attn_decode_merge(
     const float* __restrict__ part_o, const float* __restrict__ part_ml,
-    const float* __restrict__ q_gate, float* __restrict__ out, int nkv, int nchunks, int chunk,
-    SeqBatch sb) {
+    const float* __restrict__ q_gate, float* __restrict__ out, int nkv, int nchunks, SeqBatch sb) {
     const int h = blockIdx.x / (kHd / MSLICE), slice = blockIdx.x % (kHd / MSLICE);
     const int i = blockIdx.y, t = threadIdx.x;
     const int nh = nkv * kGqaGroup;
     const int kvh = h / kGqaGroup, hl = h % kGqaGroup;
-    const int nc = (sb.pos[i] + chunk) / chunk;
+    const int nc = min(nchunks, sb.pos[i] / SUB + 1);
     const size_t base = ((size_t)i * nkv + kvh) * nchunks;
     __shared__ float red[MT / kWave];
     __shared__ float4 obuf[MG][MD4];
@@ -323,7 +351,7 @@ hipError_t launch_attn_decode(q35m_ctx* c, int layer, const SeqBatch& sb, const 
     {
         ProfScope ps_(c, K_ATTN_DECODE_MERGE);
         hipExtLaunchKernelGGL(attn_decode_merge, dim3(d.nh * (kHd / MSLICE), sb.n), dim3(MT), 0, c->stream, ps_.a, ps_.b, 0, part_o,
-                           part_ml, q_gate, out, d.nkv, nchunks, chunk, sb);
+                           part_ml, q_gate, out, d.nkv, nchunks, sb);
     }
     return hipGetLastError();
 }

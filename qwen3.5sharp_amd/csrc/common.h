@@ -74,40 +74,47 @@ __device__ __forceinline__ int xcd_remap(int b, int total) {
 // the zero-centred (1+w) RMSNorm (Qwen35Ops.RmsNormZeroCentered,
 // Qwen35Ops.cs:22-66) of one 256-wide head row held as one float4 per lane of
 // a wave (lane l: dims 4l..4l+3); the result is also multiplied by post_scale.
-// cs/sn: the RoPE table row of the token's position.
-__device__ __forceinline__ float4 rope_norm_row(float4 x, int lane, const float* __restrict__ cs,
-                                                const float* __restrict__ sn,
-                                                const float* __restrict__ w, float eps,
-                                                float post_scale) {
+// The operands come in registers: c, s = the RoPE table entries 4(l%8)..+3 of
+// the token's position (used by lanes 0-15), ww = w[4l..4l+3].  No memory
+// access, so callers issue these loads together with others.
+__device__ __forceinline__ float4 rope_norm_regs(float4 x, float4 c, float4 s, float4 ww, int lane,
+                                                 float eps, float post_scale) {
     float4 p;
     p.x = __shfl_xor(x.x, 8, kWave);
     p.y = __shfl_xor(x.y, 8, kWave);
     p.z = __shfl_xor(x.z, 8, kWave);
     p.w = __shfl_xor(x.w, 8, kWave);
-    if (lane < 16) {
-        const int i0 = 4 * (lane & 7);
-        const float4 c = *reinterpret_cast<const float4*>(cs + i0);
-        const float4 s = *reinterpret_cast<const float4*>(sn + i0);
-        if (lane < 8) {   // x0' = x0 c - x1 s
-            x.x = x.x * c.x - p.x * s.x;
-            x.y = x.y * c.y - p.y * s.y;
-            x.z = x.z * c.z - p.z * s.z;
-            x.w = x.w * c.w - p.w * s.w;
-        } else {          // x1' = x0 s + x1 c
-            x.x = p.x * s.x + x.x * c.x;
-            x.y = p.y * s.y + x.y * c.y;
-            x.z = p.z * s.z + x.z * c.z;
-            x.w = p.w * s.w + x.w * c.w;
-        }
-    }
+    float4 lo, hi;      // x0' = x0 c - x1 s (lanes 0-7), x1' = x0 s + x1 c (lanes 8-15)
+    lo.x = x.x * c.x - p.x * s.x;
+    lo.y = x.y * c.y - p.y * s.y;
+    lo.z = x.z * c.z - p.z * s.z;
+    lo.w = x.w * c.w - p.w * s.w;
+    hi.x = p.x * s.x + x.x * c.x;
+    hi.y = p.y * s.y + x.y * c.y;
+    hi.z = p.z * s.z + x.z * c.z;
+    hi.w = p.w * s.w + x.w * c.w;
+    if (lane < 8) x = lo;
+    else if (lane < 16) x = hi;
     const float ss = wave_sum(x.x * x.x + x.y * x.y + x.z * x.z + x.w * x.w);
     const float scale = 1.0f / sqrtf(ss / 256.0f + eps);
-    const float4 ww = *reinterpret_cast<const float4*>(w + 4 * lane);
     x.x = x.x * scale * (1.0f + ww.x) * post_scale;
     x.y = x.y * scale * (1.0f + ww.y) * post_scale;
     x.z = x.z * scale * (1.0f + ww.z) * post_scale;
     x.w = x.w * scale * (1.0f + ww.w) * post_scale;
     return x;
+}
+
+// rope_norm_row with its operands loaded here, all at once (cs/sn: the RoPE
+// table row of the token's position).
+__device__ __forceinline__ float4 rope_norm_row(float4 x, int lane, const float* __restrict__ cs,
+                                                const float* __restrict__ sn,
+                                                const float* __restrict__ w, float eps,
+                                                float post_scale) {
+    const int i0 = 4 * (lane & 7);
+    const float4 c = *reinterpret_cast<const float4*>(cs + i0);
+    const float4 s = *reinterpret_cast<const float4*>(sn + i0);
+    const float4 ww = *reinterpret_cast<const float4*>(w + 4 * lane);
+    return rope_norm_regs(x, c, s, ww, lane, eps, post_scale);
 }
 
 }  // namespace q35
