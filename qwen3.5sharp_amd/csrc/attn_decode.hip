@@ -96,27 +96,25 @@ __global__ __launch_bounds__(NT, 2) void attn_decode_partial(
     // past pos read row pos instead (its scores are masked, its V rows are
     // zeroed before P.V), and row pos itself, which this launch writes, is
     // replaced by the new row from LDS.
-#define Q35_LOAD_SUB(S0)                                                                         \
-    {                                                                                            \
-        _Pragma("unroll") for (int m = 0; m < 4; ++m) {                                          \
-            const float4* krow = reinterpret_cast<const float4*>(                                \
-                K + (size_t)min((S0) + team + 16 * m, pos) * kHd);                               \
-            _Pragma("unroll") for (int j = 0; j < 4; ++j) kk[m][j] = krow[l16 + 16 * j];         \
-        }                                                                                        \
-        _Pragma("unroll") for (int m = 0; m < 16; ++m) {                                         \
-            const float4* vrow = reinterpret_cast<const float4*>(                                \
-                V + (size_t)min((S0) + ps + 4 * m, pos) * kHd);                                  \
-            vv[m] = vrow[d4];                                                                    \
-        }                                                                                        \
+#define Q35_LOAD_K(S0)                                                                           \
+    _Pragma("unroll") for (int m = 0; m < 4; ++m) {                                              \
+        const float4* krow = reinterpret_cast<const float4*>(                                    \
+            K + (size_t)min((S0) + team + 16 * m, pos) * kHd);                                   \
+        _Pragma("unroll") for (int j = 0; j < 4; ++j) kk[m][j] = krow[l16 + 16 * j];             \
+    }
+#define Q35_LOAD_V(S0)                                                                           \
+    _Pragma("unroll") for (int m = 0; m < 16; ++m) {                                             \
+        const float4* vrow = reinterpret_cast<const float4*>(                                    \
+            V + (size_t)min((S0) + ps + 4 * m, pos) * kHd);                                      \
+        vv[m] = vrow[d4];                                                                        \
     }
 
     // One sub-chunk at s0 from kk / vv: scores (q re-read from LDS per head,
     // so its 64 registers per thread are not held across the K/V loads), the
     // online softmax (wave h owns head h, lane = position) and P.V.  Score and
     // weight buffers alternate by sub-chunk parity PAR.
-#define Q35_SUB_BODY(PAR)                                                                        \
+#define Q35_SCORES(PAR)                                                                          \
     {                                                                                            \
-        const int np = min(SUB, pos + 1 - s0);                                                   \
         if (owner) {                           /* uniform: the new K row from LDS */             \
             _Pragma("unroll") for (int j = 0; j < 4; ++j) {                                      \
                 const float4 kn = knew_s[l16 + 16 * j];                                          \
@@ -140,6 +138,10 @@ __global__ __launch_bounds__(NT, 2) void attn_decode_partial(
             _Pragma("unroll") for (int m = 0; m < 4; ++m)                                        \
                 _Pragma("unroll") for (int h = 0; h < kGqaGroup; ++h)                            \
                     sc[PAR][h][team + 16 * m] = a[m][h];                                         \
+    }
+#define Q35_SOFTMAX_PV(PAR)                                                                      \
+    {                                                                                            \
+        const int np = min(SUB, pos + 1 - s0);                                                   \
         lds_barrier();                                                                           \
         {                                                                                        \
             const float s = lane < np ? sc[PAR][wave][lane] : -INFINITY;                         \
@@ -181,39 +183,45 @@ __global__ __launch_bounds__(NT, 2) void attn_decode_partial(
 #pragma unroll
     for (int h = 0; h < kGqaGroup; ++h) acc[h] = make_float4(0.f, 0.f, 0.f, 0.f);
 
+    // The first sub-chunk's loads go out before the q preparation.
     int s0 = c * SUB;
-    {
-        // The first sub-chunk's loads go out before the q preparation.
-        float4 kk[4][4];
-        float4 vv[16];
-        Q35_LOAD_SUB(s0)
-        // q rows (the attention scale 1/sqrt(256) folded in); the owner also
-        // rotates/norms the new K row and writes K and V into the cache.
-        q_s[wave][lane] = rope_norm_regs(xq, rc, rs, wq, lane, eps, 1.0f / sqrtf((float)kHd));
-        if (owner && wave < 2) {
-            float4* dst = reinterpret_cast<float4*>((wave == 0 ? K : V) + (size_t)pos * kHd) + lane;
-            if (wave == 0) {
-                const float4 x = rope_norm_regs(xn, rc, rs, wk, lane, eps, 1.0f);
-                knew_s[lane] = x;
-                *dst = x;
-            } else {
-                vnew_s[lane] = xn;
-                *dst = xn;
-            }
+    float4 kk[4][4];
+    float4 vv[16];
+    Q35_LOAD_K(s0)
+    Q35_LOAD_V(s0)
+    // q rows (the attention scale 1/sqrt(256) folded in); the owner also
+    // rotates/norms the new K row and writes K and V into the cache.
+    q_s[wave][lane] = rope_norm_regs(xq, rc, rs, wq, lane, eps, 1.0f / sqrtf((float)kHd));
+    if (owner && wave < 2) {
+        float4* dst = reinterpret_cast<float4*>((wave == 0 ? K : V) + (size_t)pos * kHd) + lane;
+        if (wave == 0) {
+            const float4 x = rope_norm_regs(xn, rc, rs, wk, lane, eps, 1.0f);
+            knew_s[lane] = x;
+            *dst = x;
+        } else {
+            vnew_s[lane] = xn;
+            *dst = xn;
         }
-        lds_barrier();
-        Q35_SUB_BODY(0)
     }
-    for (int sub = 1; sub < NSUB; ++sub) {
-        s0 += nchunks * SUB;
-        if (s0 > pos) break;                    // uniform across the workgroup
-        float4 kk[4][4];
-        float4 vv[16];
-        Q35_LOAD_SUB(s0)
-        Q35_SUB_BODY(sub & 1)
+    lds_barrier();
+    // Software pipeline: the next sub-chunk's K loads go out once the scores
+    // have consumed kk, its V loads once P.V has consumed vv.  After the last
+    // sub-chunk they fetch clamped rows (row pos) and are discarded.
+    for (int sub = 0;;) {
+        const int par = sub & 1;
+        Q35_SCORES(par)
+        const int s1 = s0 + nchunks * SUB;
+        Q35_LOAD_K(s1)
+        Q35_SOFTMAX_PV(par)
+        Q35_LOAD_V(s1)
+        ++sub;
+        s0 = s1;
+        if (sub == NSUB || s0 > pos) break;     // uniform across the workgroup
     }
-#undef Q35_LOAD_SUB
-#undef Q35_SUB_BODY
+#undef Q35_LOAD_K
+#undef Q35_LOAD_V
+#undef Q35_SCORES
+#undef Q35_SOFTMAX_PV
 
 #pragma unroll
     for (int h = 0; h < kGqaGroup; ++h) obuf[ps][h][d4] = acc[h];

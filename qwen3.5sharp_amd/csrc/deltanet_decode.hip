@@ -108,6 +108,10 @@ __global__ __launch_bounds__(NT) void deltanet_decode_kernel(
     const ConvOperands ov = conv_load(conv_w, win, x, v_c, conv_dim);
     const float b_in = bin[(size_t)i * nv + vh], a_in = ain[(size_t)i * nv + vh];
     const float sa = ssm_a[vh], dtb = dt_bias[vh];
+    // Operands of the gated norm at the end (threads t >= 128 load channel 127
+    // and discard it).
+    const size_t o_off = (size_t)i * value_dim + (size_t)vh * kDk + min(t, kDk - 1);
+    const float z_t = zin[o_off], nw_t = ssm_norm[min(t, kDk - 1)];
 
     // Thread owns columns 4*c4 .. +3 of rows rg + RG*j.
     float4 s[RPT];
@@ -209,8 +213,7 @@ __global__ __launch_bounds__(NT) void deltanet_decode_kernel(
     lds_barrier();
     if (t < kDk) {
         const float rs = 1.0f / sqrtf((nred[0] + nred[1]) / (float)kDk + eps);
-        const size_t off = (size_t)i * value_dim + (size_t)vh * kDk + t;
-        out[off] = ov_t * rs * ssm_norm[t] * silu(zin[off]);
+        out[o_off] = ov_t * rs * nw_t * silu(z_t);
     }
 }
 
