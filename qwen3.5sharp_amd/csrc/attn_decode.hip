@@ -248,13 +248,16 @@ __global__ __launch_bounds__(NT, 2) void attn_decode_partial(
 }
 
 // Merge of the chunk partials of one (sequence, q head, 64-dim slice): 256
-// threads; thread holds 4 dims (d4 = t % 16) of the slice and merges chunks
-// c = t / 16 (mod 16); the chunk weights exp(m_c - M) come from one shared
-// maximum M over all chunks of the head.
+// threads; thread holds 4 dims (d4 = t % 16) of the slice and folds the
+// chunks c = t / 16 (mod 16) into a running (m, l, o) by log-sum-exp
+// rescaling, MU chunks per round with all their loads issued together; the 16
+// running triples of a column are then folded the same way through LDS.  One
+// memory round trip per MU chunks (the gate is loaded up front).
 constexpr int MT = 256;
 constexpr int MSLICE = 64;                 // dims per merge workgroup
 constexpr int MD4 = MSLICE / 4;            // float4 columns per slice
 constexpr int MG = MT / MD4;               // chunk groups
+constexpr int MU = 4;                      // chunks per thread per round
 
 __global__ __launch_bounds__(MT) void attn_decode_merge(
     const float* __restrict__ part_o, const float* __restrict__ part_ml,
@@ -265,46 +268,62 @@ __global__ __launch_bounds__(MT) void attn_decode_merge(
     const int kvh = h / kGqaGroup, hl = h % kGqaGroup;
     const int nc = min(nchunks, sb.pos[i] / SUB + 1);
     const size_t base = ((size_t)i * nkv + kvh) * nchunks;
-    __shared__ float red[MT / kWave];
     __shared__ float4 obuf[MG][MD4];
-    __shared__ float lbuf[MG];
-
-    float mx = -INFINITY;
-    for (int c = t; c < nc; c += MT) mx = fmaxf(mx, part_ml[2 * ((base + c) * kGqaGroup + hl)]);
-    mx = wave_max(mx);
-    if ((t & 63) == 0) red[t >> 6] = mx;
-    __syncthreads();
-    float M = red[0];
-#pragma unroll
-    for (int w = 1; w < MT / kWave; ++w) M = fmaxf(M, red[w]);
+    __shared__ float mbuf[MG], lbuf[MG];
 
     const int d4 = t % MD4, g = t / MD4;
     const int col = slice * MD4 + d4;
+    // Gate of this thread's 4 output dims (used by threads t < MD4).
+    const int dim = slice * MSLICE + 4 * d4;
+    const float4 gt = *reinterpret_cast<const float4*>(
+        q_gate + (size_t)i * 2 * nh * kHd + (size_t)h * 2 * kHd + kHd + dim);
+
+    float m = -INFINITY, l = 0.0f;
     float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
-    float l = 0.0f;
-#pragma unroll 4
-    for (int c = g; c < nc; c += MG) {
-        const size_t pidx = (base + c) * kGqaGroup + hl;
-        const float wgt = __expf(part_ml[2 * pidx] - M);
-        const float4 oc = reinterpret_cast<const float4*>(part_o + pidx * kHd)[col];
-        l += wgt * part_ml[2 * pidx + 1];
-        o.x += wgt * oc.x; o.y += wgt * oc.y; o.z += wgt * oc.z; o.w += wgt * oc.w;
+    for (int c0 = g; c0 < nc; c0 += MG * MU) {
+        float mc[MU], lc[MU];
+        float4 oc[MU];
+#pragma unroll
+        for (int u = 0; u < MU; ++u) {
+            const size_t pidx = (base + min(c0 + u * MG, nc - 1)) * kGqaGroup + hl;
+            mc[u] = part_ml[2 * pidx];
+            lc[u] = part_ml[2 * pidx + 1];
+            oc[u] = reinterpret_cast<const float4*>(part_o + pidx * kHd)[col];
+        }
+#pragma unroll
+        for (int u = 0; u < MU; ++u) {
+            const bool valid = c0 + u * MG < nc;
+            const float mn = valid ? fmaxf(m, mc[u]) : m;
+            const float a = __expf(m - mn);             // 0 while m is -inf
+            const float b = valid ? __expf(mc[u] - mn) : 0.0f;
+            l = l * a + lc[u] * b;
+            o.x = o.x * a + oc[u].x * b;
+            o.y = o.y * a + oc[u].y * b;
+            o.z = o.z * a + oc[u].z * b;
+            o.w = o.w * a + oc[u].w * b;
+            m = mn;
+        }
     }
     obuf[g][d4] = o;
-    if (d4 == 0) lbuf[g] = l;
+    if (d4 == 0) {
+        mbuf[g] = m;
+        lbuf[g] = l;
+    }
     __syncthreads();
     if (t < MD4) {
-        float4 s = obuf[0][t];
-        float L = lbuf[0];
+        float M = mbuf[0];
 #pragma unroll
-        for (int w = 1; w < MG; ++w) {
-            s.x += obuf[w][t].x; s.y += obuf[w][t].y; s.z += obuf[w][t].z; s.w += obuf[w][t].w;
-            L += lbuf[w];
+        for (int w = 1; w < MG; ++w) M = fmaxf(M, mbuf[w]);
+        float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
+        float L = 0.0f;
+#pragma unroll
+        for (int w = 0; w < MG; ++w) {
+            const float f = __expf(mbuf[w] - M);        // 0 for groups without chunks
+            const float4 ow = obuf[w][t];
+            s.x += ow.x * f; s.y += ow.y * f; s.z += ow.z * f; s.w += ow.w * f;
+            L += lbuf[w] * f;
         }
         const float inv = 1.0f / L;
-        const int dim = slice * MSLICE + 4 * t;
-        const float4 gt = *reinterpret_cast<const float4*>(
-            q_gate + (size_t)i * 2 * nh * kHd + (size_t)h * 2 * kHd + kHd + dim);
         float4 r;
         r.x = s.x * inv * (1.0f / (1.0f + expf(-gt.x)));
         r.y = s.y * inv * (1.0f / (1.0f + expf(-gt.y)));
