@@ -51,11 +51,11 @@ DN_PREFILL_FLOP = 11_811_160_064           # T=2048, chunked WY form (32 heads x
 # Per-kernel algorithmic work of one T=2048 DeltaNet prefill (C = 64, 32 chunks,
 # 16 k-heads, 32 v-heads), as (bound, amount, description):
 DN_PREFILL_KERNELS = {
-    "dn_chunk_scan": ("mfma", 32 * 32 * 2 * (2 * 64 * DK * DK),
-                      "W S and K^T D, 2 x 2*64*128*128 FLOP per (v-head, chunk), 32 x 32"),
-    "dn_chunk_out": ("mfma", 32 * 32 * (2 * 64 * DK * DK + 10 * 2 * 16 * 16 * DK),
-                     "Q S (2*64*128*128) + the 10 causal 16x16 blocks of (M o QK^T) D "
-                     "(10 x 2*16*16*128) FLOP per (v-head, chunk), 32 x 32"),
+    "dn_chunk_scan": ("mfma", 32 * 32 * 3 * (2 * 64 * DK * DK),
+                      "W S, K^T D and Q S, 3 x 2*64*128*128 FLOP per (v-head, chunk), 32 x 32"),
+    "dn_chunk_out": ("hbm", 4 * 32 * 32 * (10 * 16 * 16 + 4 * 64 * DK),
+                     "M o QK^T causal blocks (10 x 16x16 floats), inter-chunk output, D and z "
+                     "(64x128 floats each) read, out (64x128) written, per (v-head, chunk)"),
     "dn_chunk_prep": ("mfma", 32 * 16 * 2 * 2 * 64 * 64 * DK + 32 * 32 * 2 * 2 * 64 * 64 * DK,
                       "K K^T, Q K^T (2 x 2*64*64*128 per k-head chunk) + W, U (2 x 2*64*64*128 "
                       "per v-head chunk)"),
@@ -366,8 +366,7 @@ def main():
     if want("dn_prefill"):
         log("[bench] DeltaNet prefill T=2048 ...")
         ms, kt, x = bench_dn_prefill(K, W)
-        # Per-step kernel time (the scan and output pass run in segments, the
-        # output segments on a second stream beside the scan).
+        # Per-step kernel time.
         kt = {k: (v[0] * v[1] / K, 1) for k, v in kt.items()}
         tok_s = 2048 / (ms / 1e3)
         kname, kms = dominant(kt)

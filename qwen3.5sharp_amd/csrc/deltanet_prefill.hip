@@ -36,15 +36,17 @@
 //     inverted in registers, off-diagonal blocks applied on MFMA), then
 //     W and U on MFMA.  Emits W, U, M o QK^T, gamma, e^{G_last - G}.
 //  4. dn_chunk_scan (one workgroup per v-head and 16-column tile of the
-//     state): the only sequential part.  Walks the chunks in order with the
-//     state tile in MFMA accumulators, records the entry state S and
-//     D = U - W S of every chunk, and applies
-//     S = gamma_last S + K^T (e^{G_last-G} D).  Column tiles are independent
-//     (the rule is separable over dv), so 8 workgroups per head run in
-//     parallel; the 8 tiles of a head share an XCD so W and K stay in its L2.
+//     state): the only sequential part.  Four waves walk the chunks in order
+//     with the state tile in MFMA accumulators, record D = U - W S of every
+//     chunk, and apply S = gamma_last S + K^T (e^{G_last-G} D); four more
+//     waves form the inter-chunk output diag(gamma) Q S of every chunk from
+//     the entry state the first four leave in LDS, so the states themselves
+//     never go to memory.  Column tiles are independent (the rule is
+//     separable over dv), so 8 workgroups per head run in parallel; the 8
+//     tiles of a head share an XCD so W, Q and K stay in its L2.
 //  5. dn_chunk_out (one workgroup per v-head and chunk, all in parallel):
-//     O = gamma Q S + (M o QK^T) D from the recorded S and D, with the gated
-//     RMSNorm fused into the epilogue.
+//     O = diag(gamma) Q S + (M o QK^T) D from the recorded inter-chunk output
+//     and D, with the gated RMSNorm fused into the epilogue.
 //
 // MFMA: v_mfma_f32_16x16x4f32.  Lane l = 16g + c holds A[c][g] and B[g][c];
 // D register r holds D[4g + r][c].  A 16-deep product is 4 instructions; in
@@ -99,13 +101,13 @@ struct PrefillWork {
     float* gl;     // [T][nv]   g (log decay)
     float* gam;    // [nv][nch][64]   e^{G_i}
     float* gdec;   // [nv][nch][64]   e^{G_last - G_i}
-    float* sh;     // [nv][nch][8 rb][8 cb][64][4] D layout: state on entry to each chunk
+    float* oi;     // [nv][nch] chunk blocks, D layout: diag(gamma) Q S of each chunk
     float* dh;     // [nv][nch] chunk blocks, D layout: D = U - W S of each chunk
 };
 
 size_t work_floats(const Dims& d, int T, int nch) {
-    return (size_t)nch * CB * (3 * d.nk + 4 * d.nv) + (size_t)d.nv * nch * (CH * CH + 2 * CH) +
-           (size_t)T * 2 * d.nv + (size_t)d.nv * nch * kDk * kDk;
+    return (size_t)nch * CB * (3 * d.nk + 5 * d.nv) + (size_t)d.nv * nch * (CH * CH + 2 * CH) +
+           (size_t)T * 2 * d.nv;
 }
 
 PrefillWork carve(float* w, const Dims& d, int T, int nch) {
@@ -122,8 +124,8 @@ PrefillWork carve(float* w, const Dims& d, int T, int nch) {
     p.gl = p.beta + (size_t)T * d.nv;
     p.gam = p.gl + (size_t)T * d.nv;
     p.gdec = p.gam + (size_t)d.nv * nch * CH;
-    p.sh = p.gdec + (size_t)d.nv * nch * CH;
-    p.dh = p.sh + (size_t)d.nv * nch * kDk * kDk;
+    p.oi = p.gdec + (size_t)d.nv * nch * CH;
+    p.dh = p.oi + vblk;
     return p;
 }
 
@@ -487,6 +489,12 @@ struct ScanOps {
     float glast;                 // gamma_last
 };
 
+// Operands of diag(gamma) Q S for one token block of one chunk.
+struct QsOps {
+    float4 qa[8];                // Q^ blocks (tb, kb = 0..7), A layout
+    float4 gm;                   // gamma of the block's rows 4g .. 4g+3
+};
+
 __device__ __forceinline__ void load_scan_ops(const PrefillWork& w, ScanOps& o, int n, int vh,
                                               int kh, int tl, int nch, int wave, int g,
                                               int lane) {
@@ -508,46 +516,97 @@ __device__ __forceinline__ void load_scan_ops(const PrefillWork& w, ScanOps& o, 
     o.glast = w.gam[cidx * CH + CH - 1];
 }
 
+__device__ __forceinline__ void load_qs_ops(const PrefillWork& w, QsOps& o, int n, int vh, int kh,
+                                            int nch, int tb, int g, int lane) {
+    const size_t cidx = (size_t)vh * nch + n, kidx = (size_t)kh * nch + n;
+    const float* qA = w.qa + kidx * CB;
+#pragma unroll
+    for (int kb = 0; kb < 8; ++kb) o.qa[kb] = *blk4(qA, tb, kb, lane);
+    o.gm = *reinterpret_cast<const float4*>(w.gam + cidx * CH + 16 * tb + 4 * g);
+}
+
 __device__ __forceinline__ f32x4 v4(float4 a) { return f32x4{a.x, a.y, a.z, a.w}; }
 
-// The sequential part: one workgroup per (v-head, 16-column tile); wave w owns
-// state rows 32w..32w+31 of the tile (two D-layout 16x16 tiles, kept in MFMA
-// accumulators across chunks).  Per chunk it records the entry state S and
-// D = U - W S for dn_chunk_out, then S = gamma_last S + K^T (e^{G_last-G} D).
-// Column tiles are independent (the rule is separable over dv), so 8
-// workgroups per head run in parallel, on one XCD so W and K stay in its L2.
-__global__ __launch_bounds__(256) void dn_chunk_scan(PrefillWork w, float* __restrict__ state,
+// The sequential part: one workgroup per (v-head, 16-column tile).  Waves 0-3
+// run the chain: wave w owns state rows 32w..32w+31 of the tile (two D-layout
+// 16x16 tiles, kept in MFMA accumulators across chunks); per chunk they write
+// D = U - W S for dn_chunk_out and apply S = gamma_last S + K^T (e^{G_last-G}
+// D).  Waves 4-7 (one per token block, lower issue priority) form the
+// inter-chunk output diag(gamma) Q S of each chunk from the entry state the
+// chain waves leave in LDS; their products fill the matrix pipe while the
+// chain waits on LDS and barriers.  Both kinds of wave pass the same two
+// barriers per chunk.  Column tiles are independent (the rule is separable
+// over dv), so 8 workgroups per head run in parallel, on one XCD so W, Q and
+// K stay in its L2.
+__global__ __launch_bounds__(512) void dn_chunk_scan(PrefillWork w, float* __restrict__ state,
                                                      int nk, int nv, int nch) {
     const int L = xcd_remap(blockIdx.x, gridDim.x);
     const int vh = L / 8, tl = L % 8;
     const int kh = vh / (nv / nk);
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 4, c16 = lane & 15;
+
+    // Per-wave partials of W S and the decayed D blocks, and the entry state
+    // of the chunk ([kb][lane], D layout), double-buffered by chunk parity.
+    __shared__ f32x4 red[2][4][4][64];
+    __shared__ f32x4 dg[2][4][64];
+    __shared__ f32x4 sbuf[2][8][64];
+
+    if (wave >= 4) {
+        // Inter-chunk output of token block q.  The entry state of chunk n is
+        // read between the chunk's two barriers (the chain rewrites that
+        // buffer only after the next chunk's second barrier); half of the
+        // products run before the second barrier, half after it.
+        __builtin_amdgcn_s_setprio(0);
+        const int q = wave - 4;
+        QsOps a0, a1;
+        load_qs_ops(w, a0, 0, vh, kh, nch, q, g, lane);
+        auto qs_chunk = [&](const QsOps& cur, QsOps& nxt, int n) {
+            const int par = n & 1;
+            load_qs_ops(w, nxt, min(n + 1, nch - 1), vh, kh, nch, q, g, lane);
+            lds_barrier();
+            f32x4 Sk[8];
+#pragma unroll
+            for (int kb = 0; kb < 8; ++kb) Sk[kb] = sbuf[par][kb][lane];
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb) acc = mfma16x4(cur.qa[kb], Sk[kb], acc);
+            __builtin_amdgcn_sched_barrier(0);
+            lds_barrier();
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int kb = 4; kb < 8; ++kb) acc = mfma16x4(cur.qa[kb], Sk[kb], acc);
+            *reinterpret_cast<f32x4*>(w.oi + ((size_t)vh * nch + n) * CB +
+                                      (size_t)((q * 8 + tl) * 64 + lane) * 4) = acc * v4(cur.gm);
+        };
+        const int npair = nch / 2;
+        for (int it = 0; it < npair; ++it) {
+            qs_chunk(a0, a1, 2 * it);
+            qs_chunk(a1, a0, 2 * it + 1);
+        }
+        if (2 * npair < nch) qs_chunk(a0, a1, nch - 1);
+        return;
+    }
+
+    __builtin_amdgcn_s_setprio(2);
     const int col = 16 * tl + c16;
     float* S = state + (size_t)vh * kDk * kDk;
-
     f32x4 Sb[2];
 #pragma unroll
     for (int b = 0; b < 2; ++b)
 #pragma unroll
         for (int r = 0; r < 4; ++r) Sb[b][r] = S[(size_t)(32 * wave + 16 * b + 4 * g + r) * kDk + col];
 
-    // Partials of W S per wave and the decayed D blocks, double-buffered by
-    // chunk parity.
-    __shared__ f32x4 red[2][4][4][64];
-    __shared__ f32x4 dg[2][4][64];
-
-    // One chunk: record S and D, then the state update.  The operands of
-    // chunk `pf` (two ahead; clamped, so the last chunks reload the final one)
-    // are loaded into `nxt`, their 18 loads interleaved with the 32 MFMAs of
-    // W S so the memory pipe runs beside the matrix pipe.
+    // One chunk: the entry state to LDS, D, then the state update.  The
+    // operands of chunk `pf` (the next; clamped, so the last chunk reloads
+    // itself) are loaded into `nxt`, their 18 loads interleaved with the 32
+    // MFMAs of W S so the memory pipe runs beside the matrix pipe.
     auto chunk = [&](const ScanOps& cur, ScanOps& nxt, int n, int pf) {
         const int par = n & 1;
         const size_t cidx = (size_t)vh * nch + n;
-        float* sh = w.sh + cidx * kDk * kDk;
 #pragma unroll
-        for (int b = 0; b < 2; ++b)
-            *reinterpret_cast<f32x4*>(sh + (size_t)(((2 * wave + b) * 8 + tl) * 64 + lane) * 4) = Sb[b];
+        for (int b = 0; b < 2; ++b) sbuf[par][2 * wave + b][lane] = Sb[b];
         load_scan_ops(w, nxt, min(pf, nch - 1), vh, kh, tl, nch, wave, g, lane);
         // Partial W S over this wave's 32 state rows, all 4 token blocks.
 #pragma unroll
@@ -588,22 +647,15 @@ __global__ __launch_bounds__(256) void dn_chunk_scan(PrefillWork w, float* __res
             Sb[b] = acc;
         }
     };
-    // Operands run two chunks ahead (they come from other XCDs' writes, so
-    // mostly from HBM): three register sets in rotation, no copies.
-    ScanOps o0, o1, o2;
+    // Operands run one chunk ahead: two register sets in rotation, no copies.
+    ScanOps o0, o1;
     load_scan_ops(w, o0, 0, vh, kh, tl, nch, wave, g, lane);
-    load_scan_ops(w, o1, min(1, nch - 1), vh, kh, tl, nch, wave, g, lane);
-    // Whole triples in a branch-free body, then the 0-2 remaining chunks.
-    const int ntrip = nch / 3;
-    for (int it = 0; it < ntrip; ++it) {
-        const int n = 3 * it;
-        chunk(o0, o2, n, n + 2);
-        chunk(o1, o0, n + 1, n + 3);
-        chunk(o2, o1, n + 2, n + 4);
+    const int npair = nch / 2;
+    for (int it = 0; it < npair; ++it) {
+        chunk(o0, o1, 2 * it, 2 * it + 1);
+        chunk(o1, o0, 2 * it + 1, 2 * it + 2);
     }
-    const int nt = 3 * ntrip;
-    if (nt < nch) chunk(o0, o2, nt, nt + 2);
-    if (nt + 1 < nch) chunk(o1, o0, nt + 1, nt + 3);
+    if (2 * npair < nch) chunk(o0, o1, nch - 1, nch);
 #pragma unroll
     for (int b = 0; b < 2; ++b)
 #pragma unroll
@@ -612,13 +664,12 @@ __global__ __launch_bounds__(256) void dn_chunk_scan(PrefillWork w, float* __res
 
 // Chunk outputs, in parallel over (v-head, chunk), with the gated RMSNorm
 // (Qwen35Ops.GatedRmsNorm, Qwen35Ops.cs:74-111) fused:
-//   O = diag(gamma) Q S + (M o Q K^T) D,  out = O * rms(O)^-1 * w * SiLU(z).
-// Wave w computes column tiles 2w, 2w+1 of all 4 token blocks: its S columns
-// (16 KiB) and D columns stay in registers.  The A operands shared by the 4
-// waves -- gamma-scaled Q (32 KiB) and the 10 causal blocks of M o QK^T --
-// are loaded once per workgroup into LDS.  O goes row-major through LDS (in
-// the space Q used), so the RMS of a row is a 32-lane reduction and z and out
-// move as coalesced float4 rows.
+//   O = diag(gamma) Q S + (M o Q K^T) D,  out = O * rms(O)^-1 * w * SiLU(z),
+// where diag(gamma) Q S comes from dn_chunk_scan.  Wave w computes column
+// tiles 2w, 2w+1 of all 4 token blocks: the inter-chunk output and D columns
+// stay in registers; the 10 causal blocks of M o QK^T (shared by the 4 waves)
+// are staged in LDS.  O goes row-major through LDS, so the RMS of a row is a
+// 32-lane reduction and z and out move as coalesced float4 rows.
 __global__ __launch_bounds__(256, 3) void dn_chunk_out(PrefillWork w, const float* __restrict__ z,
                                                     const float* __restrict__ wnorm,
                                                     float* __restrict__ out, int T, int nk,
@@ -627,33 +678,24 @@ __global__ __launch_bounds__(256, 3) void dn_chunk_out(PrefillWork w, const floa
     // v-heads vary fastest, so the z rows and output rows in flight are whole
     // token rows (16 KiB) rather than one 512-byte column of many rows.
     const int vh = L % nv, n = L / nv;
-    const int kh = vh / (nv / nk);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int g = lane >> 4, c16 = lane & 15;
-    const size_t cidx = (size_t)vh * nch + n, kidx = (size_t)kh * nch + n;
-    const float* sh = w.sh + cidx * kDk * kDk;
+    const size_t cidx = (size_t)vh * nch + n;
+    const float* oD = w.oi + cidx * CB;
     const float* dD = w.dh + cidx * CB;
-    const float4* qA = reinterpret_cast<const float4*>(w.qa + kidx * CB);
     const float4* aq = reinterpret_cast<const float4*>(w.aqk + cidx * CH * CH);
-    const float* gm = w.gam + cidx * CH;
 
-    // q_s: [tb][kb] A-layout blocks of gamma Q; reused as o_s, the row-major
-    // output tile [64][128 + 4], once every wave is past its last Q read.
-    __shared__ float4 qo_s[CH * (kDk + 4) / 4];
+    __shared__ float o_s[CH][kDk + 4];    // row-major output tile
     __shared__ float4 a_s[10][64];        // causal blocks (tb, j <= tb) of M o QK^T
-    float4 (*q_s)[64] = reinterpret_cast<float4 (*)[64]>(qo_s);
-    float (*o_s)[kDk + 4] = reinterpret_cast<float (*)[kDk + 4]>(qo_s);
 
-    // Load order: Q and M o QK^T first (staged into LDS), then S and D, whose
-    // blocks the MFMAs consume in arrival order (kb outer), so the products
-    // start while most of S is still in flight.
+    // Load order: M o QK^T first (staged into LDS), then the inter-chunk
+    // output and D, then z for the epilogue.
+    const int t0 = n * CH;
+    // A thread's columns are the same in every row it handles (4 (tid % 32)).
+    const float4 wn = reinterpret_cast<const float4*>(wnorm)[tid & 31];
+    float4 zr[8];
     f32x4 O[4][2];
     {
-        // Q: 2048 float4, 8 per thread; block = o4 / 64 = tb * 8 + kb, and the
-        // lane's row within the block is its c16 (A layout).
-        float4 qv[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i) qv[i] = qA[tid + 256 * i];
         // M o QK^T: the 640 float4 of the causal blocks, up to 3 per thread.
         auto aload = [&](int i) {
             const int o4 = min(tid + 256 * i, 10 * 64 - 1);
@@ -662,28 +704,26 @@ __global__ __launch_bounds__(256, 3) void dn_chunk_out(PrefillWork w, const floa
             return aq[(tb * 4 + j) * 64 + (o4 & 63)];
         };
         const float4 av0 = aload(0), av1 = aload(1), av2 = aload(2);
-        float grr[8];
+        __builtin_amdgcn_sched_barrier(0);     // keep the loads above ahead of the rest
 #pragma unroll
-        for (int i = 0; i < 8; ++i) grr[i] = gm[16 * ((tid + 256 * i) >> 9) + (tid & 15)];
-        __builtin_amdgcn_sched_barrier(0);     // keep the loads above ahead of S and D
-        f32x4 Sc[8][2];           // S[16 kb .. +15][16 (2w + cc) .. +15], D layout
+        for (int tb = 0; tb < 4; ++tb)
 #pragma unroll
-        for (int kb = 0; kb < 8; ++kb)
-#pragma unroll
-            for (int cc = 0; cc < 2; ++cc) Sc[kb][cc] = v4(*blk4(sh, kb, 2 * wave + cc, lane));
-        f32x4 Dc[4][2];           // D[16 tb .. +15][same columns]
+            for (int cc = 0; cc < 2; ++cc) O[tb][cc] = v4(*blk4(oD, tb, 2 * wave + cc, lane));
+        f32x4 Dc[4][2];           // D[16 tb .. +15][16 (2w + cc) .. +15], D layout
 #pragma unroll
         for (int tb = 0; tb < 4; ++tb)
 #pragma unroll
             for (int cc = 0; cc < 2; ++cc) Dc[tb][cc] = v4(*blk4(dD, tb, 2 * wave + cc, lane));
+        // z rows of this (chunk, v-head): float4 o4 = tid + 256 i is row
+        // o4 / 32, columns 4 (o4 % 32) ..; rows past T read row T - 1 and are
+        // not stored.
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            const int o4 = tid + 256 * i;
-            const float gr = grr[i];
-            q_s[o4 >> 6][o4 & 63] = make_float4(qv[i].x * gr, qv[i].y * gr, qv[i].z * gr, qv[i].w * gr);
+            const int o4 = tid + 256 * i, t = min(t0 + (o4 >> 5), T - 1);
+            zr[i] = reinterpret_cast<const float4*>(z + ((size_t)t * nv + vh) * kDk)[o4 & 31];
         }
         // Threads past the 640 float4 rewrite the last one with the same value
-        // (an unconditional store keeps these loads ahead of S and D).
+        // (an unconditional store keeps these loads ahead of the others).
         a_s[tid >> 6][tid & 63] = av0;
         a_s[(tid + 256) >> 6][tid & 63] = av1;
         {
@@ -691,19 +731,6 @@ __global__ __launch_bounds__(256, 3) void dn_chunk_out(PrefillWork w, const floa
             a_s[o4 >> 6][o4 & 63] = av2;
         }
         lds_barrier();
-
-#pragma unroll
-        for (int tb = 0; tb < 4; ++tb)
-#pragma unroll
-            for (int cc = 0; cc < 2; ++cc) O[tb][cc] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int kb = 0; kb < 8; ++kb)
-#pragma unroll
-            for (int tb = 0; tb < 4; ++tb) {
-                const float4 q = q_s[tb * 8 + kb][lane];
-                O[tb][0] = mfma16x4(q, Sc[kb][0], O[tb][0]);
-                O[tb][1] = mfma16x4(q, Sc[kb][1], O[tb][1]);
-            }
 #pragma unroll
         for (int j = 0; j < 4; ++j)
 #pragma unroll
@@ -713,18 +740,6 @@ __global__ __launch_bounds__(256, 3) void dn_chunk_out(PrefillWork w, const floa
                 O[tb][1] = mfma16x4(a, Dc[j][1], O[tb][1]);
             }
     }
-    // z rows of this (chunk, v-head): float4 o4 = tid + 256 i is row o4 / 32,
-    // columns 4 (o4 % 32) ..; rows past T read row T - 1 and are not stored.
-    const int t0 = n * CH;
-    // A thread's columns are the same in every row it handles (4 (tid % 32)).
-    const float4 wn = reinterpret_cast<const float4*>(wnorm)[tid & 31];
-    float4 zr[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const int o4 = tid + 256 * i, t = min(t0 + (o4 >> 5), T - 1);
-        zr[i] = reinterpret_cast<const float4*>(z + ((size_t)t * nv + vh) * kDk)[o4 & 31];
-    }
-    lds_barrier();
 #pragma unroll
     for (int tb = 0; tb < 4; ++tb)
 #pragma unroll
@@ -788,7 +803,7 @@ hipError_t launch_deltanet_prefill(q35m_ctx* c, int layer, int seq, int T, const
     if ((e = hipGetLastError()) != hipSuccess) return e;
     {
         ProfScope ps_(c, K_DN_CHUNK_SCAN);
-        hipExtLaunchKernelGGL(dn_chunk_scan, dim3(d.nv * 8), dim3(256), 0, c->stream, ps_.a, ps_.b, 0, w, state, d.nk,
+        hipExtLaunchKernelGGL(dn_chunk_scan, dim3(d.nv * 8), dim3(512), 0, c->stream, ps_.a, ps_.b, 0, w, state, d.nk,
                            d.nv, nch);
     }
     if ((e = hipGetLastError()) != hipSuccess) return e;
