@@ -60,8 +60,8 @@ DN_PREFILL_KERNELS = {
                       "K K^T, Q K^T (2 x 2*64*64*128 per k-head chunk) + W, U (2 x 2*64*64*128 "
                       "per v-head chunk)"),
     "deltanet_prefill_prep": ("hbm", 4 * (2048 * CONV_DIM + 2 * 2048 * NV) +
-                              4 * (3 * 2048 * NK * DK + 2048 * NV * DK + 2 * 2048 * NV),
-                              "qkv, b, a read once; q, k (two layouts), v chunk blocks and "
+                              4 * (2 * 2048 * NK * DK + 2048 * NV * DK + 2 * 2048 * NV),
+                              "qkv, b, a read once; q, k, v chunk blocks and "
                               "beta, g written once"),
 }
 ATTN_PREFILL_FLOP = 4 * HD * NH * 2048 * 2049 // 2

@@ -91,7 +91,6 @@ __device__ __forceinline__ const float4* blk4(const float* base, int tb, int kb,
 
 struct PrefillWork {
     float* qa;     // [nk][nch] chunk blocks, A layout: q^ (L2-normed, / sqrt(dk))
-    float* ka;     // [nk][nch] A layout: k^
     float* kt;     // [nk][nch] D layout: k^
     float* vd;     // [nv][nch] D layout: v
     float* wa;     // [nv][nch] A layout: W
@@ -106,7 +105,7 @@ struct PrefillWork {
 };
 
 size_t work_floats(const Dims& d, int T, int nch) {
-    return (size_t)nch * CB * (3 * d.nk + 5 * d.nv) + (size_t)d.nv * nch * (CH * CH + 2 * CH) +
+    return (size_t)nch * CB * (2 * d.nk + 5 * d.nv) + (size_t)d.nv * nch * (CH * CH + 2 * CH) +
            (size_t)T * 2 * d.nv;
 }
 
@@ -114,8 +113,7 @@ PrefillWork carve(float* w, const Dims& d, int T, int nch) {
     PrefillWork p;
     const size_t kblk = (size_t)d.nk * nch * CB, vblk = (size_t)d.nv * nch * CB;
     p.qa = w;
-    p.ka = p.qa + kblk;
-    p.kt = p.ka + kblk;
+    p.kt = p.qa + kblk;
     p.vd = p.kt + kblk;
     p.wa = p.vd + vblk;
     p.ud = p.wa + vblk;
@@ -230,7 +228,6 @@ __global__ __launch_bounds__(kDk) void deltanet_prefill_prep(
         if (hb < nk) {
             reinterpret_cast<float4*>(w.qa + gbase)[o4] = av;
         } else if (hb < 2 * nk) {
-            reinterpret_cast<float4*>(w.ka + gbase)[o4] = av;
             reinterpret_cast<float4*>(w.kt + gbase)[o4] = dv;
         } else {
             reinterpret_cast<float4*>(w.vd + gbase)[o4] = dv;
@@ -301,6 +298,7 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep(PrefillWork w, int T, in
     __shared__ double Gd[CH];
     __shared__ float bet[CH], gam[CH];
     __shared__ float pre_b[kMaxVPerK][CH], pre_g[kMaxVPerK][CH];
+    __shared__ float Ks[CH][kDk + 4];  // k^ of the chunk, row-major
 
     // beta and g of the R v-heads, fetched up front (thread = (v-head, token)).
     if (tid < R * CH) {
@@ -310,25 +308,46 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep(PrefillWork w, int T, in
         pre_g[rr][j] = w.gl[(size_t)t * nv + kh * R + rr];
     }
 
-    const float* kA = w.ka + ((size_t)kh * nch + n) * CB;
     const float* qA = w.qa + ((size_t)kh * nch + n) * CB;
     const float* kD = w.kt + ((size_t)kh * nch + n) * CB;
 
+    // k^ arrives in the D layout only (the scan's K^T D operand); its rows,
+    // the A operands of K K^T and Q K^T, are read from a row-major LDS copy.
+    // Float4 o4 = (tb * 8 + kb) * 64 + lane holds rows 16 tb + 4 g + s,
+    // column 16 kb + c.
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int o4 = tid + 256 * i, bk = o4 >> 6, ln = o4 & 63;
+        const int r0 = 16 * (bk >> 3) + 4 * (ln >> 4), c0 = 16 * (bk & 7) + (ln & 15);
+        const float4 v = reinterpret_cast<const float4*>(kD)[o4];
+        Ks[r0][c0] = v.x;
+        Ks[r0 + 1][c0] = v.y;
+        Ks[r0 + 2][c0] = v.z;
+        Ks[r0 + 3][c0] = v.w;
+    }
+    __syncthreads();
+
     // Block bi: bi < 10 -> K K^T block (rb, cb), rows 16rb + 4g + r, cols 16cb + c;
     //           bi >= 10 -> (Q K^T)^T block: D rows = keys 16cb + 4g + r, cols = queries 16rb + c.
-    // The 16 operand loads of block m + 1 are in flight while block m's 32
-    // MFMAs run.
+    // The Q operand loads of block m + 1 are in flight while block m's 32
+    // MFMAs run; the K operands come from LDS.
     f32x4 blk[5];
     float4 oa[2][8], ob[2][8];
     auto load_blk = [&](int m, float4 (&a)[8], float4 (&b)[8]) {
         const int bi = wave + 4 * m;
         const int mat = bi / 10, rb = kTriRb[bi % 10], cb = kTriCb[bi % 10];
-        const float* pa = kA + (size_t)(mat ? cb : rb) * 8 * 256;
-        const float* pb = (mat ? qA : kA) + (size_t)(mat ? rb : cb) * 8 * 256;
+        const int ra = mat ? cb : rb;
 #pragma unroll
-        for (int q = 0; q < kDk / 16; ++q) {
-            a[q] = *blk4(pa, 0, q, lane);
-            b[q] = *blk4(pb, 0, q, lane);
+        for (int q = 0; q < kDk / 16; ++q)
+            a[q] = *reinterpret_cast<const float4*>(&Ks[16 * ra + c16][16 * q + 4 * g]);
+        if (mat) {
+            const float* pb = qA + (size_t)rb * 8 * 256;
+#pragma unroll
+            for (int q = 0; q < kDk / 16; ++q) b[q] = *blk4(pb, 0, q, lane);
+        } else {
+#pragma unroll
+            for (int q = 0; q < kDk / 16; ++q)
+                b[q] = *reinterpret_cast<const float4*>(&Ks[16 * cb + c16][16 * q + 4 * g]);
         }
     };
     load_blk(0, oa[0], ob[0]);
