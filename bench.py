@@ -58,11 +58,7 @@ DN_PREFILL_KERNELS = {
                      "(64x128 floats each) read, out (64x128) written, per (v-head, chunk)"),
     "dn_chunk_prep": ("mfma", 32 * 16 * 2 * 2 * 64 * 64 * DK + 32 * 32 * 2 * 2 * 64 * 64 * DK,
                       "K K^T, Q K^T (2 x 2*64*64*128 per k-head chunk) + W, U (2 x 2*64*64*128 "
-                      "per v-head chunk)"),
-    "deltanet_prefill_prep": ("hbm", 4 * (2048 * CONV_DIM + 2 * 2048 * NV) +
-                              4 * (2 * 2048 * NK * DK + 2048 * NV * DK + 2 * 2048 * NV),
-                              "qkv, b, a read once; q, k, v chunk blocks and "
-                              "beta, g written once"),
+                      "per v-head chunk); also the conv, gates and norms of the inputs"),
 }
 ATTN_PREFILL_FLOP = 4 * HD * NH * 2048 * 2049 // 2
 PROFILES = os.path.join(ROOT, "profiles")

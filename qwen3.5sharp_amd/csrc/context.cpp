@@ -131,10 +131,9 @@ namespace q35 {
 
 const char* kernel_name(int id) {
     static const char* names[K_COUNT] = {
-        "deltanet_decode_kernel", "deltanet_prefill_prep", "deltanet_conv_writeback",
-        "dn_chunk_prep",          "dn_chunk_scan",         "dn_chunk_out",
-        "attn_decode_partial",    "attn_decode_merge",     "attn_prefill_prep",
-        "attn_prefill_flash"};
+        "deltanet_decode_kernel", "deltanet_conv_writeback", "dn_chunk_prep",
+        "dn_chunk_scan",          "dn_chunk_out",            "attn_decode_partial",
+        "attn_decode_merge",      "attn_prefill_prep",       "attn_prefill_flash"};
     return (id >= 0 && id < K_COUNT) ? names[id] : nullptr;
 }
 

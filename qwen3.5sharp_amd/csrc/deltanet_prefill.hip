@@ -96,8 +96,6 @@ struct PrefillWork {
     float* wa;     // [nv][nch] A layout: W
     float* ud;     // [nv][nch] D layout: U
     float* aqk;    // [nv][nch][4 rb][4 cb][64][4]: lane (g,c) holds (M o QK^T)[16rb+c][16cb+4g+s]
-    float* beta;   // [T][nv]
-    float* gl;     // [T][nv]   g (log decay)
     float* gam;    // [nv][nch][64]   e^{G_i}
     float* gdec;   // [nv][nch][64]   e^{G_last - G_i}
     float* oi;     // [nv][nch] chunk blocks, D layout: diag(gamma) Q S of each chunk
@@ -105,8 +103,7 @@ struct PrefillWork {
 };
 
 size_t work_floats(const Dims& d, int T, int nch) {
-    return (size_t)nch * CB * (2 * d.nk + 5 * d.nv) + (size_t)d.nv * nch * (CH * CH + 2 * CH) +
-           (size_t)T * 2 * d.nv;
+    return (size_t)nch * CB * (2 * d.nk + 5 * d.nv) + (size_t)d.nv * nch * (CH * CH + 2 * CH);
 }
 
 PrefillWork carve(float* w, const Dims& d, int T, int nch) {
@@ -118,126 +115,63 @@ PrefillWork carve(float* w, const Dims& d, int T, int nch) {
     p.wa = p.vd + vblk;
     p.ud = p.wa + vblk;
     p.aqk = p.ud + vblk;
-    p.beta = p.aqk + (size_t)d.nv * nch * CH * CH;
-    p.gl = p.beta + (size_t)T * d.nv;
-    p.gam = p.gl + (size_t)T * d.nv;
+    p.gam = p.aqk + (size_t)d.nv * nch * CH * CH;
     p.gdec = p.gam + (size_t)d.nv * nch * CH;
     p.oi = p.gdec + (size_t)d.nv * nch * CH;
     p.dh = p.oi + vblk;
     return p;
 }
 
-// One workgroup per (16-token group, head block); a thread owns one channel
-// and slides the 4-tap window over the 16 tokens, so each qkv element is read
-// once.  Head blocks 0..nk-1 are q heads, nk..2nk-1 k heads, then v heads.
-// Groups past T (up to the end of the last chunk) write zeros.  The group's
-// 16 x 128 outputs are transposed through LDS and written as contiguous
-// 8 KiB runs of the chunk-block layouts.
-constexpr int PT = 16;
-
-__global__ __launch_bounds__(kDk) void deltanet_prefill_prep(
-    const float* __restrict__ qkv, const float* __restrict__ bin, const float* __restrict__ ain,
-    const float* __restrict__ conv_w, const float* __restrict__ ssm_a,
-    const float* __restrict__ dt_bias, PrefillWork w, float* __restrict__ cs, int T, int nk,
-    int nv, int nch, float eps) {
-    // Head blocks vary fastest over the launch, so the workgroups in flight
-    // read whole 32 KiB token rows of qkv rather than one 512-byte column of
-    // many rows (which would fall on few HBM channels).
-    const int hb = blockIdx.x, tg = blockIdx.y, tid = threadIdx.x;
-    const int t0 = tg * PT, n = tg >> 2, tb = tg & 3;
-    const int key_dim = nk * kDk, conv_dim = 2 * key_dim + nv * kDk;
-    int c;
-    if (hb < nk) c = hb * kDk + tid;
-    else if (hb < 2 * nk) c = key_dim + (hb - nk) * kDk + tid;
-    else c = 2 * key_dim + (hb - 2 * nk) * kDk + tid;
-    const float w0 = conv_w[c], w1 = conv_w[conv_dim + c], w2 = conv_w[2 * conv_dim + c],
-                w3 = conv_w[3 * conv_dim + c];
-    // All 19 loads issue back to back from clamped rows; the zero padding is a
-    // multiply by 0/1 (a select on the uniform row test would become a branch
-    // around each load and serialise them).
-    float x[PT + 3];
+// SiLU of the zero-padded causal conv of channel c (prefill tap order: tap j
+// multiplies x[t - j], GatedDeltaNetOps.cs:27-53) over the N tokens from
+// `ts`; tokens at or past T give 0.  conv_load issues the N + 3 raw-input
+// loads unconditionally from clamped rows (a select on the row test would
+// become a branch around each load and serialise them), so callers can put
+// them in flight early; conv_finish applies the zero padding as a multiply by
+// 0/1 and the taps.  Each qkv element is read once per range.  For T >= 3 the
+// range that holds token T - 1 also writes the conv window <- the last K - 1
+// raw inputs (Prefill.cs:192-204).
+template <int N>
+__device__ __forceinline__ void conv_load(const float* __restrict__ qkv, int c, int conv_dim,
+                                          int T, int ts, float (&x)[N + 3]) {
 #pragma unroll
-    for (int j = 0; j < PT + 3; ++j) {
-        const int t = t0 - 3 + j;
+    for (int j = 0; j < N + 3; ++j) {
+        const int t = ts - 3 + j;
         x[j] = qkv[(size_t)min(max(t, 0), T - 1) * conv_dim + c];
     }
+}
+
+template <int N>
+__device__ __forceinline__ void conv_finish(const float* __restrict__ conv_w,
+                                            float* __restrict__ cs, int c, int conv_dim, int T,
+                                            int ts, float (&x)[N + 3], float (&y)[N]) {
+    const float w0 = conv_w[c], w1 = conv_w[conv_dim + c], w2 = conv_w[2 * conv_dim + c],
+                w3 = conv_w[3 * conv_dim + c];
+    if (ts < 3 || ts + N > T) {          // edge ranges only (uniform per wave)
 #pragma unroll
-    for (int j = 0; j < PT + 3; ++j) {
-        const int t = t0 - 3 + j;
-        x[j] *= (t >= 0 && t < T) ? 1.0f : 0.0f;
+        for (int j = 0; j < N + 3; ++j) {
+            const int t = ts - 3 + j;
+            x[j] *= (t >= 0 && t < T) ? 1.0f : 0.0f;
+        }
     }
-    // Conv window write-back (T >= 3): the group holding token T - 1 also holds
-    // the raw inputs T-3 .. T-1, at x[T - t0 + j].
-    if (T >= kConvState && t0 <= T - 1 && T - 1 < t0 + PT) {
+    if (T >= kConvState && ts <= T - 1 && T - 1 < ts + N) {
 #pragma unroll
         for (int j = 0; j < kConvState; ++j) {
             float v = 0.0f;
 #pragma unroll
-            for (int jj = 0; jj < PT + 3; ++jj)
-                if (jj == T - t0 + j) v = x[jj];
+            for (int jj = 0; jj < N + 3; ++jj)
+                if (jj == T - ts + j) v = x[jj];
             cs[(size_t)c * kConvState + j] = v;
         }
     }
-    __shared__ float tile[PT][kDk + 4];
-    __shared__ float nrm[PT];
-    float y[PT];
 #pragma unroll
-    for (int j = 0; j < PT; ++j) {
+    for (int j = 0; j < N; ++j) {
         // Taps in the reference's order: j = 0 (current) .. 3 (x[t-3]), zero pad.
         float acc = w0 * x[j + 3];
         acc += w1 * x[j + 2];
         acc += w2 * x[j + 1];
         acc += w3 * x[j];
-        y[j] = t0 + j < T ? silu(acc) : 0.0f;
-    }
-    float scale[PT];
-    if (hb < 2 * nk) {
-        // Sum of squares per token: transpose through LDS, then thread
-        // (token tid/8, part tid%8) adds 16 channels and 8 lanes combine.
-#pragma unroll
-        for (int j = 0; j < PT; ++j) tile[j][tid] = y[j] * y[j];
-        __syncthreads();
-        {
-            const int j = tid >> 3, part = tid & 7;
-            float a = 0.0f;
-#pragma unroll
-            for (int e = 0; e < 16; ++e) a += tile[j][16 * part + e];
-            a = group_sum<8>(a);
-            if (part == 0) nrm[j] = a;
-        }
-        __syncthreads();
-        const float pre = hb < nk ? 1.0f / sqrtf((float)kDk) : 1.0f;
-#pragma unroll
-        for (int j = 0; j < PT; ++j) scale[j] = pre / sqrtf(nrm[j] + eps);
-    } else {
-#pragma unroll
-        for (int j = 0; j < PT; ++j) scale[j] = 1.0f;
-    }
-#pragma unroll
-    for (int j = 0; j < PT; ++j) tile[j][tid] = y[j] * scale[j];
-    __syncthreads();
-    // Thread writes float4 o4 = tid + 128 i of the group's 512 (kb = o4/64, lane = o4%64).
-    const int head = hb < nk ? hb : (hb < 2 * nk ? hb - nk : hb - 2 * nk);
-    const size_t gbase = ((size_t)head * nch + n) * CB + (size_t)tb * 8 * 256;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const int o4 = tid + 128 * i, kb = o4 >> 6, ln = o4 & 63, g = ln >> 4, cc = ln & 15;
-        const float4 av = *reinterpret_cast<const float4*>(&tile[cc][16 * kb + 4 * g]);
-        const float4 dv = make_float4(tile[4 * g][16 * kb + cc], tile[4 * g + 1][16 * kb + cc],
-                                      tile[4 * g + 2][16 * kb + cc], tile[4 * g + 3][16 * kb + cc]);
-        if (hb < nk) {
-            reinterpret_cast<float4*>(w.qa + gbase)[o4] = av;
-        } else if (hb < 2 * nk) {
-            reinterpret_cast<float4*>(w.kt + gbase)[o4] = dv;
-        } else {
-            reinterpret_cast<float4*>(w.vd + gbase)[o4] = dv;
-        }
-    }
-    if (hb >= 2 * nk && tid < PT && t0 + tid < T) {
-        const int vh = hb - 2 * nk;
-        const size_t gi = (size_t)(t0 + tid) * nv + vh;
-        w.beta[gi] = 1.0f / (1.0f + expf(-bin[gi]));
-        w.gl[gi] = ssm_a[vh] * softplus_ref(ain[gi] + dt_bias[vh]);
+        y[j] = ts + j < T ? silu(acc) : 0.0f;
     }
 }
 
@@ -275,62 +209,111 @@ __global__ void deltanet_conv_writeback(const float* __restrict__ qkv,
 __constant__ int kTriRb[10] = {0, 1, 1, 2, 2, 2, 3, 3, 3, 3};
 __constant__ int kTriCb[10] = {0, 0, 1, 0, 1, 2, 0, 1, 2, 3};
 
-// One workgroup per (k-head, chunk).  K K^T and (Q K^T)^T are formed once for
-// the R v-heads of the k-head (their 20 lower 16x16 blocks, 5 per wave, kept
-// in registers); every operand is a coalesced float4 of the chunk-block
-// layouts.  (Q K^T)^T = K Q^T comes out of the MFMA already in the A layout
-// of M o QK^T that dn_chunk_scan reads.  Per v-head: the decay masks, the
-// 16x16 diagonal-block inverses of I + A, and the blocked forward
-// substitution for W (written in the A layout through an LDS transpose) and
-// U (written in the D layout straight from the MFMA tile).
-__global__ __launch_bounds__(256, 2) void dn_chunk_prep(PrefillWork w, int T, int nk, int nv,
-                                                        int nch) {
+// One workgroup per (k-head, chunk): the conv, gates and L2 norms of the
+// chunk's inputs (Prefill.cs:181-248), then the chunked WY preparation.
+//  - q and k of the k-head: conv + SiLU (thread = channel, 32 tokens) into a
+//    row-major LDS tile, L2 norm per token (q also / sqrt(dk)); q goes to the
+//    workspace in the A layout (for Q K^T and the scan's Q S), k in the D
+//    layout (the scan's K^T D), and k stays in LDS for the rest.
+//  - beta = sigmoid(b), g = ssm_a * softplus(a + dt_bias) of the R v-heads.
+//  - K K^T and (Q K^T)^T once for the R v-heads (their 20 lower 16x16 blocks,
+//    5 per wave, kept in registers); (Q K^T)^T = K Q^T comes out of the MFMA
+//    already in the A layout of M o QK^T that dn_chunk_out reads.
+//  - Per v-head: the decay masks, the 16x16 diagonal-block inverses of I + A,
+//    and the blocked forward substitution for W (right-hand sides from the k
+//    tile; written in the A layout through an LDS transpose) and U (v conv'd
+//    into LDS 64 channels at a time; written in the D layout straight from
+//    the MFMA tile).
+// The normalised q, k, v thus never make a round trip through HBM except
+// the q and k blocks the scan needs.
+__global__ __launch_bounds__(256, 2) void dn_chunk_prep(
+    const float* __restrict__ qkv, const float* __restrict__ bin, const float* __restrict__ ain,
+    const float* __restrict__ conv_w, const float* __restrict__ ssm_a,
+    const float* __restrict__ dt_bias, PrefillWork w, float* __restrict__ cs, int T, int nk,
+    int nv, int nch, float eps) {
     const int kh = blockIdx.x / nch, n = blockIdx.x % nch;
     const int R = nv / nk;
     const int t0 = n * CH;
     const int tn = min(CH, T - t0);
+    const int key_dim = nk * kDk, conv_dim = 2 * key_dim + nv * kDk;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int g = lane >> 4, c16 = lane & 15;
 
-    __shared__ float Am[CH][LDA];     // -A (strictly lower part of the lower blocks)
-    __shared__ float Td[4][16][17];   // inverses of the 16x16 diagonal blocks of I + A
-    __shared__ float tr[4][16][17];   // per-wave transpose scratch
+    __shared__ float Ks[CH][kDk + 4];  // q, then k^ of the chunk, row-major
+    __shared__ float Vs[CH][LDA];      // 64 channels of v, row-major
+    __shared__ float Am[CH][LDA];      // -A (strictly lower part of the lower blocks)
+    __shared__ float Td[4][16][17];    // inverses of the 16x16 diagonal blocks of I + A
+    __shared__ float tr[4][16][17];    // per-wave transpose scratch
     __shared__ double Gd[CH];
-    __shared__ float bet[CH], gam[CH];
+    __shared__ float bet[CH], gam[CH], nrm[CH];
     __shared__ float pre_b[kMaxVPerK][CH], pre_g[kMaxVPerK][CH];
-    __shared__ float Ks[CH][kDk + 4];  // k^ of the chunk, row-major
 
-    // beta and g of the R v-heads, fetched up front (thread = (v-head, token)).
+    // beta and g of the R v-heads (thread = (v-head, token); padded tokens
+    // read the last row and are masked below).
     if (tid < R * CH) {
-        const int rr = tid / CH, j = tid % CH;
-        const int t = min(t0 + j, T - 1);
-        pre_b[rr][j] = w.beta[(size_t)t * nv + kh * R + rr];
-        pre_g[rr][j] = w.gl[(size_t)t * nv + kh * R + rr];
+        const int rr = tid / CH, j = tid % CH, vh = kh * R + rr;
+        const size_t gi = (size_t)min(t0 + j, T - 1) * nv + vh;
+        pre_b[rr][j] = 1.0f / (1.0f + expf(-bin[gi]));
+        pre_g[rr][j] = ssm_a[vh] * softplus_ref(ain[gi] + dt_bias[vh]);
     }
 
-    const float* qA = w.qa + ((size_t)kh * nch + n) * CB;
-    const float* kD = w.kt + ((size_t)kh * nch + n) * CB;
-
-    // k^ arrives in the D layout only (the scan's K^T D operand); its rows,
-    // the A operands of K K^T and Q K^T, are read from a row-major LDS copy.
-    // Float4 o4 = (tb * 8 + kb) * 64 + lane holds rows 16 tb + 4 g + s,
-    // column 16 kb + c.
+    // q, then k: conv'd into Ks (thread = channel tid % 128, tokens 32 (tid /
+    // 128) ..), then the per-token sum of squares (thread = (token, quarter)).
+    // The raw inputs of both are loaded up front.
+    const int cq = tid & (kDk - 1), hq = tid >> 7;
+    const int cq_q = kh * kDk + cq, cq_k = key_dim + kh * kDk + cq;
+    float xq[35], xk[35];
+    conv_load<32>(qkv, cq_q, conv_dim, T, t0 + 32 * hq, xq);
+    conv_load<32>(qkv, cq_k, conv_dim, T, t0 + 32 * hq, xk);
+    auto conv_qk = [&](int ch, float (&x)[35], float (&y)[32]) {
+        conv_finish<32>(conv_w, cs, ch, conv_dim, T, t0 + 32 * hq, x, y);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const int o4 = tid + 256 * i, bk = o4 >> 6, ln = o4 & 63;
-        const int r0 = 16 * (bk >> 3) + 4 * (ln >> 4), c0 = 16 * (bk & 7) + (ln & 15);
-        const float4 v = reinterpret_cast<const float4*>(kD)[o4];
-        Ks[r0][c0] = v.x;
-        Ks[r0 + 1][c0] = v.y;
-        Ks[r0 + 2][c0] = v.z;
-        Ks[r0 + 3][c0] = v.w;
+        for (int j = 0; j < 32; ++j) Ks[32 * hq + j][cq] = y[j];
+        lds_barrier();
+        {
+            const int row = tid >> 2, part = tid & 3;
+            float acc = 0.0f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float4 v = *reinterpret_cast<const float4*>(&Ks[row][32 * part + 4 * e]);
+                acc += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+            }
+            acc = group_sum<4>(acc);
+            if (part == 0) nrm[row] = __builtin_amdgcn_rsqf(acc + eps);   // 1 / |x|
+        }
+        lds_barrier();
+    };
+    const size_t kidx = (size_t)kh * nch + n;
+    {
+        float y[32];
+        conv_qk(cq_q, xq, y);
+        // q^ = q / |q| / sqrt(dk) to the workspace, A layout: float4 o4 =
+        // (tb * 8 + kb) * 64 + lane holds row 16 tb + c, columns 16 kb + 4 g ..
+        float4* qA = reinterpret_cast<float4*>(w.qa + kidx * CB);
+        const float pre = 1.0f / sqrtf((float)kDk);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int o4 = tid + 256 * i, bk = o4 >> 6, ln = o4 & 63;
+            const int row = 16 * (bk >> 3) + (ln & 15), col = 16 * (bk & 7) + 4 * (ln >> 4);
+            const float sc = pre * nrm[row];
+            const float4 v = *reinterpret_cast<const float4*>(&Ks[row][col]);
+            qA[o4] = make_float4(v.x * sc, v.y * sc, v.z * sc, v.w * sc);
+        }
+        lds_barrier();
+        conv_qk(cq_k, xk, y);
+        // k^ = k / |k| in place (thread owns its channel's 32 rows).
+#pragma unroll
+        for (int j = 0; j < 32; ++j) Ks[32 * hq + j][cq] = y[j] * nrm[32 * hq + j];
     }
+    // Also makes this workgroup's q^ stores visible to its own loads below
+    // (the only barrier here that waits for global stores).
     __syncthreads();
 
     // Block bi: bi < 10 -> K K^T block (rb, cb), rows 16rb + 4g + r, cols 16cb + c;
     //           bi >= 10 -> (Q K^T)^T block: D rows = keys 16cb + 4g + r, cols = queries 16rb + c.
     // The Q operand loads of block m + 1 are in flight while block m's 32
     // MFMAs run; the K operands come from LDS.
+    const float* qA = w.qa + kidx * CB;
     f32x4 blk[5];
     float4 oa[2][8], ob[2][8];
     auto load_blk = [&](int m, float4 (&a)[8], float4 (&b)[8]) {
@@ -365,24 +348,28 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep(PrefillWork w, int T, in
         }
         blk[m] = acc;
     }
-    __syncthreads();
+    // k^ to the workspace, D layout: float4 o4 holds rows 16 tb + 4 g + s,
+    // column 16 kb + c.
+    {
+        float4* kD = reinterpret_cast<float4*>(w.kt + kidx * CB);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const int o4 = tid + 256 * i, bk = o4 >> 6, ln = o4 & 63;
+            const int r0 = 16 * (bk >> 3) + 4 * (ln >> 4), c0 = 16 * (bk & 7) + (ln & 15);
+            kD[o4] = make_float4(Ks[r0][c0], Ks[r0 + 1][c0], Ks[r0 + 2][c0], Ks[r0 + 3][c0]);
+        }
+    }
 
 #pragma unroll 1
     for (int rr = 0; rr < R; ++rr) {
         const int vh = kh * R + rr;
         const size_t cidx = (size_t)vh * nch + n;
-        // Right-hand sides of the solve, one column block (k^ blocks 0..7, v
-        // blocks 8..15) ahead: the first is issued now, so its latency hides
-        // behind the gates, masks and diagonal inverses.
-        const float* vD = w.vd + cidx * CB;
-        auto load_rhs = [&](int k4, float4 (&x)[4]) {
-            const int cbk = wave + 4 * k4;
-            const float* src = cbk >= 8 ? vD : kD;
-#pragma unroll
-            for (int ib = 0; ib < 4; ++ib) x[ib] = *blk4(src, ib, cbk & 7, lane);
-        };
-        float4 xc[4];
-        load_rhs(0, xc);
+        // v of this head, conv'd 64 channels at a time into Vs (thread =
+        // channel tid % 64, tokens 16 (tid / 64) ..); the first half's raw
+        // inputs go out now, behind the gates, masks and diagonal inverses.
+        const int cl = tid & 63, qt = tid >> 6;
+        float xv[19];
+        conv_load<16>(qkv, 2 * key_dim + vh * kDk + cl, conv_dim, T, t0 + 16 * qt, xv);
         // Gates and the fp64 running sum of g; padded tokens get beta = g = 0.
         if (wave == 0) {
             const bool valid = lane < tn;
@@ -399,7 +386,7 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep(PrefillWork w, int T, in
             gam[lane] = gm;
             w.gam[cidx * CH + lane] = gm;
         }
-        __syncthreads();
+        lds_barrier();
         if (wave == 1) w.gdec[cidx * CH + lane] = expf((float)(Gd[CH - 1] - Gd[lane]));
         // Decay masks on the register blocks: -A into LDS, M o QK^T to the workspace.
         float* aqk = w.aqk + cidx * CH * CH;
@@ -426,7 +413,7 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep(PrefillWork w, int T, in
                 reinterpret_cast<float4*>(aqk)[(rb * 4 + cb) * 64 + lane] = v;
             }
         }
-        __syncthreads();
+        lds_barrier();
         // Inverse of each unit-lower 16x16 diagonal block of I + A by forward
         // substitution: column j of the inverse, x_i = [i == j] + sum_{m<i} (-A)_im x_m.
         if (lane < 16) {
@@ -442,9 +429,11 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep(PrefillWork w, int T, in
 #pragma unroll
             for (int i = 0; i < 16; ++i) Td[wave][i][j] = x[i];
         }
-        __syncthreads();
+        lds_barrier();
         // Y = (I + A)^-1 X for X = diag(beta gamma) K^ (-> W) and diag(beta) V (-> U),
-        // block row by block row; the wave takes column blocks wave + 4k of the 16.
+        // block row by block row; the wave takes column blocks wave + 4k of the 16
+        // (k^ blocks 0..7 from Ks, v blocks 8..15 from Vs, which holds v channels
+        // 64 (k - 2) .. + 63 while k = 2, 3).
         float* wA = w.wa + cidx * CB;
         float* uD = w.ud + cidx * CB;
 #pragma unroll 1
@@ -452,19 +441,27 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep(PrefillWork w, int T, in
             const int cbk = wave + 4 * k4;
             const bool isV = cbk >= 8;
             const int kb = cbk & 7;
-            float4 xn[4];
-            load_rhs(min(k4 + 1, 3), xn);
+            if (k4 >= 2) {
+                float y[16];
+                const int ch = 2 * key_dim + vh * kDk + 64 * (k4 - 2) + cl;
+                conv_finish<16>(conv_w, cs, ch, conv_dim, T, t0 + 16 * qt, xv, y);
+                // The second half's raw inputs go out behind the first half's solve.
+                if (k4 == 2) conv_load<16>(qkv, ch + 64, conv_dim, T, t0 + 16 * qt, xv);
+                if (k4 == 3) lds_barrier();   // every wave is past the first half
+#pragma unroll
+                for (int j = 0; j < 16; ++j) Vs[16 * qt + j][cl] = y[j];
+                lds_barrier();
+            }
             f32x4 Y[4];
 #pragma unroll
             for (int ib = 0; ib < 4; ++ib) {
-                const float4 xv = xc[ib];
-                const float* xp = reinterpret_cast<const float*>(&xv);
                 f32x4 acc;
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const int row = 16 * ib + 4 * g + r;
                     const float gm = gam[row];
-                    acc[r] = xp[r] * bet[row] * (isV ? 1.0f : gm);
+                    const float xv = isV ? Vs[row][16 * (kb & 3) + c16] : Ks[row][16 * kb + c16];
+                    acc[r] = xv * bet[row] * (isV ? 1.0f : gm);
                 }
 #pragma unroll
                 for (int jb = 0; jb < ib; ++jb) {
@@ -490,10 +487,8 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep(PrefillWork w, int T, in
                     reinterpret_cast<float4*>(wA)[(ib * 8 + kb) * 64 + lane] = av;
                 }
             }
-#pragma unroll
-            for (int ib = 0; ib < 4; ++ib) xc[ib] = xn[ib];
         }
-        __syncthreads();
+        lds_barrier();
     }
 }
 
@@ -801,23 +796,16 @@ hipError_t launch_deltanet_prefill(q35m_ctx* c, int layer, int seq, int T, const
     float* state = L.state + (size_t)seq * d.nv * kDk * kDk;
     float* cs = L.conv_window(seq, c->n_seqs, d.conv_dim);
     hipError_t e;
-    {
-        ProfScope ps_(c, K_DN_PREFILL_PREP);
-        hipExtLaunchKernelGGL(deltanet_prefill_prep, dim3(2 * d.nk + d.nv, nch * (CH / PT)), dim3(kDk),
-                           0, c->stream, ps_.a, ps_.b, 0, qkv, b, a, L.conv_w, L.ssm_a, L.dt_bias, w, cs, T, d.nk,
-                           d.nv, nch, d.eps);
-    }
     if (T < kConvState) {
-        if ((e = hipGetLastError()) != hipSuccess) return e;
         ProfScope ps_(c, K_DN_CONV_WRITEBACK);
         hipExtLaunchKernelGGL(deltanet_conv_writeback, dim3((d.conv_dim + 255) / 256), dim3(256), 0,
                            c->stream, ps_.a, ps_.b, 0, qkv, L.conv_w, cs, T, d.conv_dim);
+        if ((e = hipGetLastError()) != hipSuccess) return e;
     }
-    if ((e = hipGetLastError()) != hipSuccess) return e;
     {
         ProfScope ps_(c, K_DN_CHUNK_PREP);
-        hipExtLaunchKernelGGL(dn_chunk_prep, dim3(d.nk * nch), dim3(256), 0, c->stream, ps_.a, ps_.b, 0, w, T, d.nk,
-                           d.nv, nch);
+        hipExtLaunchKernelGGL(dn_chunk_prep, dim3(d.nk * nch), dim3(256), 0, c->stream, ps_.a, ps_.b, 0, qkv,
+                           b, a, L.conv_w, L.ssm_a, L.dt_bias, w, cs, T, d.nk, d.nv, nch, d.eps);
     }
     if ((e = hipGetLastError()) != hipSuccess) return e;
     {

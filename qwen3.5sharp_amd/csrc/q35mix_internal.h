@@ -58,7 +58,6 @@ struct AttnLayer {
 // Qwen35Model.cs:42-72).
 enum KernelId {
     K_DN_DECODE = 0,
-    K_DN_PREFILL_PREP,
     K_DN_CONV_WRITEBACK,
     K_DN_CHUNK_PREP,
     K_DN_CHUNK_SCAN,
