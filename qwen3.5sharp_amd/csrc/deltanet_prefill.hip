@@ -125,19 +125,37 @@ PrefillWork carve(float* w, const Dims& d, int T, int nch) {
 // SiLU of the zero-padded causal conv of channel c (prefill tap order: tap j
 // multiplies x[t - j], GatedDeltaNetOps.cs:27-53) over the N tokens from
 // `ts`; tokens at or past T give 0.  conv_load issues the N + 3 raw-input
-// loads unconditionally from clamped rows (a select on the row test would
-// become a branch around each load and serialise them), so callers can put
-// them in flight early; conv_finish applies the zero padding as a multiply by
-// 0/1 and the taps.  Each qkv element is read once per range.  For T >= 3 the
-// range that holds token T - 1 also writes the conv window <- the last K - 1
-// raw inputs (Prefill.cs:192-204).
+// loads so callers can put them in flight early; conv_finish applies the
+// taps.  Each qkv element is read once per range.  For T >= 3 the range that
+// holds token T - 1 also writes the conv window <- the last K - 1 raw inputs
+// (Prefill.cs:192-204).
+//
+// The raw inputs come through a buffer descriptor based at row r0 of qkv and
+// ending at row T: rows before 0 (negative offsets wrap past the end) and
+// rows from T on fall outside it and load as 0, which is the conv's zero
+// padding, so the loads need no clamps or masks.  Offsets stay below 2^31 for
+// any T (a chunk spans 67 rows of the descriptor).
+struct QkvRows {
+    __amdgpu_buffer_rsrc_t rsrc;
+    int r0;
+};
+
+__device__ __forceinline__ QkvRows qkv_rows(const float* qkv, int conv_dim, int T, int r0) {
+    const long long bytes = (long long)(T - r0) * conv_dim * sizeof(float);
+    return {__builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(qkv + (size_t)r0 * conv_dim), 0,
+                                              (int)min(bytes, 0x7fffffffLL), 0x00020000),
+            r0};
+}
+
+// `ts` is wave-uniform, so the row offsets are scalar work.
 template <int N>
-__device__ __forceinline__ void conv_load(const float* __restrict__ qkv, int c, int conv_dim,
-                                          int T, int ts, float (&x)[N + 3]) {
+__device__ __forceinline__ void conv_load(const QkvRows& q, int c, int conv_dim, int ts,
+                                          float (&x)[N + 3]) {
 #pragma unroll
     for (int j = 0; j < N + 3; ++j) {
-        const int t = ts - 3 + j;
-        x[j] = qkv[(size_t)min(max(t, 0), T - 1) * conv_dim + c];
+        const int row = ts - 3 + j - q.r0;
+        x[j] = __builtin_bit_cast(
+            float, __builtin_amdgcn_raw_buffer_load_b32(q.rsrc, (row * conv_dim + c) * 4, 0, 0));
     }
 }
 
@@ -147,13 +165,6 @@ __device__ __forceinline__ void conv_finish(const float* __restrict__ conv_w,
                                             int ts, float (&x)[N + 3], float (&y)[N]) {
     const float w0 = conv_w[c], w1 = conv_w[conv_dim + c], w2 = conv_w[2 * conv_dim + c],
                 w3 = conv_w[3 * conv_dim + c];
-    if (ts < 3 || ts + N > T) {          // edge ranges only (uniform per wave)
-#pragma unroll
-        for (int j = 0; j < N + 3; ++j) {
-            const int t = ts - 3 + j;
-            x[j] *= (t >= 0 && t < T) ? 1.0f : 0.0f;
-        }
-    }
     if (T >= kConvState && ts <= T - 1 && T - 1 < ts + N) {
 #pragma unroll
         for (int j = 0; j < kConvState; ++j) {
@@ -260,11 +271,12 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep(
     // q, then k: conv'd into Ks (thread = channel tid % 128, tokens 32 (tid /
     // 128) ..), then the per-token sum of squares (thread = (token, quarter)).
     // The raw inputs of both are loaded up front.
-    const int cq = tid & (kDk - 1), hq = tid >> 7;
+    const int cq = tid & (kDk - 1), hq = __builtin_amdgcn_readfirstlane(tid >> 7);
     const int cq_q = kh * kDk + cq, cq_k = key_dim + kh * kDk + cq;
+    const QkvRows rows = qkv_rows(qkv, conv_dim, T, max(t0 - 3, 0));
     float xq[35], xk[35];
-    conv_load<32>(qkv, cq_q, conv_dim, T, t0 + 32 * hq, xq);
-    conv_load<32>(qkv, cq_k, conv_dim, T, t0 + 32 * hq, xk);
+    conv_load<32>(rows, cq_q, conv_dim, t0 + 32 * hq, xq);
+    conv_load<32>(rows, cq_k, conv_dim, t0 + 32 * hq, xk);
     auto conv_qk = [&](int ch, float (&x)[35], float (&y)[32]) {
         conv_finish<32>(conv_w, cs, ch, conv_dim, T, t0 + 32 * hq, x, y);
 #pragma unroll
@@ -367,9 +379,9 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep(
         // v of this head, conv'd 64 channels at a time into Vs (thread =
         // channel tid % 64, tokens 16 (tid / 64) ..); the first half's raw
         // inputs go out now, behind the gates, masks and diagonal inverses.
-        const int cl = tid & 63, qt = tid >> 6;
+        const int cl = tid & 63, qt = __builtin_amdgcn_readfirstlane(wave);
         float xv[19];
-        conv_load<16>(qkv, 2 * key_dim + vh * kDk + cl, conv_dim, T, t0 + 16 * qt, xv);
+        conv_load<16>(rows, 2 * key_dim + vh * kDk + cl, conv_dim, t0 + 16 * qt, xv);
         // Gates and the fp64 running sum of g; padded tokens get beta = g = 0.
         if (wave == 0) {
             const bool valid = lane < tn;
@@ -382,12 +394,12 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep(
             }
             Gd[lane] = G;
             bet[lane] = valid ? bv : 0.0f;
-            const float gm = expf((float)G);
+            const float gm = __expf((float)G);
             gam[lane] = gm;
             w.gam[cidx * CH + lane] = gm;
         }
         lds_barrier();
-        if (wave == 1) w.gdec[cidx * CH + lane] = expf((float)(Gd[CH - 1] - Gd[lane]));
+        if (wave == 1) w.gdec[cidx * CH + lane] = __expf((float)(Gd[CH - 1] - Gd[lane]));
         // Decay masks on the register blocks: -A into LDS, M o QK^T to the workspace.
         float* aqk = w.aqk + cidx * CH * CH;
 #pragma unroll
@@ -399,7 +411,7 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep(
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const int i = 16 * rb + 4 * g + r;
-                    Am[i][j] = j < i ? -bet[i] * expf((float)(Gd[i] - Gd[j])) * blk[m][r] : 0.0f;
+                    Am[i][j] = j < i ? -bet[i] * __expf((float)(Gd[i] - Gd[j])) * blk[m][r] : 0.0f;
                 }
             } else {
                 const int iq = 16 * rb + c16;   // query token
@@ -408,7 +420,7 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep(
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const int jk = 16 * cb + 4 * g + r;   // key token
-                    vp[r] = jk <= iq ? expf((float)(Gd[iq] - Gd[jk])) * blk[m][r] : 0.0f;
+                    vp[r] = jk <= iq ? __expf((float)(Gd[iq] - Gd[jk])) * blk[m][r] : 0.0f;
                 }
                 reinterpret_cast<float4*>(aqk)[(rb * 4 + cb) * 64 + lane] = v;
             }
@@ -446,7 +458,7 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep(
                 const int ch = 2 * key_dim + vh * kDk + 64 * (k4 - 2) + cl;
                 conv_finish<16>(conv_w, cs, ch, conv_dim, T, t0 + 16 * qt, xv, y);
                 // The second half's raw inputs go out behind the first half's solve.
-                if (k4 == 2) conv_load<16>(qkv, ch + 64, conv_dim, T, t0 + 16 * qt, xv);
+                if (k4 == 2) conv_load<16>(rows, ch + 64, conv_dim, t0 + 16 * qt, xv);
                 if (k4 == 3) lds_barrier();   // every wave is past the first half
 #pragma unroll
                 for (int j = 0; j < 16; ++j) Vs[16 * qt + j][cl] = y[j];
