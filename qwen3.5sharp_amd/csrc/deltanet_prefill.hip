@@ -254,7 +254,6 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep(
     __shared__ float Vs[CH][LDA];      // 64 channels of v, row-major
     __shared__ float Am[CH][LDA];      // -A (strictly lower part of the lower blocks)
     __shared__ float Td[4][16][17];    // inverses of the 16x16 diagonal blocks of I + A
-    __shared__ float tr[4][16][17];    // per-wave transpose scratch
     __shared__ double Gd[CH];
     __shared__ float bet[CH], gam[CH], nrm[CH];
     __shared__ float pre_b[kMaxVPerK][CH], pre_g[kMaxVPerK][CH];
@@ -443,61 +442,55 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep(
         }
         lds_barrier();
         // Y = (I + A)^-1 X for X = diag(beta gamma) K^ (-> W) and diag(beta) V (-> U),
-        // block row by block row; the wave takes column blocks wave + 4k of the 16
-        // (k^ blocks 0..7 from Ks, v blocks 8..15 from Vs, which holds v channels
-        // 64 (k - 2) .. + 63 while k = 2, 3).
+        // block row by block row.  Pass h: the wave solves K block wave + 4h and
+        // v block wave + 4h together (two independent MFMA chains sharing the
+        // A and T operands; Vs holds v channels 64 h .. + 63).  W goes out in
+        // the A layout as Y^T = X^T T^T, one more MFMA per block on the same
+        // operands (the D tile of Y^T is Y in the A layout).
         float* wA = w.wa + cidx * CB;
         float* uD = w.ud + cidx * CB;
 #pragma unroll 1
-        for (int k4 = 0; k4 < 4; ++k4) {
-            const int cbk = wave + 4 * k4;
-            const bool isV = cbk >= 8;
-            const int kb = cbk & 7;
-            if (k4 >= 2) {
+        for (int h = 0; h < 2; ++h) {
+            const int kb = wave + 4 * h;
+            {
                 float y[16];
-                const int ch = 2 * key_dim + vh * kDk + 64 * (k4 - 2) + cl;
+                const int ch = 2 * key_dim + vh * kDk + 64 * h + cl;
                 conv_finish<16>(conv_w, cs, ch, conv_dim, T, t0 + 16 * qt, xv, y);
                 // The second half's raw inputs go out behind the first half's solve.
-                if (k4 == 2) conv_load<16>(rows, ch + 64, conv_dim, t0 + 16 * qt, xv);
-                if (k4 == 3) lds_barrier();   // every wave is past the first half
+                if (h == 0) conv_load<16>(rows, ch + 64, conv_dim, t0 + 16 * qt, xv);
+                if (h == 1) lds_barrier();   // every wave is past the first half
 #pragma unroll
                 for (int j = 0; j < 16; ++j) Vs[16 * qt + j][cl] = y[j];
                 lds_barrier();
             }
-            f32x4 Y[4];
+            f32x4 YK[4], YV[4];
 #pragma unroll
             for (int ib = 0; ib < 4; ++ib) {
-                f32x4 acc;
+                f32x4 accK, accV;
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const int row = 16 * ib + 4 * g + r;
-                    const float gm = gam[row];
-                    const float xv = isV ? Vs[row][16 * (kb & 3) + c16] : Ks[row][16 * kb + c16];
-                    acc[r] = xv * bet[row] * (isV ? 1.0f : gm);
+                    const float bt = bet[row];
+                    accK[r] = Ks[row][16 * kb + c16] * bt * gam[row];
+                    accV[r] = Vs[row][16 * wave + c16] * bt;
                 }
 #pragma unroll
                 for (int jb = 0; jb < ib; ++jb) {
                     const float4 a = *reinterpret_cast<const float4*>(&Am[16 * ib + c16][16 * jb + 4 * g]);
-                    acc = mfma16x4(a, Y[jb], acc);
+                    accK = mfma16x4(a, YK[jb], accK);
+                    accV = mfma16x4(a, YV[jb], accV);
                 }
                 const float4 tdv = make_float4(Td[ib][c16][4 * g], Td[ib][c16][4 * g + 1],
                                                Td[ib][c16][4 * g + 2], Td[ib][c16][4 * g + 3]);
                 const f32x4 zero = {0.f, 0.f, 0.f, 0.f};
-                Y[ib] = mfma16x4(tdv, acc, zero);
-                if (isV) {
-                    reinterpret_cast<float4*>(uD)[(ib * 8 + kb) * 64 + lane] =
-                        make_float4(Y[ib][0], Y[ib][1], Y[ib][2], Y[ib][3]);
-                } else {
-                    // D tile -> A layout: element (token 4g+r, dim c16) moves to
-                    // lane (dim/4 = c16/4, token) slot c16%4.
-#pragma unroll
-                    for (int r = 0; r < 4; ++r) tr[wave][4 * g + r][c16] = Y[ib][r];
-                    __builtin_amdgcn_wave_barrier();
-                    const float4 av = make_float4(tr[wave][c16][4 * g], tr[wave][c16][4 * g + 1],
-                                                  tr[wave][c16][4 * g + 2], tr[wave][c16][4 * g + 3]);
-                    __builtin_amdgcn_wave_barrier();
-                    reinterpret_cast<float4*>(wA)[(ib * 8 + kb) * 64 + lane] = av;
-                }
+                YK[ib] = mfma16x4(tdv, accK, zero);
+                YV[ib] = mfma16x4(tdv, accV, zero);
+                const f32x4 wt = mfma16x4(make_float4(accK[0], accK[1], accK[2], accK[3]),
+                                          f32x4{tdv.x, tdv.y, tdv.z, tdv.w}, zero);
+                reinterpret_cast<float4*>(uD)[(ib * 8 + kb) * 64 + lane] =
+                    make_float4(YV[ib][0], YV[ib][1], YV[ib][2], YV[ib][3]);
+                reinterpret_cast<float4*>(wA)[(ib * 8 + kb) * 64 + lane] =
+                    make_float4(wt[0], wt[1], wt[2], wt[3]);
             }
         }
         lds_barrier();
