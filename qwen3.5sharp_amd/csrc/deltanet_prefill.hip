@@ -21,21 +21,20 @@
 // (G reaches ~ -2000) keep full fp32 accuracy.
 //
 // Kernels:
-//  1. deltanet_prefill_prep: zero-padded causal conv with the prefill tap
-//     order (tap j multiplies x[t-j], GatedDeltaNetOps.cs:27-53) + SiLU, read
-//     straight from the token-major qkv (no transpose); q/k L2 norm (q also
-//     scaled by 1/sqrt(dk)); beta = sigmoid(b), g = ssm_a * softplus(a +
-//     dt_bias) (Prefill.cs:239-248).
-//     For T >= K-1 it also writes the conv window <- last K-1 raw inputs
-//     (Prefill.cs:192-204).
-//  2. deltanet_conv_writeback (T < K-1 only): the conv window write-back
+//  1. deltanet_conv_writeback (T < K-1 only): the conv window write-back
 //     reproducing the reference's read past the channel row.
-//  3. dn_chunk_prep (one workgroup per k-head and chunk; the R v-heads of the
-//     k-head share K K^T and Q K^T): K K^T and Q K^T on MFMA, the decay masks,
-//     T = (I+A)^-1 by blocked forward substitution (16x16 diagonal blocks
-//     inverted in registers, off-diagonal blocks applied on MFMA), then
-//     W and U on MFMA.  Emits W, U, M o QK^T, gamma, e^{G_last - G}.
-//  4. dn_chunk_scan (one workgroup per v-head and 16-column tile of the
+//  2. dn_chunk_prep (one workgroup per k-head and chunk; the R v-heads of the
+//     k-head share K K^T and Q K^T): the zero-padded causal conv with the
+//     prefill tap order (tap j multiplies x[t-j], GatedDeltaNetOps.cs:27-53)
+//     + SiLU of the chunk's q, k and v channels, read straight from the
+//     token-major qkv; q/k L2 norm (q also scaled by 1/sqrt(dk)); beta =
+//     sigmoid(b), g = ssm_a * softplus(a + dt_bias) (Prefill.cs:239-248); for
+//     T >= K-1 the conv window <- last K-1 raw inputs (Prefill.cs:192-204).
+//     Then K K^T and Q K^T on MFMA, the decay masks, T = (I+A)^-1 by blocked
+//     forward substitution (16x16 diagonal blocks inverted in registers,
+//     off-diagonal blocks applied on MFMA), and W and U on MFMA.  Emits q^,
+//     k^, W, U, M o QK^T, gamma, e^{G_last - G}.
+//  3. dn_chunk_scan (one workgroup per v-head and 16-column tile of the
 //     state): the only sequential part.  Four waves walk the chunks in order
 //     with the state tile in MFMA accumulators, record D = U - W S of every
 //     chunk, and apply S = gamma_last S + K^T (e^{G_last-G} D); four more
@@ -44,7 +43,7 @@
 //     never go to memory.  Column tiles are independent (the rule is
 //     separable over dv), so 8 workgroups per head run in parallel; the 8
 //     tiles of a head share an XCD so W, Q and K stay in its L2.
-//  5. dn_chunk_out (one workgroup per v-head and chunk, all in parallel):
+//  4. dn_chunk_out (one workgroup per v-head and chunk, all in parallel):
 //     O = diag(gamma) Q S + (M o QK^T) D from the recorded inter-chunk output
 //     and D, with the gated RMSNorm fused into the epilogue.
 //
