@@ -101,11 +101,11 @@ struct PrefillWork {
     float* dh;     // [nv][nch] chunk blocks, D layout: D = U - W S of each chunk
 };
 
-size_t work_floats(const Dims& d, int T, int nch) {
+size_t work_floats(const Dims& d, int nch) {
     return (size_t)nch * CB * (2 * d.nk + 5 * d.nv) + (size_t)d.nv * nch * (CH * CH + 2 * CH);
 }
 
-PrefillWork carve(float* w, const Dims& d, int T, int nch) {
+PrefillWork carve(float* w, const Dims& d, int nch) {
     PrefillWork p;
     const size_t kblk = (size_t)d.nk * nch * CB, vblk = (size_t)d.nv * nch * CB;
     p.qa = w;
@@ -690,8 +690,8 @@ __global__ __launch_bounds__(512) void dn_chunk_scan(PrefillWork w, float* __res
 // 32-lane reduction and z and out move as coalesced float4 rows.
 __global__ __launch_bounds__(256, 3) void dn_chunk_out(PrefillWork w, const float* __restrict__ z,
                                                     const float* __restrict__ wnorm,
-                                                    float* __restrict__ out, int T, int nk,
-                                                    int nv, int nch, float eps) {
+                                                    float* __restrict__ out, int T, int nv,
+                                                    int nch, float eps) {
     const int L = xcd_remap(blockIdx.x, gridDim.x);
     // v-heads vary fastest, so the z rows and output rows in flight are whole
     // token rows (16 KiB) rather than one 512-byte column of many rows.
@@ -788,7 +788,7 @@ __global__ __launch_bounds__(256, 3) void dn_chunk_out(PrefillWork w, const floa
 }  // namespace
 
 size_t deltanet_prefill_work_bytes(const Dims& d, int T) {
-    return work_floats(d, T, (T + CH - 1) / CH) * sizeof(float);
+    return work_floats(d, (T + CH - 1) / CH) * sizeof(float);
 }
 
 hipError_t launch_deltanet_prefill(q35m_ctx* c, int layer, int seq, int T, const float* qkv,
@@ -796,7 +796,7 @@ hipError_t launch_deltanet_prefill(q35m_ctx* c, int layer, int seq, int T, const
     const Dims& d = c->d;
     const DeltaNetLayer& L = c->lin[layer];
     const int nch = (T + CH - 1) / CH;
-    PrefillWork w = carve(c->work, d, T, nch);
+    PrefillWork w = carve(c->work, d, nch);
     float* state = L.state + (size_t)seq * d.nv * kDk * kDk;
     float* cs = L.conv_window(seq, c->n_seqs, d.conv_dim);
     hipError_t e;
@@ -821,7 +821,7 @@ hipError_t launch_deltanet_prefill(q35m_ctx* c, int layer, int seq, int T, const
     {
         ProfScope ps_(c, K_DN_CHUNK_OUT);
         hipExtLaunchKernelGGL(dn_chunk_out, dim3(d.nv * nch), dim3(256), 0, c->stream, ps_.a, ps_.b, 0, w, z,
-                           L.ssm_norm, out, T, d.nk, d.nv, nch, d.eps);
+                           L.ssm_norm, out, T, d.nv, nch, d.eps);
     }
     return hipGetLastError();
 }
