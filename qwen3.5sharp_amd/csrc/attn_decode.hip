@@ -205,18 +205,24 @@ __global__ __launch_bounds__(NT, 2) void attn_decode_partial(
     }
     lds_barrier();
     // Software pipeline: the next sub-chunk's K loads go out once the scores
-    // have consumed kk, its V loads once P.V has consumed vv.  After the last
-    // sub-chunk they fetch clamped rows (row pos) and are discarded.
-    for (int sub = 0;;) {
+    // have consumed kk, its V loads once P.V has consumed vv.
+    // The last sub-chunk runs after the loop, without loads for a next one.
+    int sub = 0;
+    for (;;) {
+        const int s1 = s0 + nchunks * SUB;
+        if (sub + 1 == NSUB || s1 > pos) break;     // uniform across the workgroup
         const int par = sub & 1;
         Q35_SCORES(par)
-        const int s1 = s0 + nchunks * SUB;
         Q35_LOAD_K(s1)
         Q35_SOFTMAX_PV(par)
         Q35_LOAD_V(s1)
         ++sub;
         s0 = s1;
-        if (sub == NSUB || s0 > pos) break;     // uniform across the workgroup
+    }
+    {
+        const int par = sub & 1;
+        Q35_SCORES(par)
+        Q35_SOFTMAX_PV(par)
     }
 #undef Q35_LOAD_K
 #undef Q35_LOAD_V
