@@ -63,6 +63,29 @@ def test_deltanet_prefill_chunk_counts(ctx, T):
     np.testing.assert_array_equal(ctx.state_read(0, 5, q35mix.STATE_CONV), cs_ref)
 
 
+@pytest.mark.parametrize("T", [63, 65, 66, 67, 129])
+def test_deltanet_prefill_chunk_tails(ctx, T):
+    """Last chunk holding 63, 1, 2, 3 and 1 tokens: the conv's zero padding
+    past T, the conv-window write-back from the raw inputs T-3..T-1 when they
+    straddle a chunk boundary, and the masked gates of the padded tokens."""
+    w = synth.deltanet_weights(NK, NV, 128, salt=31)
+    st = synth.deltanet_state(NK, NV, 128, salt=1500 + T)
+    ctx.state_write(0, 9, q35mix.STATE_RECURRENT, st["state"])
+    ctx.state_write(0, 9, q35mix.STATE_CONV, st["conv_state"])
+    x = synth.deltanet_inputs(T, NK, NV, 128, salt=1600 + T)
+    args = [ctx.array((T, ctx.conv_dim), x["qkv"]), ctx.array((T, ctx.value_dim), x["z"]),
+            ctx.array((T, NV), x["b"]), ctx.array((T, NV), x["a"])]
+    out = ctx.array((T, ctx.value_dim))
+    ctx.deltanet_prefill(0, 9, T, *args, out)
+    o_ref, cs_ref, st_ref, _ = oracle.deltanet_prefill(DIMS, T, x["qkv"], x["z"], x["b"], x["a"],
+                                                       w, st["state"], st["conv_state"])
+    e_out = rel(out.download(), o_ref)
+    e_st = rel(ctx.state_read(0, 9, q35mix.STATE_RECURRENT), st_ref)
+    say(f"deltanet_prefill tail T={T}: out rel err {e_out:.2e}, state rel err {e_st:.2e}")
+    assert e_out <= TOL and e_st <= TOL
+    np.testing.assert_array_equal(ctx.state_read(0, 9, q35mix.STATE_CONV), cs_ref)
+
+
 def test_decode_batch_of_64(ctx):
     """Both decode mixers with the full 64-sequence batch, ragged KV lengths."""
     seqs = list(range(NSEQ))
