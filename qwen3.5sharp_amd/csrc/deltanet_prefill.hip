@@ -91,7 +91,6 @@ __device__ __forceinline__ const float4* blk4(const float* base, int tb, int kb,
 struct PrefillWork {
     float* qa;     // [nk][nch] chunk blocks, A layout: q^ (L2-normed, / sqrt(dk))
     float* kt;     // [nk][nch] D layout: k^
-    float* vd;     // [nv][nch] D layout: v
     float* wa;     // [nv][nch] A layout: W
     float* ud;     // [nv][nch] D layout: U
     float* aqk;    // [nv][nch][4 rb][4 cb][64][4]: lane (g,c) holds (M o QK^T)[16rb+c][16cb+4g+s]
@@ -102,7 +101,7 @@ struct PrefillWork {
 };
 
 size_t work_floats(const Dims& d, int nch) {
-    return (size_t)nch * CB * (2 * d.nk + 5 * d.nv) + (size_t)d.nv * nch * (CH * CH + 2 * CH);
+    return (size_t)nch * CB * (2 * d.nk + 4 * d.nv) + (size_t)d.nv * nch * (CH * CH + 2 * CH);
 }
 
 PrefillWork carve(float* w, const Dims& d, int nch) {
@@ -110,8 +109,7 @@ PrefillWork carve(float* w, const Dims& d, int nch) {
     const size_t kblk = (size_t)d.nk * nch * CB, vblk = (size_t)d.nv * nch * CB;
     p.qa = w;
     p.kt = p.qa + kblk;
-    p.vd = p.kt + kblk;
-    p.wa = p.vd + vblk;
+    p.wa = p.kt + kblk;
     p.ud = p.wa + vblk;
     p.aqk = p.ud + vblk;
     p.gam = p.aqk + (size_t)d.nv * nch * CH * CH;
@@ -124,8 +122,8 @@ PrefillWork carve(float* w, const Dims& d, int nch) {
 // SiLU of the zero-padded causal conv of channel c (prefill tap order: tap j
 // multiplies x[t - j], GatedDeltaNetOps.cs:27-53) over the N tokens from
 // `ts`; tokens at or past T give 0.  conv_load issues the N + 3 raw-input
-// loads so callers can put them in flight early; conv_finish applies the
-// taps.  Each qkv element is read once per range.  For T >= 3 the range that
+// loads and the 4 tap weights so callers can put them in flight early;
+// conv_finish applies the taps.  Each qkv element is read once per range.  For T >= 3 the range that
 // holds token T - 1 also writes the conv window <- the last K - 1 raw inputs
 // (Prefill.cs:192-204).
 //
@@ -148,8 +146,9 @@ __device__ __forceinline__ QkvRows qkv_rows(const float* qkv, int conv_dim, int 
 
 // `ts` is wave-uniform, so the row offsets are scalar work.
 template <int N>
-__device__ __forceinline__ void conv_load(const QkvRows& q, int c, int conv_dim, int ts,
-                                          float (&x)[N + 3]) {
+__device__ __forceinline__ void conv_load(const QkvRows& q, const float* __restrict__ conv_w, int c,
+                                          int conv_dim, int ts, float (&x)[N + 3], float4& wt) {
+    wt = make_float4(conv_w[c], conv_w[conv_dim + c], conv_w[2 * conv_dim + c], conv_w[3 * conv_dim + c]);
 #pragma unroll
     for (int j = 0; j < N + 3; ++j) {
         const int row = ts - 3 + j - q.r0;
@@ -159,11 +158,8 @@ __device__ __forceinline__ void conv_load(const QkvRows& q, int c, int conv_dim,
 }
 
 template <int N>
-__device__ __forceinline__ void conv_finish(const float* __restrict__ conv_w,
-                                            float* __restrict__ cs, int c, int conv_dim, int T,
-                                            int ts, float (&x)[N + 3], float (&y)[N]) {
-    const float w0 = conv_w[c], w1 = conv_w[conv_dim + c], w2 = conv_w[2 * conv_dim + c],
-                w3 = conv_w[3 * conv_dim + c];
+__device__ __forceinline__ void conv_finish(float4 wt, float* __restrict__ cs, int c, int conv_dim,
+                                            int T, int ts, float (&x)[N + 3], float (&y)[N]) {
     if (T >= kConvState && ts <= T - 1 && T - 1 < ts + N) {
 #pragma unroll
         for (int j = 0; j < kConvState; ++j) {
@@ -177,10 +173,10 @@ __device__ __forceinline__ void conv_finish(const float* __restrict__ conv_w,
 #pragma unroll
     for (int j = 0; j < N; ++j) {
         // Taps in the reference's order: j = 0 (current) .. 3 (x[t-3]), zero pad.
-        float acc = w0 * x[j + 3];
-        acc += w1 * x[j + 2];
-        acc += w2 * x[j + 1];
-        acc += w3 * x[j];
+        float acc = wt.x * x[j + 3];
+        acc += wt.y * x[j + 2];
+        acc += wt.z * x[j + 1];
+        acc += wt.w * x[j];
         y[j] = ts + j < T ? silu(acc) : 0.0f;
     }
 }
@@ -216,8 +212,10 @@ __global__ void deltanet_conv_writeback(const float* __restrict__ qkv,
 }
 
 // Lower-triangular 16x16 blocks (rb >= cb) of a 64x64 matrix, in work order.
-__constant__ int kTriRb[10] = {0, 1, 1, 2, 2, 2, 3, 3, 3, 3};
-__constant__ int kTriCb[10] = {0, 0, 1, 0, 1, 2, 0, 1, 2, 3};
+// Block i = 0..9 is (rb, cb) = (0,0), (1,0), (1,1), (2,0), ..., (3,3); i is
+// wave-uniform, so this is scalar arithmetic.
+__device__ __forceinline__ int tri_rb(int i) { return (i >= 1) + (i >= 3) + (i >= 6); }
+__device__ __forceinline__ int tri_cb(int i) { return i - tri_rb(i) * (tri_rb(i) + 1) / 2; }
 
 // One workgroup per (k-head, chunk): the conv, gates and L2 norms of the
 // chunk's inputs (Prefill.cs:181-248), then the chunked WY preparation.
@@ -246,7 +244,8 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep(
     const int t0 = n * CH;
     const int tn = min(CH, T - t0);
     const int key_dim = nk * kDk, conv_dim = 2 * key_dim + nv * kDk;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 4, c16 = lane & 15;
 
     __shared__ float Ks[CH][kDk + 4];  // q, then k^ of the chunk, row-major
@@ -273,10 +272,11 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep(
     const int cq_q = kh * kDk + cq, cq_k = key_dim + kh * kDk + cq;
     const QkvRows rows = qkv_rows(qkv, conv_dim, T, max(t0 - 3, 0));
     float xq[35], xk[35];
-    conv_load<32>(rows, cq_q, conv_dim, t0 + 32 * hq, xq);
-    conv_load<32>(rows, cq_k, conv_dim, t0 + 32 * hq, xk);
-    auto conv_qk = [&](int ch, float (&x)[35], float (&y)[32]) {
-        conv_finish<32>(conv_w, cs, ch, conv_dim, T, t0 + 32 * hq, x, y);
+    float4 wq, wk;
+    conv_load<32>(rows, conv_w, cq_q, conv_dim, t0 + 32 * hq, xq, wq);
+    conv_load<32>(rows, conv_w, cq_k, conv_dim, t0 + 32 * hq, xk, wk);
+    auto conv_qk = [&](int ch, float4 wt, float (&x)[35], float (&y)[32]) {
+        conv_finish<32>(wt, cs, ch, conv_dim, T, t0 + 32 * hq, x, y);
 #pragma unroll
         for (int j = 0; j < 32; ++j) Ks[32 * hq + j][cq] = y[j];
         lds_barrier();
@@ -296,7 +296,7 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep(
     const size_t kidx = (size_t)kh * nch + n;
     {
         float y[32];
-        conv_qk(cq_q, xq, y);
+        conv_qk(cq_q, wq, xq, y);
         // q^ = q / |q| / sqrt(dk) to the workspace, A layout: float4 o4 =
         // (tb * 8 + kb) * 64 + lane holds row 16 tb + c, columns 16 kb + 4 g ..
         float4* qA = reinterpret_cast<float4*>(w.qa + kidx * CB);
@@ -310,7 +310,7 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep(
             qA[o4] = make_float4(v.x * sc, v.y * sc, v.z * sc, v.w * sc);
         }
         lds_barrier();
-        conv_qk(cq_k, xk, y);
+        conv_qk(cq_k, wk, xk, y);
         // k^ = k / |k| in place (thread owns its channel's 32 rows).
 #pragma unroll
         for (int j = 0; j < 32; ++j) Ks[32 * hq + j][cq] = y[j] * nrm[32 * hq + j];
@@ -328,7 +328,7 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep(
     float4 oa[2][8], ob[2][8];
     auto load_blk = [&](int m, float4 (&a)[8], float4 (&b)[8]) {
         const int bi = wave + 4 * m;
-        const int mat = bi / 10, rb = kTriRb[bi % 10], cb = kTriCb[bi % 10];
+        const int mat = bi / 10, rb = tri_rb(bi % 10), cb = tri_cb(bi % 10);
         const int ra = mat ? cb : rb;
 #pragma unroll
         for (int q = 0; q < kDk / 16; ++q)
@@ -375,11 +375,15 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep(
         const int vh = kh * R + rr;
         const size_t cidx = (size_t)vh * nch + n;
         // v of this head, conv'd 64 channels at a time into Vs (thread =
-        // channel tid % 64, tokens 16 (tid / 64) ..); the first half's raw
-        // inputs go out now, behind the gates, masks and diagonal inverses.
-        const int cl = tid & 63, qt = __builtin_amdgcn_readfirstlane(wave);
-        float xv[19];
-        conv_load<16>(rows, 2 * key_dim + vh * kDk + cl, conv_dim, t0 + 16 * qt, xv);
+        // channel tid % 64, tokens 16 (tid / 64) ..); the raw inputs of both
+        // halves go out now, behind the gates, masks and diagonal inverses.
+        const int cl = tid & 63, qt = wave;
+        float xv[2][19];
+        float4 wv[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+            conv_load<16>(rows, conv_w, 2 * key_dim + vh * kDk + 64 * h + cl, conv_dim, t0 + 16 * qt,
+                          xv[h], wv[h]);
         // Gates and the fp64 running sum of g; padded tokens get beta = g = 0.
         if (wave == 0) {
             const bool valid = lane < tn;
@@ -403,7 +407,7 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep(
 #pragma unroll
         for (int m = 0; m < 5; ++m) {
             const int bi = wave + 4 * m;
-            const int mat = bi / 10, rb = kTriRb[bi % 10], cb = kTriCb[bi % 10];
+            const int mat = bi / 10, rb = tri_rb(bi % 10), cb = tri_cb(bi % 10);
             if (mat == 0) {
                 const int j = 16 * cb + c16;
 #pragma unroll
@@ -448,15 +452,13 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep(
         // operands (the D tile of Y^T is Y in the A layout).
         float* wA = w.wa + cidx * CB;
         float* uD = w.ud + cidx * CB;
-#pragma unroll 1
+#pragma unroll
         for (int h = 0; h < 2; ++h) {
             const int kb = wave + 4 * h;
             {
                 float y[16];
                 const int ch = 2 * key_dim + vh * kDk + 64 * h + cl;
-                conv_finish<16>(conv_w, cs, ch, conv_dim, T, t0 + 16 * qt, xv, y);
-                // The second half's raw inputs go out behind the first half's solve.
-                if (h == 0) conv_load<16>(rows, ch + 64, conv_dim, t0 + 16 * qt, xv);
+                conv_finish<16>(wv[h], cs, ch, conv_dim, T, t0 + 16 * qt, xv[h], y);
                 if (h == 1) lds_barrier();   // every wave is past the first half
 #pragma unroll
                 for (int j = 0; j < 16; ++j) Vs[16 * qt + j][cl] = y[j];
@@ -513,25 +515,30 @@ struct QsOps {
     float4 gm;                   // gamma of the block's rows 4g .. 4g+3
 };
 
-__device__ __forceinline__ void load_scan_ops(const PrefillWork& w, ScanOps& o, int n, int vh,
-                                              int kh, int tl, int nch, int wave, int g,
-                                              int lane) {
-    const size_t cidx = (size_t)vh * nch + n, kidx = (size_t)kh * nch + n;
+// The operands used first in a chunk (W, U, the decays) and K^, loaded in
+// different phases of the previous chunk so that the L2 reads spread over it.
+__device__ __forceinline__ void load_scan_w(const PrefillWork& w, ScanOps& o, int n, int vh,
+                                            int tl, int nch, int wave, int g, int lane) {
+    const size_t cidx = (size_t)vh * nch + n;
     const float* wA = w.wa + cidx * CB;
-    const float* kD = w.kt + kidx * CB;
     const float* uD = w.ud + cidx * CB;
     const float* gd = w.gdec + cidx * CH;
+    o.glast = w.gam[cidx * CH + CH - 1];
 #pragma unroll
-    for (int tb = 0; tb < 4; ++tb) {
+    for (int tb = 0; tb < 4; ++tb)
 #pragma unroll
-        for (int b = 0; b < 2; ++b) {
-            o.wa[tb][b] = *blk4(wA, tb, 2 * wave + b, lane);
-            o.kt[tb][b] = *blk4(kD, tb, 2 * wave + b, lane);
-        }
-    }
+        for (int b = 0; b < 2; ++b) o.wa[tb][b] = *blk4(wA, tb, 2 * wave + b, lane);
     o.ut = *blk4(uD, wave, tl, lane);
     o.gdv = *reinterpret_cast<const float4*>(gd + 16 * wave + 4 * g);
-    o.glast = w.gam[cidx * CH + CH - 1];
+}
+
+__device__ __forceinline__ void load_scan_k(const PrefillWork& w, ScanOps& o, int n, int kh,
+                                            int nch, int wave, int lane) {
+    const float* kD = w.kt + ((size_t)kh * nch + n) * CB;
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb)
+#pragma unroll
+        for (int b = 0; b < 2; ++b) o.kt[tb][b] = *blk4(kD, tb, 2 * wave + b, lane);
 }
 
 __device__ __forceinline__ void load_qs_ops(const PrefillWork& w, QsOps& o, int n, int vh, int kh,
@@ -575,14 +582,14 @@ __global__ __launch_bounds__(512) void dn_chunk_scan(PrefillWork w, float* __res
         // Inter-chunk output of token block q.  The entry state of chunk n is
         // read between the chunk's two barriers (the chain rewrites that
         // buffer only after the next chunk's second barrier); half of the
-        // products run before the second barrier, half after it.
+        // products run before the second barrier, half after it, behind the
+        // loads of the next chunk's Q^ (issued while the chain runs K^T D).
         __builtin_amdgcn_s_setprio(0);
         const int q = wave - 4;
         QsOps a0, a1;
         load_qs_ops(w, a0, 0, vh, kh, nch, q, g, lane);
         auto qs_chunk = [&](const QsOps& cur, QsOps& nxt, int n) {
             const int par = n & 1;
-            load_qs_ops(w, nxt, min(n + 1, nch - 1), vh, kh, nch, q, g, lane);
             lds_barrier();
             f32x4 Sk[8];
 #pragma unroll
@@ -593,6 +600,7 @@ __global__ __launch_bounds__(512) void dn_chunk_scan(PrefillWork w, float* __res
             __builtin_amdgcn_sched_barrier(0);
             lds_barrier();
             __builtin_amdgcn_sched_barrier(0);
+            load_qs_ops(w, nxt, min(n + 1, nch - 1), vh, kh, nch, q, g, lane);
 #pragma unroll
             for (int kb = 4; kb < 8; ++kb) acc = mfma16x4(cur.qa[kb], Sk[kb], acc);
             *reinterpret_cast<f32x4*>(w.oi + ((size_t)vh * nch + n) * CB +
@@ -618,14 +626,16 @@ __global__ __launch_bounds__(512) void dn_chunk_scan(PrefillWork w, float* __res
 
     // One chunk: the entry state to LDS, D, then the state update.  The
     // operands of chunk `pf` (the next; clamped, so the last chunk reloads
-    // itself) are loaded into `nxt`, their 18 loads interleaved with the 32
-    // MFMAs of W S so the memory pipe runs beside the matrix pipe.
+    // itself) are loaded into `nxt`: W, U and the decays interleaved 1:1
+    // with the MFMAs of W S, K^ with those of K^T D, so the operand reads
+    // (L2 hits, shared by the 8 column tiles of a head) spread over the chunk
+    // and every operand has a whole chunk to arrive.
     auto chunk = [&](const ScanOps& cur, ScanOps& nxt, int n, int pf) {
         const int par = n & 1;
         const size_t cidx = (size_t)vh * nch + n;
 #pragma unroll
         for (int b = 0; b < 2; ++b) sbuf[par][2 * wave + b][lane] = Sb[b];
-        load_scan_ops(w, nxt, min(pf, nch - 1), vh, kh, tl, nch, wave, g, lane);
+        load_scan_w(w, nxt, min(pf, nch - 1), vh, tl, nch, wave, g, lane);
         // Partial W S over this wave's 32 state rows, all 4 token blocks.
 #pragma unroll
         for (int tb = 0; tb < 4; ++tb) {
@@ -635,11 +645,11 @@ __global__ __launch_bounds__(512) void dn_chunk_scan(PrefillWork w, float* __res
             red[par][wave][tb][lane] = pws;
         }
 #pragma unroll
-        for (int i = 0; i < 18; ++i) {
+        for (int i = 0; i < 11; ++i) {
             __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);   // one VMEM read
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one MFMA
         }
-        __builtin_amdgcn_sched_group_barrier(0x008, 14, 0);
+        __builtin_amdgcn_sched_group_barrier(0x008, 21, 0);
         lds_barrier();
         // Wave w forms D = U - W S of token block w, records it, and shares
         // e^{G_last - G} D with the other waves (each needs all 4 blocks for
@@ -656,6 +666,7 @@ __global__ __launch_bounds__(512) void dn_chunk_scan(PrefillWork w, float* __res
         f32x4 D[4];
 #pragma unroll
         for (int tb = 0; tb < 4; ++tb) D[tb] = dg[par][tb][lane];
+        load_scan_k(w, nxt, min(pf, nch - 1), kh, nch, wave, lane);
         // S = gamma_last S + K^T (e^{G_last - G} D).
 #pragma unroll
         for (int b = 0; b < 2; ++b) {
@@ -664,10 +675,17 @@ __global__ __launch_bounds__(512) void dn_chunk_scan(PrefillWork w, float* __res
             for (int tb = 0; tb < 4; ++tb) acc = mfma16x4(cur.kt[tb][b], D[tb], acc);
             Sb[b] = acc;
         }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, 24, 0);
     };
     // Operands run one chunk ahead: two register sets in rotation, no copies.
     ScanOps o0, o1;
-    load_scan_ops(w, o0, 0, vh, kh, tl, nch, wave, g, lane);
+    load_scan_w(w, o0, 0, vh, tl, nch, wave, g, lane);
+    load_scan_k(w, o0, 0, kh, nch, wave, lane);
     const int npair = nch / 2;
     for (int it = 0; it < npair; ++it) {
         chunk(o0, o1, 2 * it, 2 * it + 1);

@@ -41,10 +41,10 @@ def ctx():
     c.close()
 
 
-@pytest.mark.parametrize("T", [200, 2049])
+@pytest.mark.parametrize("T", [200, 600, 1030, 2049])
 def test_deltanet_prefill_chunk_counts(ctx, T):
-    """4 chunks (one whole triple of the scan loop plus one left over) and 33
-    chunks (whole triples only, ragged last chunk), from a non-zero state."""
+    """4, 10, 17 and 33 chunks (whole pairs of the scan loop, or one chunk
+    left over; ragged last chunk at 1030 and 2049), from a non-zero state."""
     w = synth.deltanet_weights(NK, NV, 128, salt=31)
     st = synth.deltanet_state(NK, NV, 128, salt=500 + T)
     ctx.state_write(0, 5, q35mix.STATE_RECURRENT, st["state"])
