@@ -785,6 +785,8 @@ __global__ __launch_bounds__(256, 3) void dn_chunk_out(PrefillWork w, const floa
         }
     lds_barrier();
     // Row-major epilogue: lanes 0-31 of a wave hold one row, 32-63 the next.
+    // The output is not read again by this path, so it is streamed out with
+    // non-temporal stores (it does not sit dirty in L2 at the kernel's end).
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
         const int o4 = tid + 256 * i, row = o4 >> 5, c4 = o4 & 31, t = t0 + row;
@@ -799,7 +801,7 @@ __global__ __launch_bounds__(256, 3) void dn_chunk_out(PrefillWork w, const floa
         r.y = o.y * rs * wn.y * silu(zr[i].y);
         r.z = o.z * rs * wn.z * silu(zr[i].z);
         r.w = o.w * rs * wn.w * silu(zr[i].w);
-        reinterpret_cast<float4*>(out + ((size_t)t * nv + vh) * kDk)[c4] = r;
+        __builtin_nontemporal_store(v4(r), reinterpret_cast<f32x4*>(out + ((size_t)t * nv + vh) * kDk) + c4);
     }
 }
 
