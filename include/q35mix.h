@@ -164,6 +164,24 @@ int q35m_sync(q35m_ctx* ctx);
 void* q35m_stream(q35m_ctx* ctx);
 int q35m_device_count(int* count);
 
+/* Quantized projections: y[t][n_out] = W x[t] for t < tokens, W given as
+ * GGUF rows of n_in/256 blocks in device memory, Q4_K (144 B a block) or
+ * Q6_K (210 B), x and y fp32 row-major [tokens][n_in] / [tokens][n_out] in
+ * device memory.  Each token row is quantized to Q8_K first, as the reference
+ * does.  Replaces Qwen35Model.DecodeLinear / Linear
+ * (src/Qwen35Sharp.Model/Qwen35Model.Decode.cs:22-88) over MulMatQ4K.Gemv
+ * (src/Qwen35Sharp.Kernels/MulMatQ4K.cs:12-43) and Q6K.Gemv / Q6K.Gemm
+ * (src/Qwen35Sharp.Kernels/Q6K.cs:301-353): results are bit-identical to the
+ * reference's AVX2 GEMV; for Q4_K with tokens > 1 the reference switches to
+ * its packed panel GEMM (MulMatQ4K.Gemm, MulMatQ4K.cs:45-127), whose fp32
+ * accumulation order differs, while this entry point keeps the GEMV order
+ * per token.  w and x must be 16-byte aligned; n_in a multiple of 256 up to
+ * 16384. */
+int q35m_linear_q4k(q35m_ctx* ctx, const void* w, const float* x, float* y, int n_in, int n_out,
+                    int tokens);
+int q35m_linear_q6k(q35m_ctx* ctx, const void* w, const float* x, float* y, int n_in, int n_out,
+                    int tokens);
+
 /* Per-kernel HIP event timers, the device-side counterpart of the
  * reference's Qwen35Model.ProfileEnabled / Ticks* counters
  * (Qwen35Model.cs:42-72).  q35m_profile(ctx, 1) zeroes the totals and times

@@ -228,3 +228,63 @@ def attn_prefill(d: Dims, start, T, q_gate, k, v, w: dict, cache_k, cache_v, n_t
                             _p(_f32(v)), _p(_f32(w["q_norm"])), _p(_f32(w["k_norm"])), _p(ck),
                             _p(cv), _p(out), n_threads)
     return out, ck, cv
+
+
+# ---- quantized projections (q35_oracle_quant.c) --------------------------
+
+QK = 256
+Q4K_BYTES, Q6K_BYTES, Q8K_BYTES = 144, 210, 292
+_U8 = ctypes.POINTER(ctypes.c_uint8)
+
+
+def _bytes(a) -> np.ndarray:
+    a = np.ascontiguousarray(a, dtype=np.uint8)
+    return a
+
+
+def half_to_float(h) -> np.ndarray:
+    h = np.ascontiguousarray(h, dtype=np.uint16).ravel()
+    f = lib().q35o_half_to_float
+    f.restype = ctypes.c_float
+    f.argtypes = [ctypes.c_uint16]
+    return np.array([f(int(v)) for v in h], dtype=np.float32)
+
+
+def q8k_quantize(x) -> np.ndarray:
+    """Q8_K blocks (292 bytes each) of a row of n floats, n a multiple of 256."""
+    x = _f32(x).ravel()
+    out = np.zeros(x.size // QK * Q8K_BYTES, dtype=np.uint8)
+    lib().q35o_q8k_quantize_row(_p(x), out.ctypes.data_as(_U8), ctypes.c_int(x.size))
+    return out
+
+
+def q4k_dot(w, q8, n) -> float:
+    f = lib().q35o_q4k_dot
+    f.restype = ctypes.c_float
+    w, q8 = _bytes(w), _bytes(q8)
+    return f(w.ctypes.data_as(_U8), q8.ctypes.data_as(_U8), ctypes.c_int(n))
+
+
+def q6k_dot(w, q8, n) -> float:
+    f = lib().q35o_q6k_dot
+    f.restype = ctypes.c_float
+    w, q8 = _bytes(w), _bytes(q8)
+    return f(w.ctypes.data_as(_U8), q8.ctypes.data_as(_U8), ctypes.c_int(n))
+
+
+def dequantize(qtype: int, w, k) -> np.ndarray:
+    w = _bytes(w)
+    y = np.empty(k, dtype=np.float32)
+    fn = lib().q35o_q4k_dequantize_row if qtype == 4 else lib().q35o_q6k_dequantize_row
+    fn(w.ctypes.data_as(_U8), _p(y), ctypes.c_int(k))
+    return y
+
+
+def linear_q(qtype: int, w, x, n_in, n_out) -> np.ndarray:
+    """y[t] = W x[t] with W given as GGUF Q4_K (qtype 4) or Q6_K (qtype 6) rows."""
+    w = _bytes(w)
+    x = _f32(x).reshape(-1, n_in)
+    y = np.empty((x.shape[0], n_out), dtype=np.float32)
+    lib().q35o_linear_q(ctypes.c_int(qtype), w.ctypes.data_as(_U8), _p(x), _p(y),
+                        ctypes.c_int(n_in), ctypes.c_int(n_out), ctypes.c_int(x.shape[0]))
+    return y

@@ -13,6 +13,8 @@
 #ifndef Q35_ORACLE_H
 #define Q35_ORACLE_H
 
+#include <stdint.h>
+
 #ifdef __cplusplus
 extern "C" {
 #endif
@@ -83,6 +85,16 @@ void q35o_attn_prefill(const q35o_dims* d, int start, int T, const float* q_gate
                        const float* k, const float* v, const float* q_norm,
                        const float* k_norm, float* cache_k, float* cache_v, float* out,
                        int n_threads);
+
+/* Quantized projections (q35_oracle_quant.c). */
+float q35o_half_to_float(uint16_t h);
+void q35o_q8k_quantize_row(const float* x, void* out, int k);
+float q35o_q4k_dot(const void* w, const void* q8, int n);
+float q35o_q6k_dot(const void* w, const void* q8, int n);
+void q35o_q4k_dequantize_row(const void* w, float* y, int k);
+void q35o_q6k_dequantize_row(const void* w, float* y, int k);
+void q35o_linear_q(int type, const void* w, const float* x, float* y, int n_in, int n_out,
+                   int tokens);
 
 #ifdef __cplusplus
 }

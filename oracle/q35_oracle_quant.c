@@ -1,0 +1,293 @@
+/*
+ * q35_oracle_quant.c -- CPU restatement of the reference's quantized
+ * projections on the decode path: Q8_K activation quantization and the
+ * Q4_K x Q8_K and Q6_K x Q8_K dot products behind Qwen35Model.DecodeLinear
+ * (src/Qwen35Sharp.Model/Qwen35Model.Decode.cs:56-88).
+ *
+ * TEST INFRASTRUCTURE ONLY (the parity oracle).  The product library never
+ * links or calls this file.
+ *
+ * The reference requires AVX2+FMA and runs its AVX2 paths, so those are the
+ * ones restated: the integer sums are exact in any order, and the fp32
+ * accumulation keeps the reference's 8 lanes (lane k of a 32-byte group holds
+ * bytes 4k..4k+3, as _mm256_madd_epi16 leaves them), its FMA and its
+ * horizontal-sum order.  Compiled with -ffp-contract=off; fmaf() only where
+ * the C# calls Fma.MultiplyAdd.
+ *
+ * Block formats (src/Qwen35Sharp.Kernels/BlockLayout.cs:32-78), packed:
+ *   Q4_K (144 B): u16 d, u16 dmin (fp16), u8 scales[12], u8 qs[128]
+ *   Q6_K (210 B): u8 ql[128], u8 qh[64], i8 scales[16], u16 d (fp16)
+ *   Q8_K (292 B): f32 d, i8 qs[256], i16 bsums[16]
+ */
+#include "q35_oracle.h"
+
+#include <math.h>
+#include <stdint.h>
+#include <string.h>
+
+#define QK 256
+
+typedef struct __attribute__((packed)) {
+    uint16_t d, dmin;
+    uint8_t scales[12];
+    uint8_t qs[QK / 2];
+} blk_q4k;
+
+typedef struct __attribute__((packed)) {
+    uint8_t ql[QK / 2];
+    uint8_t qh[QK / 4];
+    int8_t scales[QK / 16];
+    uint16_t d;
+} blk_q6k;
+
+typedef struct __attribute__((packed)) {
+    float d;
+    int8_t qs[QK];
+    int16_t bsums[QK / 16];
+} blk_q8k;
+
+_Static_assert(sizeof(blk_q4k) == 144, "Q4_K block");
+_Static_assert(sizeof(blk_q6k) == 210, "Q6_K block");
+_Static_assert(sizeof(blk_q8k) == 292, "Q8_K block");
+
+/* HalfBits.ToSingle (BlockLayout.cs:155): the exact fp16 -> fp32 conversion
+ * of .NET's Half, subnormals, infinities and NaNs included. */
+float q35o_half_to_float(uint16_t h) {
+    const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    const uint32_t ex = (h >> 10) & 0x1fu, man = h & 0x3ffu;
+    uint32_t u;
+    if (ex == 0x1f) {
+        u = sign | 0x7f800000u | (man << 13);
+    } else if (ex != 0) {
+        u = sign | ((ex + 112u) << 23) | (man << 13);
+    } else if (man == 0) {
+        u = sign;
+    } else {
+        /* subnormal half: man * 2^-24, exact in fp32 */
+        float f = (float)man * 5.9604644775390625e-8f;
+        memcpy(&u, &f, 4);
+        u |= sign;
+    }
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+/* Q8K.ScaleBlock, src/Qwen35Sharp.Kernels/Q8K.cs:81-146 (AVX path): amax =
+ * max |x|; the sign is that of the first element whose magnitude is amax;
+ * iscale = -127 / max, delta = 1 / iscale.  Returns iscale (0 for an
+ * all-zero block, with delta = 0). */
+static float q8k_scale_block(const float* src, float* delta) {
+    float amax = 0.0f;
+    for (int j = 0; j < QK; j++) {
+        const float a = fabsf(src[j]);
+        amax = a > amax ? a : amax;  /* _mm256_max_ps(vacc, |x|) keeps vacc on ties */
+    }
+    if (amax == 0.0f) {
+        *delta = 0.0f;
+        return 0.0f;
+    }
+    float max = amax;
+    for (int j = 0; j < QK; j++) {
+        if (src[j] == amax) { max = amax; break; }
+        if (src[j] == -amax) { max = -amax; break; }
+    }
+    const float iscale = -127.0f / max;
+    *delta = 1.0f / iscale;
+    return iscale;
+}
+
+/* Q8K.QuantizeRow, src/Qwen35Sharp.Kernels/Q8K.cs:12-78 (AVX path):
+ * q = clamp(round_half_even(x * iscale), -127, 127), bsums = sums of 16. */
+void q35o_q8k_quantize_row(const float* x, void* out, int k) {
+    blk_q8k* y = (blk_q8k*)out;
+    const int nb = k / QK;
+    for (int i = 0; i < nb; i++) {
+        const float* src = x + (size_t)i * QK;
+        float delta;
+        const float iscale = q8k_scale_block(src, &delta);
+        if (iscale == 0.0f) {
+            memset(&y[i], 0, sizeof(blk_q8k));
+            continue;
+        }
+        y[i].d = delta;
+        for (int j = 0; j < QK; j++) {
+            const float r = rintf(src[j] * iscale);  /* default mode: ties to even */
+            int v = (int)r;
+            if (v > 127) v = 127;
+            if (v < -127) v = -127;
+            y[i].qs[j] = (int8_t)v;
+        }
+        for (int j = 0; j < QK / 16; j++) {
+            int s = 0;
+            for (int l = 0; l < 16; l++) s += y[i].qs[16 * j + l];
+            y[i].bsums[j] = (int16_t)s;
+        }
+    }
+}
+
+/* Q4K.UnpackScales, src/Qwen35Sharp.Kernels/Q4K.cs:20-33: 8 six-bit scales
+ * (bytes 0..7) and 8 six-bit mins (bytes 8..15). */
+static void q4k_unpack_scales(const uint8_t* packed, uint8_t out[16]) {
+    const uint32_t kmask1 = 0x3f3f3f3fu, kmask2 = 0x0f0f0f0fu, kmask3 = 0x03030303u;
+    uint32_t u[4];
+    memcpy(&u[0], packed, 4);
+    memcpy(&u[1], packed + 4, 4);
+    memcpy(&u[2], packed + 8, 4);
+    u[3] = ((u[2] >> 4) & kmask2) | (((u[1] >> 6) & kmask3) << 4);
+    const uint32_t uaux = u[1] & kmask1;
+    u[1] = (u[2] & kmask2) | (((u[0] >> 6) & kmask3) << 4);
+    u[2] = uaux;
+    u[0] &= kmask1;
+    memcpy(out, u, 16);
+}
+
+/* VecDotQ4K.HorizontalSum, src/Qwen35Sharp.Kernels/VecDotQ4K.cs:145-151. */
+static float hsum8(const float a[8]) {
+    const float s0 = a[0] + a[4], s1 = a[1] + a[5], s2 = a[2] + a[6], s3 = a[3] + a[7];
+    const float t0 = s0 + s2, t1 = s1 + s3;
+    return t0 + t1;
+}
+
+/* VecDotQ4K.DotAvx2, src/Qwen35Sharp.Kernels/VecDotQ4K.cs:67-126. */
+float q35o_q4k_dot(const void* wx, const void* wy, int n) {
+    const blk_q4k* x = (const blk_q4k*)wx;
+    const blk_q8k* y = (const blk_q8k*)wy;
+    const int nb = n / QK;
+    float acc[8] = {0}, acc_min[4] = {0};
+    for (int i = 0; i < nb; i++) {
+        const float d = y[i].d * q35o_half_to_float(x[i].d);
+        const float dmin = -y[i].d * q35o_half_to_float(x[i].dmin);
+        uint8_t sm[16];
+        q4k_unpack_scales(x[i].scales, sm);
+        /* mins . (pairwise bsums): _mm_madd_epi16(mins, hadd(bsums lo, bsums hi)) */
+        int32_t prod[4];
+        for (int k = 0; k < 4; k++) {
+            const int s0 = (int16_t)(y[i].bsums[4 * k] + y[i].bsums[4 * k + 1]);
+            const int s1 = (int16_t)(y[i].bsums[4 * k + 2] + y[i].bsums[4 * k + 3]);
+            prod[k] = sm[8 + 2 * k] * s0 + sm[8 + 2 * k + 1] * s1;
+        }
+        for (int k = 0; k < 4; k++) acc_min[k] = acc_min[k] + dmin * (float)prod[k];
+        /* sumi lane k: bytes 4k..4k+3 of every 32-byte group */
+        int32_t sumi[8] = {0};
+        const uint8_t* q4 = x[i].qs;
+        const int8_t* q8 = y[i].qs;
+        for (int j = 0; j < QK / 64; j++) {
+            const int sl = sm[2 * j], sh = sm[2 * j + 1];
+            for (int k = 0; k < 8; k++) {
+                int pl = 0, ph = 0;
+                for (int b = 4 * k; b < 4 * k + 4; b++) {
+                    pl += (q4[b] & 0xf) * q8[b];
+                    ph += (q4[b] >> 4) * q8[32 + b];
+                }
+                sumi[k] += pl * sl + ph * sh;
+            }
+            q4 += 32;
+            q8 += 64;
+        }
+        for (int k = 0; k < 8; k++) acc[k] = fmaf((float)sumi[k], d, acc[k]);
+    }
+    /* accMin: + MoveHighToLow, then lane 0 + lane 1 */
+    const float m = (acc_min[0] + acc_min[2]) + (acc_min[1] + acc_min[3]);
+    return hsum8(acc) + m;
+}
+
+/* Q6K.DotAvx2, src/Qwen35Sharp.Kernels/Q6K.cs:87-165. */
+float q35o_q6k_dot(const void* wx, const void* wy, int n) {
+    const blk_q6k* x = (const blk_q6k*)wx;
+    const blk_q8k* y = (const blk_q8k*)wy;
+    const int nb = n / QK;
+    float acc[8] = {0};
+    for (int i = 0; i < nb; i++) {
+        const float d = y[i].d * q35o_half_to_float(x[i].d);
+        int32_t sumi[8] = {0};
+        const uint8_t* ql = x[i].ql;
+        const uint8_t* qh = x[i].qh;
+        const int8_t* q8 = y[i].qs;
+        for (int j = 0; j < QK / 128; j++) {
+            for (int b = 0; b < 32; b++) {
+                const int h = qh[b];
+                const int v[4] = {(ql[b] & 15) | ((h & 3) << 4), (ql[32 + b] & 15) | ((h & 12) << 2),
+                                  (ql[b] >> 4) | (h & 48), (ql[32 + b] >> 4) | ((h & 0xc0) >> 2)};
+                const int k = b / 4, half = b / 16;
+                for (int m = 0; m < 4; m++)
+                    sumi[k] += x[i].scales[8 * j + 2 * m + half] * (v[m] * q8[32 * m + b]);
+            }
+            ql += 64;
+            qh += 32;
+            q8 += 128;
+        }
+        /* minus 32 * (bsums . scales), pairwise per lane */
+        for (int k = 0; k < 8; k++)
+            sumi[k] -= (y[i].bsums[2 * k] * x[i].scales[2 * k] +
+                        y[i].bsums[2 * k + 1] * x[i].scales[2 * k + 1]) * 32;
+        for (int k = 0; k < 8; k++) acc[k] = fmaf(d, (float)sumi[k], acc[k]);
+    }
+    return hsum8(acc);
+}
+
+/* Q4K.DequantizeRow, src/Qwen35Sharp.Kernels/Q4K.cs:35-59. */
+void q35o_q4k_dequantize_row(const void* wx, float* y, int k) {
+    const blk_q4k* x = (const blk_q4k*)wx;
+    for (int i = 0; i < k / QK; i++) {
+        uint8_t sm[16];
+        q4k_unpack_scales(x[i].scales, sm);
+        const float d = q35o_half_to_float(x[i].d), mn = q35o_half_to_float(x[i].dmin);
+        const uint8_t* q = x[i].qs;
+        for (int j = 0; j < QK / 64; j++) {
+            const float d1 = d * sm[2 * j], m1 = mn * sm[8 + 2 * j];
+            const float d2 = d * sm[2 * j + 1], m2 = mn * sm[8 + 2 * j + 1];
+            for (int l = 0; l < 32; l++) *y++ = d1 * (q[l] & 0xf) - m1;
+            for (int l = 0; l < 32; l++) *y++ = d2 * (q[l] >> 4) - m2;
+            q += 32;
+        }
+    }
+}
+
+/* Q6K.DequantizeRow, src/Qwen35Sharp.Kernels/Q6K.cs:9-39. */
+void q35o_q6k_dequantize_row(const void* wx, float* y, int k) {
+    const blk_q6k* x = (const blk_q6k*)wx;
+    for (int i = 0; i < k / QK; i++) {
+        const float d = q35o_half_to_float(x[i].d);
+        const uint8_t* ql = x[i].ql;
+        const uint8_t* qh = x[i].qh;
+        const int8_t* sc = x[i].scales;
+        for (int n = 0; n < QK; n += 128) {
+            for (int l = 0; l < 32; l++) {
+                const int is = l / 16;
+                const int q1 = (ql[l] & 0xf) | ((qh[l] & 3) << 4);
+                const int q2 = (ql[l + 32] & 0xf) | (((qh[l] >> 2) & 3) << 4);
+                const int q3 = (ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4);
+                const int q4 = (ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4);
+                y[l] = d * sc[is] * (q1 - 32);
+                y[l + 32] = d * sc[is + 2] * (q2 - 32);
+                y[l + 64] = d * sc[is + 4] * (q3 - 32);
+                y[l + 96] = d * sc[is + 6] * (q4 - 32);
+            }
+            y += 128;
+            ql += 64;
+            qh += 32;
+            sc += 8;
+        }
+    }
+}
+
+/* MulMatQ4K.Gemv (src/Qwen35Sharp.Kernels/MulMatQ4K.cs:12-43) and
+ * Q6K.Gemv/Gemm (src/Qwen35Sharp.Kernels/Q6K.cs:301-413): each token row is
+ * quantized to Q8_K, then every output is one dot product.  (Q6K.Gemm's
+ * four-token DotAvx2x4 gives the same value per token as DotAvx2: the same
+ * integer lanes and the same fma per block.)  type 4 = Q4_K, 6 = Q6_K. */
+void q35o_linear_q(int type, const void* w, const float* x, float* y, int n_in, int n_out,
+                   int tokens) {
+    const int nb = n_in / QK;
+    const size_t wrow = (size_t)nb * (type == 4 ? sizeof(blk_q4k) : sizeof(blk_q6k));
+    blk_q8k q8[64];
+    if (nb > 64) return;
+    for (int t = 0; t < tokens; t++) {
+        q35o_q8k_quantize_row(x + (size_t)t * n_in, q8, n_in);
+        for (int r = 0; r < n_out; r++) {
+            const void* wr = (const uint8_t*)w + (size_t)r * wrow;
+            y[(size_t)t * n_out + r] = type == 4 ? q35o_q4k_dot(wr, q8, n_in) : q35o_q6k_dot(wr, q8, n_in);
+        }
+    }
+}

@@ -133,7 +133,8 @@ const char* kernel_name(int id) {
     static const char* names[K_COUNT] = {
         "deltanet_decode_kernel", "deltanet_conv_writeback", "dn_chunk_prep",
         "dn_chunk_scan",          "dn_chunk_out",            "attn_decode_partial",
-        "attn_decode_merge",      "attn_prefill_prep",       "attn_prefill_flash"};
+        "attn_decode_merge",      "attn_prefill_prep",       "attn_prefill_flash",
+        "q8k_quantize",           "q4k_linear",              "q6k_linear"};
     return (id >= 0 && id < K_COUNT) ? names[id] : nullptr;
 }
 
@@ -483,6 +484,33 @@ int q35m_attn_prefill(q35m_ctx* ctx, int layer, int seq, int T, const float* q_g
     HIP_TRY(q35::ensure_work(ctx, q35::attn_prefill_work_bytes(ctx->d, T)), "workspace");
     HIP_TRY(q35::launch_attn_prefill(ctx, layer, seq, start, T, q_gate, k, v, out), "attn_prefill");
     return Q35M_OK;
+}
+
+static int linear_q(q35m_ctx* ctx, int qtype, const void* w, const float* x, float* y, int n_in,
+                    int n_out, int tokens) {
+    int r = check_ctx(ctx);
+    if (r) return r;
+    if (!w || !x || !y) return fail(Q35M_ERR_INVALID, "null pointer");
+    if (((uintptr_t)w & 15) || ((uintptr_t)x & 15))
+        return fail(Q35M_ERR_INVALID, "weights and input must be 16-byte aligned");
+    if (n_in < 256 || n_in > 16384 || n_in % 256)
+        return fail(Q35M_ERR_UNSUPPORTED, "n_in must be a multiple of 256 in [256, 16384] (got %d)", n_in);
+    if (n_out < 1) return fail(Q35M_ERR_INVALID, "n_out must be >= 1 (got %d)", n_out);
+    if (tokens < 1 || tokens > 65535)
+        return fail(Q35M_ERR_INVALID, "tokens must be in [1, 65535] (got %d)", tokens);
+    HIP_TRY(q35::ensure_work(ctx, q35::linear_q_work_bytes(n_in, tokens)), "workspace");
+    HIP_TRY(q35::launch_linear_q(ctx, qtype, w, x, y, n_in, n_out, tokens), "linear_q");
+    return Q35M_OK;
+}
+
+int q35m_linear_q4k(q35m_ctx* ctx, const void* w, const float* x, float* y, int n_in, int n_out,
+                    int tokens) {
+    return linear_q(ctx, 4, w, x, y, n_in, n_out, tokens);
+}
+
+int q35m_linear_q6k(q35m_ctx* ctx, const void* w, const float* x, float* y, int n_in, int n_out,
+                    int tokens) {
+    return linear_q(ctx, 6, w, x, y, n_in, n_out, tokens);
 }
 
 static int state_locate(q35m_ctx* ctx, int layer, int seq, int kind, char** base, size_t* bytes) {

@@ -66,6 +66,9 @@ enum KernelId {
     K_ATTN_DECODE_MERGE,
     K_ATTN_PREFILL_PREP,
     K_ATTN_PREFILL_FLASH,
+    K_Q8K_QUANTIZE,
+    K_Q4K_LINEAR,
+    K_Q6K_LINEAR,
     K_COUNT
 };
 const char* kernel_name(int id);
@@ -121,6 +124,9 @@ size_t attn_decode_work_bytes(const Dims& d, int n, int max_kv_len);
 hipError_t launch_attn_prefill(q35m_ctx* c, int layer, int seq, int start, int T,
                                const float* q_gate, const float* k, const float* v, float* out);
 size_t attn_prefill_work_bytes(const Dims& d, int T);
+hipError_t launch_linear_q(q35m_ctx* c, int qtype, const void* w, const float* x, float* y,
+                           int n_in, int n_out, int tokens);
+size_t linear_q_work_bytes(int n_in, int tokens);
 
 // Ensures ctx->work holds at least `bytes` (synchronises before regrowing).
 hipError_t ensure_work(q35m_ctx* c, size_t bytes);

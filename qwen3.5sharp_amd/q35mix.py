@@ -62,6 +62,10 @@ def lib() -> ctypes.CDLL:
         _lib.q35m_state_device_ptr.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
                                                ctypes.c_int, ctypes.POINTER(ctypes.c_void_p),
                                                ctypes.POINTER(ctypes.c_size_t)]
+        for name in ("q35m_linear_q4k", "q35m_linear_q6k"):
+            getattr(_lib, name).argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                            ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
+                                            ctypes.c_int]
     return _lib
 
 
@@ -128,6 +132,20 @@ class DeviceArray:
         if self.ptr:
             lib().q35m_free(self.ptr)
             self.ptr = None
+
+
+class DeviceBytes(DeviceArray):
+    """Raw byte buffer in device memory (quantized weight blocks)."""
+
+    def __init__(self, ctx: "Context", data: np.ndarray):
+        a = np.ascontiguousarray(data, dtype=np.uint8).ravel()
+        self.ctx = ctx
+        self.shape = a.shape
+        self.nbytes = a.nbytes
+        p = ctypes.c_void_p()
+        check(lib().q35m_malloc(ctypes.byref(p), max(self.nbytes, 4)))
+        self.ptr = p.value
+        check(lib().q35m_copy_h2d(self.ctx.handle, self.ptr, a.ctypes.data, a.nbytes))
 
     def __del__(self):
         try:
@@ -223,6 +241,15 @@ class Context:
     def attn_prefill(self, layer, seq, T, q_gate, k, v, out) -> None:
         check(lib().q35m_attn_prefill(ctypes.c_void_p(self.handle), layer, seq, T,
                                       *[ctypes.c_void_p(x.ptr) for x in (q_gate, k, v, out)]))
+
+    def bytes_array(self, data) -> DeviceBytes:
+        return DeviceBytes(self, data)
+
+    def linear_q(self, qtype: int, w, x, y, n_in, n_out, tokens) -> None:
+        """y[tokens][n_out] = W x for GGUF Q4_K (qtype 4) or Q6_K (qtype 6) weight rows."""
+        fn = lib().q35m_linear_q4k if qtype == 4 else lib().q35m_linear_q6k
+        check(fn(ctypes.c_void_p(self.handle), ctypes.c_void_p(w.ptr), ctypes.c_void_p(x.ptr),
+                 ctypes.c_void_p(y.ptr), n_in, n_out, tokens))
 
     # ---- per-kernel event timers -----------------------------------------
     def profile(self, enable: bool) -> None:

@@ -1,0 +1,118 @@
+"""numpy helpers for the GGUF Q4_K / Q6_K / Q8_K block formats used by the
+quantized-projection tests: random blocks, independent decoders and packers.
+
+Layouts (src/Qwen35Sharp.Kernels/BlockLayout.cs:32-78 of the reference):
+  Q4_K (144 B): f16 d, f16 dmin, u8 scales[12], u8 qs[128]
+  Q6_K (210 B): u8 ql[128], u8 qh[64], i8 scales[16], f16 d
+  Q8_K (292 B): f32 d, i8 qs[256], i16 bsums[16]
+"""
+from __future__ import annotations
+
+import numpy as np
+
+QK = 256
+BYTES = {4: 144, 6: 210}
+
+
+def parse_q8k(buf):
+    b = np.asarray(buf, dtype=np.uint8).reshape(-1, 292)
+    d = b[:, 0:4].copy().view(np.float32).ravel()
+    q = b[:, 4:260].copy().view(np.int8)
+    bs = b[:, 260:292].copy().view(np.int16)
+    return d, q, bs
+
+
+def _f16(v):
+    return np.frombuffer(np.float16(v).tobytes(), np.uint8)
+
+
+def random_blocks(rng, qtype, nblocks, dscale=0.02):
+    """Random but well-formed blocks: finite positive fp16 scales of a realistic
+    size, every other byte uniform."""
+    n = BYTES[qtype]
+    b = rng.integers(0, 256, size=(nblocks, n), dtype=np.uint8)
+    d = (rng.uniform(0.2, 1.0, nblocks) * dscale).astype(np.float16)
+    if qtype == 4:
+        b[:, 0:2] = d.view(np.uint8).reshape(-1, 2)
+        dm = (rng.uniform(0.2, 1.0, nblocks) * dscale).astype(np.float16)
+        b[:, 2:4] = dm.view(np.uint8).reshape(-1, 2)
+    else:
+        b[:, 208:210] = d.view(np.uint8).reshape(-1, 2)
+    return b.ravel()
+
+
+def q4k_scale_min(sc: np.ndarray, j: int):
+    """Q4K.GetScaleMin (src/Qwen35Sharp.Kernels/Q4K.cs:7-18)."""
+    if j < 4:
+        return int(sc[j] & 63), int(sc[j + 4] & 63)
+    return (int((sc[j + 4] & 0xF) | ((sc[j - 4] >> 6) << 4)),
+            int((sc[j + 4] >> 4) | ((sc[j] >> 6) << 4)))
+
+
+def pack_q4k_scales(scales, mins):
+    p = np.zeros(12, dtype=np.uint8)
+    for g in range(8):
+        ls, lm = scales[g], mins[g]
+        if g < 4:
+            p[g] |= ls
+            p[g + 4] |= lm
+        else:
+            p[g + 4] = (ls & 0xF) | ((lm & 0xF) << 4)
+            p[g - 4] |= (ls >> 4) << 6
+            p[g] |= (lm >> 4) << 6
+    return p
+
+
+def pack_q6k_values(vals):
+    """ql[128] | qh[64] for 256 six-bit values (the inverse of the decoder below)."""
+    ql = np.zeros(128, dtype=np.uint8)
+    qh = np.zeros(64, dtype=np.uint8)
+    v = np.asarray(vals, dtype=np.int64)
+    for half in range(2):
+        base = 128 * half
+        for l in range(32):
+            q1, q2, q3, q4 = v[base + l], v[base + l + 32], v[base + l + 64], v[base + l + 96]
+            ql[64 * half + l] = (q1 & 15) | ((q3 & 15) << 4)
+            ql[64 * half + l + 32] = (q2 & 15) | ((q4 & 15) << 4)
+            qh[32 * half + l] = (q1 >> 4) | ((q2 >> 4) << 2) | ((q3 >> 4) << 4) | ((q4 >> 4) << 6)
+    return np.concatenate([ql, qh])
+
+
+def _dequant(qtype, w, dtype):
+    b = np.asarray(w, dtype=np.uint8).reshape(-1, BYTES[qtype])
+    out = np.empty((b.shape[0], QK), dtype=dtype)
+    for i, blk in enumerate(b):
+        if qtype == 4:
+            d = dtype(blk[0:2].copy().view(np.float16)[0])
+            dmin = dtype(blk[2:4].copy().view(np.float16)[0])
+            sc, qs = blk[4:16], blk[16:144]
+            for j in range(4):
+                s0, m0 = q4k_scale_min(sc, 2 * j)
+                s1, m1 = q4k_scale_min(sc, 2 * j + 1)
+                q = qs[32 * j:32 * j + 32]
+                out[i, 64 * j:64 * j + 32] = dtype(d * dtype(s0)) * (q & 15) - dtype(dmin * dtype(m0))
+                out[i, 64 * j + 32:64 * j + 64] = dtype(d * dtype(s1)) * (q >> 4) - dtype(dmin * dtype(m1))
+        else:
+            ql, qh = blk[0:128].astype(np.int64), blk[128:192].astype(np.int64)
+            sc = blk[192:208].view(np.int8).astype(np.int64)
+            d = dtype(blk[208:210].copy().view(np.float16)[0])
+            vals = np.empty(256, dtype=np.int64)
+            for half in range(2):
+                l = np.arange(32)
+                a, c, h = ql[64 * half + l], ql[64 * half + 32 + l], qh[32 * half + l]
+                vals[128 * half + l] = (a & 15) | ((h & 3) << 4)
+                vals[128 * half + 32 + l] = (c & 15) | (((h >> 2) & 3) << 4)
+                vals[128 * half + 64 + l] = (a >> 4) | (((h >> 4) & 3) << 4)
+                vals[128 * half + 96 + l] = (c >> 4) | (((h >> 6) & 3) << 4)
+            scale = np.repeat(sc, 16).astype(dtype)
+            out[i] = dtype(d) * scale * (vals - 32).astype(dtype)
+    return out.ravel()
+
+
+def dequant(qtype, w):
+    """fp32, in the reference's DequantizeRow operation order."""
+    return _dequant(qtype, w, np.float32)
+
+
+def dequant_f64(qtype, w):
+    return _dequant(qtype, w, np.float64)

@@ -70,6 +70,8 @@ def test_null_context_is_rejected():
     assert L.q35m_stream(None) is None
     n = ctypes.c_int()
     assert L.q35m_kv_len(None, 0, ctypes.byref(n)) == q35mix.ERR_INVALID
+    assert L.q35m_linear_q4k(None, None, None, None, 256, 1, 1) == q35mix.ERR_INVALID
+    assert L.q35m_linear_q6k(None, None, None, None, 256, 1, 1) == q35mix.ERR_INVALID
 
 
 def test_no_device_here_is_an_error_not_a_fallback():

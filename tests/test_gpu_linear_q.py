@@ -1,0 +1,100 @@
+"""Quantized projections (q35m_linear_q4k / q35m_linear_q6k) through the C ABI
+against the oracle: bit-exact (the kernels keep the reference's integer lanes
+and fp32 accumulation order), at the projection shapes of the 4B mixers
+(hidden 2560: qkv 8192, gate 4096, beta/alpha 32, ssm_out and attn_output
+4096 -> 2560, attn k/v 1024), ragged small shapes, several tokens, zero and
+extreme activation blocks, and weight buffers whose size is not a multiple of
+16 bytes."""
+import sys
+
+import numpy as np
+import pytest
+
+import oracle
+import q35mix
+import quant_blocks as qb
+
+pytestmark = pytest.mark.gpu
+
+
+def say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    c = q35mix.Context(q35mix.qwen35_config(num_layers=1, is_recurrent=[1]), n_seqs=1,
+                       kv_capacity=16)
+    yield c
+    c.close()
+
+
+def run(ctx, qtype, w, x, n_in, n_out):
+    tokens = x.shape[0]
+    dw = ctx.bytes_array(w)
+    dx = ctx.array((tokens, n_in), x)
+    dy = ctx.array((tokens, n_out))
+    ctx.linear_q(qtype, dw, dx, dy, n_in, n_out, tokens)
+    y = dy.download()
+    for a in (dw, dx, dy):
+        a.free()
+    return y
+
+
+SHAPES = [(2560, 8192, 1), (2560, 4096, 1), (2560, 32, 1), (4096, 2560, 1), (2560, 1024, 1),
+          (256, 7, 1), (512, 33, 5), (2560, 1024, 3), (16384, 19, 2)]
+
+
+@pytest.mark.parametrize("qtype", [4, 6])
+@pytest.mark.parametrize("n_in,n_out,tokens", SHAPES)
+def test_linear_q_bit_exact(ctx, qtype, n_in, n_out, tokens):
+    say(f"linear_q Q{qtype}_K n_in={n_in} n_out={n_out} tokens={tokens}")
+    rng = np.random.default_rng(1000 * qtype + n_in + n_out + tokens)
+    w = qb.random_blocks(rng, qtype, n_out * n_in // 256)
+    x = rng.standard_normal((tokens, n_in)).astype(np.float32)
+    got = run(ctx, qtype, w, x, n_in, n_out)
+    want = oracle.linear_q(qtype, w, x, n_in, n_out)
+    bad = np.flatnonzero(got.view(np.uint32) != want.view(np.uint32))
+    say(f"  mismatches {bad.size} of {got.size}; max|d| {np.max(np.abs(got - want)):.3e}")
+    assert bad.size == 0
+
+
+@pytest.mark.parametrize("qtype", [4, 6])
+def test_linear_q_activation_edges(ctx, qtype):
+    """Zero blocks (scale 0), a first extremum that is positive (negative
+    scale) or repeated with both signs, ties at .5 after scaling, huge and tiny
+    magnitudes, and an fp16 subnormal weight scale."""
+    n_in, n_out = 2048, 40
+    rng = np.random.default_rng(77 + qtype)
+    w = qb.random_blocks(rng, qtype, n_out * n_in // 256)
+    w.reshape(-1, qb.BYTES[qtype])[3, (0 if qtype == 4 else 208):(2 if qtype == 4 else 210)] = \
+        np.frombuffer(np.float16(3e-6).tobytes(), np.uint8)
+    x = rng.standard_normal((2, n_in)).astype(np.float32)
+    x[0, 0:256] = 0.0
+    x[0, 256:512] *= 1e-30
+    x[0, 512 + 5], x[0, 512 + 9] = 50.0, -50.0
+    x[0, 768 + 2], x[0, 768 + 1] = 50.0, -50.0
+    blk = x[1, 1024:1280]
+    blk[:] = np.arange(256, dtype=np.float32) - 128.0   # iscale exactly 127/128... ties
+    blk[0] = -127.0
+    blk[1:] = np.clip(blk[1:], -126.5, 126.5)
+    x[1, 1280:1536] *= 1e20
+    got = run(ctx, qtype, w, x, n_in, n_out)
+    want = oracle.linear_q(qtype, w, x, n_in, n_out)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_linear_q_rejects_bad_arguments(ctx):
+    dw = ctx.bytes_array(np.zeros(144 * 4, np.uint8))
+    dx = ctx.array((1, 512))
+    dy = ctx.array((1, 2))
+    L = q35mix.lib()
+    h = ctx.handle
+    assert L.q35m_linear_q4k(h, dw.ptr, dx.ptr, dy.ptr, 300, 2, 1) == q35mix.ERR_UNSUPPORTED
+    assert L.q35m_linear_q4k(h, dw.ptr + 4, dx.ptr, dy.ptr, 512, 2, 1) == q35mix.ERR_INVALID
+    assert L.q35m_linear_q6k(h, dw.ptr, dx.ptr, dy.ptr, 512, 0, 1) == q35mix.ERR_INVALID
+    assert L.q35m_linear_q6k(h, dw.ptr, dx.ptr, dy.ptr, 512, 2, 0) == q35mix.ERR_INVALID
+    assert L.q35m_linear_q6k(h, None, dx.ptr, dy.ptr, 512, 2, 1) == q35mix.ERR_INVALID
+    for a in (dw, dx, dy):
+        a.free()

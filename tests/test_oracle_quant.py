@@ -1,0 +1,149 @@
+"""Pins the oracle's quantized-projection restatement (oracle/q35_oracle_quant.c).
+
+The reference has no tests for Q4_K / Q6_K / Q8_K, so the restatement is pinned
+by what the formats and the mathematics fix:
+  - fp16 decoding against numpy's float16 for every bit pattern;
+  - Q8_K: the first extremum maps to exactly -127, ties round to even, the
+    sign of the scale follows the first extremum, bsums are the sums of 16,
+    and every value reconstructs within half a step;
+  - Q4_K / Q6_K dequantization against independent numpy decoders of the bit
+    layouts (Q4_K scales through the per-index GetScaleMin formula, not the
+    word-mask unpacking the dot product uses);
+  - the integer dot products against fp64 dots of the dequantized weights
+    with the dequantized activations (equal in exact arithmetic), and exact
+    values on hand-built blocks.
+The fp32 lane order of the reference's AVX2 accumulation is restated, not
+pinned bit for bit (no reference run is possible here).
+"""
+from __future__ import annotations
+
+import os
+import sys
+
+import numpy as np
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+sys.path.insert(0, os.path.join(ROOT, "oracle"))
+sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+
+import oracle  # noqa: E402
+import quant_blocks as qb  # noqa: E402
+
+
+def test_half_to_float_all_patterns():
+    h = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    got = oracle.half_to_float(h)
+    want = h.view(np.float16).astype(np.float32)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+
+
+def test_q8k_zero_block_and_rules():
+    x = np.zeros(512, dtype=np.float32)
+    x[256 + 7] = -127.0          # first extremum of block 1, negative -> iscale = 1
+    x[256 + 9] = 127.0
+    x[256 + 1], x[256 + 2], x[256 + 3], x[256 + 4] = 2.5, 3.5, -2.5, 0.49999997
+    d, q, bs = qb.parse_q8k(oracle.q8k_quantize(x))
+    assert d[0] == 0 and not q[0].any() and not bs[0].any()
+    assert d[1] == 1.0
+    assert q[1][7] == -127 and q[1][9] == 127
+    assert list(q[1][1:5]) == [2, 4, -2, 0]     # ties to even
+    # first extremum positive -> negative scale
+    y = np.zeros(256, dtype=np.float32)
+    y[3], y[5] = 4.0, -4.0
+    d2, q2, _ = qb.parse_q8k(oracle.q8k_quantize(y))
+    assert d2[0] < 0 and q2[0][3] == -127 and q2[0][5] == 127
+
+
+def test_q8k_random_against_numpy():
+    rng = np.random.default_rng(11)
+    x = (rng.standard_normal(256 * 64) * rng.uniform(0.01, 50, 256 * 64)).astype(np.float32)
+    d, q, bs = qb.parse_q8k(oracle.q8k_quantize(x))
+    xb = x.reshape(64, 256)
+    for i in range(64):
+        amax = np.abs(xb[i]).max()
+        first = int(np.argmax(np.abs(xb[i]) == amax))
+        mx = xb[i][first]
+        iscale = np.float32(-127.0) / np.float32(mx)
+        qq = np.clip(np.rint(xb[i] * iscale), -127, 127).astype(np.int8)
+        assert np.array_equal(q[i], qq)
+        assert d[i] == np.float32(1.0) / iscale
+        assert q[i][first] == -127
+        assert np.array_equal(bs[i], q[i].astype(np.int32).reshape(16, 16).sum(1))
+        assert np.all(np.abs(xb[i].astype(np.float64) - d[i] * q[i]) <= 0.5 * abs(d[i]) * (1 + 1e-6))
+
+
+@pytest.mark.parametrize("qtype", [4, 6])
+def test_dequantize_against_numpy_decoder(qtype):
+    rng = np.random.default_rng(3 + qtype)
+    w = qb.random_blocks(rng, qtype, 24)
+    got = oracle.dequantize(qtype, w, 24 * 256)
+    want = qb.dequant(qtype, w)
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("qtype", [4, 6])
+def test_dot_against_fp64(qtype):
+    rng = np.random.default_rng(20 + qtype)
+    n = 256 * 16
+    for trial in range(8):
+        w = qb.random_blocks(rng, qtype, 16)
+        x = (rng.standard_normal(n) * (1 + 3 * trial)).astype(np.float32)
+        q8 = oracle.q8k_quantize(x)
+        d, q, _ = qb.parse_q8k(q8)
+        xd = (d[:, None].astype(np.float64) * q.astype(np.float64)).ravel()
+        wd = qb.dequant_f64(qtype, w)
+        exact = float(np.dot(wd, xd))
+        scale = float(np.dot(np.abs(wd), np.abs(xd)))
+        got = oracle.q4k_dot(w, q8, n) if qtype == 4 else oracle.q6k_dot(w, q8, n)
+        assert abs(got - exact) <= 2e-6 * scale + 1e-30, (trial, got, exact)
+
+
+def test_q4k_dot_hand_built():
+    # d = 1, dmin = 0.5, every scale 1, every min 2, every nibble 1 (low) / 3 (high);
+    # q8 all 1 with D = 1: sum = 128*1 + 128*3 - 8 sub-blocks * 2 * 0.5 * 32 = 256.
+    blk = np.zeros(144, dtype=np.uint8)
+    blk[0:2] = np.frombuffer(np.float16(1.0).tobytes(), np.uint8)
+    blk[2:4] = np.frombuffer(np.float16(0.5).tobytes(), np.uint8)
+    blk[4:16] = qb.pack_q4k_scales([1] * 8, [2] * 8)
+    blk[16:] = 0x31
+    x = np.full(256, -1.0, dtype=np.float32)        # first extremum negative: D = 1/127*...
+    x[0] = -127.0
+    x[1:] = -127.0                                  # all equal -> q = -127, D = 1
+    q8 = oracle.q8k_quantize(x)
+    d, q, _ = qb.parse_q8k(q8)
+    assert d[0] == 1.0 and np.all(q[0] == -127)
+    # dot = -127 * (128*1 + 128*3) - 0.5*2*(-127*256) = -127*512 + 127*256
+    assert oracle.q4k_dot(blk, q8, 256) == np.float32(-127 * 512 + 127 * 256)
+
+
+def test_q6k_dot_hand_built():
+    # d = 0.25, scales alternate 2 / -1, every 6-bit value 40 (-> 8 after the -32)
+    blk = np.zeros(210, dtype=np.uint8)
+    vals = np.full(256, 40, dtype=np.int64)
+    blk[:192] = qb.pack_q6k_values(vals)
+    blk[192:208] = np.array([2, -1] * 8, dtype=np.int8).view(np.uint8)
+    blk[208:210] = np.frombuffer(np.float16(0.25).tobytes(), np.uint8)
+    x = np.full(256, -127.0, dtype=np.float32)
+    q8 = oracle.q8k_quantize(x)
+    # sum over 16 sub-blocks of 16 values: scale * 8 * (-127); 8 sub-blocks at 2, 8 at -1
+    want = 0.25 * 16 * 8 * (-127) * (8 * 2 + 8 * -1)
+    assert oracle.q6k_dot(blk, q8, 256) == np.float32(want)
+
+
+@pytest.mark.parametrize("qtype", [4, 6])
+def test_linear_q_against_fp64(qtype):
+    rng = np.random.default_rng(40 + qtype)
+    n_in, n_out, tokens = 512, 96, 3
+    w = qb.random_blocks(rng, qtype, n_out * n_in // 256)
+    x = rng.standard_normal((tokens, n_in)).astype(np.float32)
+    y = oracle.linear_q(qtype, w, x, n_in, n_out)
+    wd = qb.dequant_f64(qtype, w).reshape(n_out, n_in)
+    for t in range(tokens):
+        d, q, _ = qb.parse_q8k(oracle.q8k_quantize(x[t]))
+        xd = (d[:, None].astype(np.float64) * q).ravel()
+        exact = wd @ xd
+        scale = np.abs(wd) @ np.abs(xd)
+        assert np.all(np.abs(y[t] - exact) <= 2e-6 * scale)
