@@ -192,6 +192,24 @@ def bench_attn_prefill(steps, warmup, T=2048):
     return ms, kt
 
 
+def bench_linear_q(qtype, n_in, n_out, steps, warmup, copies):
+    """One-token projection (the decode GEMV) rotating over `copies` weight
+    copies, more bytes than the 256 MB MALL."""
+    ctx = q35mix.Context(q35mix.qwen35_config(num_layers=1, is_recurrent=[1]), 1, 16)
+    w = synth.quant_weights(qtype, n_out, n_in)
+    ws = [ctx.bytes_array(w) for _ in range(copies)]
+    x = ctx.array((1, n_in), synth.normal(310, n_in))
+    y = ctx.array((1, n_out))
+
+    def step(i):
+        ctx.linear_q(qtype, ws[i % copies], x, y, n_in, n_out, 1)
+
+    ms = time_calls(ctx, step, steps, warmup)
+    kt = kernel_times(ctx, step, steps)
+    ctx.close()
+    return ms, kt, w.nbytes + 4 * (n_in + n_out)
+
+
 def bench_stack(n_steps=128, warmup=4, n_seqs=8, ctx_len=32768, n_layers=32):
     """32-layer mixer stack, 8 sequences decoding from context 32640 to 32768."""
     is_rec = [(i + 1) % 4 != 0 for i in range(n_layers)]
@@ -325,7 +343,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default="", help="comma list of: dn_prefill,dn_decode,attn_decode,"
-                                               "attn_prefill,stack,peaks")
+                                               "attn_prefill,linear_q,stack,peaks")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="also run one device-to-device copy of MIB MiB (a plain copy kernel "
                          "of known traffic, to scale FETCH_SIZE/WRITE_SIZE counters)")
@@ -429,6 +447,19 @@ def main():
             "mfma_frac": ATTN_PREFILL_FLOP / (ms / 1e3) / FP32_PEAK,
             "kernels_ms": {k: v[0] for k, v in kt.items()}}
         log(f"[bench] GQA prefill: {workloads['attn_prefill_2048']}")
+
+    for qtype, n_in, n_out, copies in ((4, 2560, 8192, 32), (6, 4096, 2560, 40)):
+        if not want("linear_q"):
+            break
+        name = f"linear_q{qtype}k_{n_in}x{n_out}"
+        log(f"[bench] Q{qtype}_K projection {n_in} -> {n_out}, one token ...")
+        ms, kt, by = bench_linear_q(qtype, n_in, n_out, max(K, 200), max(W, 20), copies)
+        kus = {k: v[0] * 1e3 for k, v in kt.items()}
+        gemv = f"linear_q<{qtype}>"
+        workloads[name] = {
+            "us_per_call": ms * 1e3, "bytes": by, "hbm_frac_call": by / (ms / 1e3) / HBM_PEAK,
+            "kernels_us": kus, "hbm_frac_kernel": by / (kus[gemv] / 1e6) / HBM_PEAK}
+        log(f"[bench] {name}: {workloads[name]}")
 
     if want("stack"):
         log("[bench] 32-layer mixer stack, 8 seqs x ctx 32768, 128 decode steps ...")

@@ -21,11 +21,13 @@
 // block in block order, then its horizontal-sum order.
 //
 // Work split: the projection is HBM-bound on the weights (4.5 / 6.56 bits a
-// weight).  A workgroup takes whole rows (up to 256 blocks), stages their
-// contiguous bytes in LDS with 16-byte coalesced loads, and one thread per
-// block forms the block's integer lanes; one thread per row then runs the
-// fp32 accumulation over the row's blocks in order.  Extra tokens reuse the
-// staged weights.
+// weight).  q8k_quantize turns each token row into Q8_K blocks (one wave a
+// block) in the workspace.  linear_q then runs one 64-thread workgroup per
+// group of up to 8 whole rows (at most 64 blocks): it stages the rows'
+// contiguous bytes in LDS with 16-byte loads and the token's Q8_K row from
+// L2, forms one block's integer lanes per thread, and runs each row's fp32
+// accumulation on 8 threads, one per reference lane, in block order.  Extra
+// tokens reuse the staged weights.
 #include "common.h"
 #include "q35mix_internal.h"
 
@@ -33,64 +35,69 @@ namespace q35 {
 namespace {
 
 constexpr int QK = 256;
-constexpr int Q4K_BYTES = 144, Q6K_BYTES = 210, Q8K_BYTES = 292;
-constexpr int Q8K_WORDS = Q8K_BYTES / 4;
-constexpr int LQ_THREADS = 256;
-constexpr int LQ_MAX_NB = 64;      // n_in up to 16384
+constexpr int Q4K_BYTES = 144, Q6K_BYTES = 210;
+constexpr int Q8K_WORDS = 76;      // workspace stride of a Q8_K block: 292 B padded to 19 x 16 B
+constexpr int LQ_THREADS = 64;
+constexpr int LQ_MAX_ROWS = 8;     // rows per workgroup (8 threads a row in the fp32 pass)
+constexpr int LANES_LD = 13;       // padded stride of the per-block integer lanes in LDS
 
 __device__ __forceinline__ float half_bits_to_float(uint32_t h) {
     return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(h)));
 }
 
-// Q8K.QuantizeRow / ScaleBlock (Q8K.cs:12-146): one wave per (256-value
-// block, token).  amax = max |x|; the scale's sign is that of the first
-// element of magnitude amax; iscale = -127 / max (IEEE division), delta =
-// 1 / iscale; q = clamp(round-half-even(x * iscale), -127, 127); bsums =
-// sums of 16.
+// Q8K.QuantizeRow / ScaleBlock (Q8K.cs:12-146), four 256-value blocks of one
+// token per wave: a 16-lane group per block, 16 consecutive values a lane (so
+// a lane's values are exactly one bsums group).  amax = max |x|; the scale's
+// sign is that of the first element of magnitude amax; iscale = -127 / max
+// (IEEE division), delta = 1 / iscale; q = clamp(round-half-even(x * iscale),
+// -127, 127).  Output: Q8_K blocks [tokens][nb] in the workspace, each
+// padded to 304 bytes so that rows stage with 16-byte loads.
 __global__ __launch_bounds__(kWave) void q8k_quantize(const float* __restrict__ x,
-                                                      unsigned char* __restrict__ out,
-                                                      int n_in) {
-    const int b = blockIdx.x, t = blockIdx.y, lane = threadIdx.x;
-    const int nb = n_in / QK;
-    const float4 v = reinterpret_cast<const float4*>(x + (size_t)t * n_in + (size_t)b * QK)[lane];
-    float amax = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+                                                      uint32_t* __restrict__ q8, int nb) {
+    const int lane = threadIdx.x, grp = lane >> 4, li = lane & 15;
+    const int t = blockIdx.y, b = 4 * blockIdx.x + grp, bb = min(b, nb - 1);
+    const float4* src = reinterpret_cast<const float4*>(x + ((size_t)t * nb + bb) * QK + 16 * li);
+    float v[16];
 #pragma unroll
-    for (int m = 1; m < kWave; m <<= 1) amax = fmaxf(amax, __shfl_xor(amax, m, kWave));
-    const int e = fabsf(v.x) == amax ? 0 : fabsf(v.y) == amax ? 1 : fabsf(v.z) == amax ? 2
-                : fabsf(v.w) == amax ? 3 : 4;
-    int first = e < 4 ? 4 * lane + e : 4 * kWave;
+    for (int i = 0; i < 4; ++i) {
+        const float4 f = src[i];
+        v[4 * i] = f.x; v[4 * i + 1] = f.y; v[4 * i + 2] = f.z; v[4 * i + 3] = f.w;
+    }
+    float amax = 0.0f;
 #pragma unroll
-    for (int m = 1; m < kWave; m <<= 1) first = min(first, __shfl_xor(first, m, kWave));
-    const int fe = first & 3;
-    const float mine = fe == 0 ? v.x : fe == 1 ? v.y : fe == 2 ? v.z : v.w;
-    const float mx = __shfl(mine, min(first >> 2, kWave - 1), kWave);
-
-    unsigned char* blk = out + ((size_t)t * nb + b) * Q8K_BYTES;
-    int q0 = 0, q1 = 0, q2 = 0, q3 = 0;
+    for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(v[i]));
+#pragma unroll
+    for (int m = 1; m < 16; m <<= 1) amax = fmaxf(amax, __shfl_xor(amax, m, kWave));
+    int e = 16;
+#pragma unroll
+    for (int i = 15; i >= 0; --i) e = fabsf(v[i]) == amax ? i : e;
+    int first = e < 16 ? 16 * li + e : QK;
+#pragma unroll
+    for (int m = 1; m < 16; m <<= 1) first = min(first, __shfl_xor(first, m, kWave));
+    float mine = v[0];
+#pragma unroll
+    for (int i = 1; i < 16; ++i) mine = (first & 15) == i ? v[i] : mine;
+    const float mx = __shfl(mine, (lane & ~15) + min(first >> 4, 15), kWave);
+    uint32_t pk[4] = {0u, 0u, 0u, 0u};
+    int bsum = 0;
     float delta = 0.0f;
     if (amax != 0.0f) {
         const float iscale = -127.0f / mx;
         delta = 1.0f / iscale;
-        q0 = min(max((int)rintf(v.x * iscale), -127), 127);
-        q1 = min(max((int)rintf(v.y * iscale), -127), 127);
-        q2 = min(max((int)rintf(v.z * iscale), -127), 127);
-        q3 = min(max((int)rintf(v.w * iscale), -127), 127);
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int q = min(max((int)rintf(v[i] * iscale), -127), 127);
+            bsum += q;
+            pk[i >> 2] |= (uint32_t)(q & 0xff) << (8 * (i & 3));
+        }
     }
-    reinterpret_cast<uint32_t*>(blk + 4)[lane] =
-        (uint32_t)(q0 & 0xff) | ((uint32_t)(q1 & 0xff) << 8) | ((uint32_t)(q2 & 0xff) << 16) |
-        ((uint32_t)(q3 & 0xff) << 24);
-    int s = q0 + q1 + q2 + q3;
-    s += __shfl_xor(s, 1, kWave);
-    s += __shfl_xor(s, 2, kWave);
-    if ((lane & 3) == 0) reinterpret_cast<int16_t*>(blk + 260)[lane >> 2] = (int16_t)s;
-    if (lane == 0) *reinterpret_cast<float*>(blk) = delta;
-}
-
-// Stages `nwords` dwords of token t's Q8_K row into LDS.
-__device__ __forceinline__ void stage_q8(uint32_t* __restrict__ q8s, const unsigned char* __restrict__ q8,
-                                         int t, int nb, int tid) {
-    const uint32_t* src = reinterpret_cast<const uint32_t*>(q8 + (size_t)t * nb * Q8K_BYTES);
-    for (int i = tid; i < nb * Q8K_WORDS; i += LQ_THREADS) q8s[i] = src[i];
+    if (b < nb) {
+        uint32_t* blk = q8 + ((size_t)t * nb + b) * Q8K_WORDS;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) blk[1 + 4 * li + i] = pk[i];
+        reinterpret_cast<int16_t*>(blk + 65)[li] = (int16_t)bsum;
+        if (li == 0) blk[0] = __builtin_bit_cast(uint32_t, delta);
+    }
 }
 
 // VecDotQ4K.HorizontalSum (VecDotQ4K.cs:145-151).
@@ -146,58 +153,6 @@ __device__ __forceinline__ void q4k_block_lanes(const uint32_t* __restrict__ wb,
     }
 }
 
-__global__ __launch_bounds__(LQ_THREADS) void q4k_linear(const unsigned char* __restrict__ w,
-                                                         const unsigned char* __restrict__ q8,
-                                                         float* __restrict__ y, int n_in, int n_out,
-                                                         int tokens, int rows_per_wg) {
-#pragma clang fp contract(off)
-    const int nb = n_in / QK;
-    const int row0 = blockIdx.x * rows_per_wg;
-    const int nrows = min(rows_per_wg, n_out - row0);
-    const int nblk = nrows * nb;
-    const int tid = threadIdx.x;
-
-    __shared__ uint4 wsh[LQ_THREADS * (Q4K_BYTES / 16)];   // 36 KiB
-    __shared__ uint32_t q8s[LQ_MAX_NB * Q8K_WORDS];        // 18.3 KiB
-    __shared__ int lanes[LQ_THREADS][13];
-
-    const uint4* src = reinterpret_cast<const uint4*>(w + (size_t)row0 * nb * Q4K_BYTES);
-    for (int i = tid; i < nblk * (Q4K_BYTES / 16); i += LQ_THREADS) wsh[i] = src[i];
-
-    for (int t = 0; t < tokens; ++t) {
-        stage_q8(q8s, q8, t, nb, tid);
-        __syncthreads();
-        if (tid < nblk) {
-            int sumi[8], prod[4];
-            q4k_block_lanes(reinterpret_cast<const uint32_t*>(wsh + tid * (Q4K_BYTES / 16)),
-                            q8s + (tid % nb) * Q8K_WORDS, sumi, prod);
-#pragma unroll
-            for (int k = 0; k < 8; ++k) lanes[tid][k] = sumi[k];
-#pragma unroll
-            for (int k = 0; k < 4; ++k) lanes[tid][8 + k] = prod[k];
-        }
-        __syncthreads();
-        if (tid < nrows) {
-            float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-            float accm[4] = {0.f, 0.f, 0.f, 0.f};
-            for (int b = 0; b < nb; ++b) {
-                const int blk = tid * nb + b;
-                const uint32_t hdr = reinterpret_cast<const uint32_t*>(wsh + blk * (Q4K_BYTES / 16))[0];
-                const float yd = __builtin_bit_cast(float, q8s[b * Q8K_WORDS]);
-                const float d = yd * half_bits_to_float(hdr & 0xffff);
-                const float dmin = -yd * half_bits_to_float(hdr >> 16);
-#pragma unroll
-                for (int k = 0; k < 4; ++k) accm[k] = accm[k] + dmin * (float)lanes[blk][8 + k];
-#pragma unroll
-                for (int k = 0; k < 8; ++k) acc[k] = fmaf((float)lanes[blk][k], d, acc[k]);
-            }
-            const float m = (accm[0] + accm[2]) + (accm[1] + accm[3]);
-            y[(size_t)t * n_out + row0 + tid] = hsum8(acc) + m;
-        }
-        __syncthreads();
-    }
-}
-
 // ---------------------------------------------------------------- Q6_K
 
 // Dword of LDS at an arbitrary even byte offset.
@@ -248,64 +203,135 @@ __device__ __forceinline__ void q6k_block_lanes(const uint32_t* __restrict__ bas
     }
 }
 
-__global__ __launch_bounds__(LQ_THREADS) void q6k_linear(const unsigned char* __restrict__ w,
-                                                         const unsigned char* __restrict__ q8,
-                                                         float* __restrict__ y, int n_in, int n_out,
-                                                         int tokens, int rows_per_wg) {
+// LDS bytes of one workgroup: staged weights (16-byte chunks, one of slack at
+// each end), the token's Q8_K row, the integer lanes and the fp32 partials.
+__host__ __device__ constexpr int lq_wchunks(int rows, int nb, int bytes) {
+    return (rows * nb * bytes + 31) / 16 + 1;
+}
+
+template <int QT>
+__global__ __launch_bounds__(LQ_THREADS) void linear_q(const unsigned char* __restrict__ w,
+                                                       const uint32_t* __restrict__ q8,
+                                                       float* __restrict__ y, int n_in, int n_out,
+                                                       int tokens, int rows_per_wg) {
 #pragma clang fp contract(off)
-    const int nb = n_in / QK;
+    constexpr int BB = QT == 4 ? Q4K_BYTES : Q6K_BYTES;
+    constexpr int NL = QT == 4 ? 12 : 8;          // integer lanes per block
+    extern __shared__ uint4 smem[];
+    const int nb = n_in / QK, lane = threadIdx.x;
     const int row0 = blockIdx.x * rows_per_wg;
     const int nrows = min(rows_per_wg, n_out - row0);
     const int nblk = nrows * nb;
-    const int tid = threadIdx.x;
+    uint4* wsh = smem;
+    uint32_t* q8s = reinterpret_cast<uint32_t*>(smem + lq_wchunks(rows_per_wg, nb, BB));
+    int* lanes = reinterpret_cast<int*>(q8s + nb * Q8K_WORDS);
+    float* accs = reinterpret_cast<float*>(lanes + LQ_THREADS * LANES_LD);
 
-    // The workgroup's blocks start at an even byte; they are staged from the
-    // 16-byte boundary below, with one 16-byte chunk of slack at each end.
-    __shared__ uint4 wsh[(LQ_THREADS * Q6K_BYTES) / 16 + 2];  // 52.5 KiB
-    __shared__ uint32_t q8s[LQ_MAX_NB * Q8K_WORDS];
-    __shared__ int lanes[LQ_THREADS][9];
-
-    const size_t total = (size_t)n_out * nb * Q6K_BYTES;
-    const size_t start = (size_t)row0 * nb * Q6K_BYTES;
-    const size_t end = start + (size_t)nblk * Q6K_BYTES;
+    // The workgroup's rows are contiguous bytes starting at an even offset;
+    // they are staged from the 16-byte boundary below.  Only the weight
+    // buffer's last chunk can be partial: it is read with 2-byte loads.
+    const size_t total = (size_t)n_out * nb * BB;
+    const size_t start = (size_t)row0 * nb * BB;
     const size_t s16 = start & ~(size_t)15;
     const int shift = (int)(start - s16);
-    const int nchunks = (int)((end - s16 + 15) >> 4);
-    for (int i = tid; i < nchunks; i += LQ_THREADS) {
+    const int nchunks = (int)((start + (size_t)nblk * BB - s16 + 15) >> 4);
+    // All of a lane's weight loads are issued before the first LDS store.
+    constexpr int MAXC = (LQ_THREADS * BB + 31 + LQ_THREADS * 16 - 1) / (LQ_THREADS * 16) + 1;
+    uint4 wv[MAXC];
+#pragma unroll
+    for (int c = 0; c < MAXC; ++c) {
+        const int i = lane + LQ_THREADS * c;
         const size_t off = s16 + 16 * (size_t)i;
-        if (off + 16 <= total) {
-            wsh[i] = *reinterpret_cast<const uint4*>(w + off);
-        } else {
-            // The weight buffer's last chunk: 2-byte loads up to its end.
-            uint32_t wd[4] = {0u, 0u, 0u, 0u};
-            for (int hb = 0; hb < 8 && off + 2 * hb < total; ++hb)
-                wd[hb >> 1] |= (uint32_t)(*reinterpret_cast<const uint16_t*>(w + off + 2 * hb)) << (16 * (hb & 1));
-            wsh[i] = make_uint4(wd[0], wd[1], wd[2], wd[3]);
+        wv[c] = make_uint4(0u, 0u, 0u, 0u);
+        if (i < nchunks && off + 16 <= total) wv[c] = *reinterpret_cast<const uint4*>(w + off);
+    }
+#pragma unroll
+    for (int c = 0; c < MAXC; ++c) {
+        const int i = lane + LQ_THREADS * c;
+        const size_t off = s16 + 16 * (size_t)i;
+        if (i < nchunks) {
+            if (off + 16 <= total) {
+                wsh[i] = wv[c];
+            } else {
+                uint32_t wd[4] = {0u, 0u, 0u, 0u};
+                for (int hb = 0; hb < 8 && off + 2 * hb < total; ++hb)
+                    wd[hb >> 1] |= (uint32_t)(*reinterpret_cast<const uint16_t*>(w + off + 2 * hb)) << (16 * (hb & 1));
+                wsh[i] = make_uint4(wd[0], wd[1], wd[2], wd[3]);
+            }
         }
     }
     const uint32_t* wbase = reinterpret_cast<const uint32_t*>(wsh);
 
     for (int t = 0; t < tokens; ++t) {
-        stage_q8(q8s, q8, t, nb, tid);
-        __syncthreads();
-        if (tid < nblk) {
-            int sumi[8];
-            q6k_block_lanes(wbase, shift + tid * Q6K_BYTES, q8s + (tid % nb) * Q8K_WORDS, sumi);
+        {
+            // The token's Q8_K row, nb x 19 16-byte chunks, 8 loads a lane in flight.
+            const uint4* src = reinterpret_cast<const uint4*>(q8 + (size_t)t * nb * Q8K_WORDS);
+            uint4* dst = reinterpret_cast<uint4*>(q8s);
+            const int n4 = nb * (Q8K_WORDS / 4);
+            for (int i0 = 0; i0 < n4; i0 += 8 * LQ_THREADS) {
+                uint4 qv[8];
 #pragma unroll
-            for (int k = 0; k < 8; ++k) lanes[tid][k] = sumi[k];
+                for (int c = 0; c < 8; ++c) {
+                    qv[c] = make_uint4(0u, 0u, 0u, 0u);
+                    if (i0 + lane + LQ_THREADS * c < n4) qv[c] = src[i0 + lane + LQ_THREADS * c];
+                }
+#pragma unroll
+                for (int c = 0; c < 8; ++c)
+                    if (i0 + lane + LQ_THREADS * c < n4) dst[i0 + lane + LQ_THREADS * c] = qv[c];
+            }
         }
         __syncthreads();
-        if (tid < nrows) {
-            float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-            for (int b = 0; b < nb; ++b) {
-                const int blk = tid * nb + b;
-                const int o = shift + blk * Q6K_BYTES + 208;
-                const uint32_t dh = lds_word(wbase, o) & 0xffff;
-                const float d = __builtin_bit_cast(float, q8s[b * Q8K_WORDS]) * half_bits_to_float(dh);
+        if (lane < nblk) {
+            const uint32_t* q8b = q8s + (lane % nb) * Q8K_WORDS;
+            int* out = lanes + lane * LANES_LD;
+            if constexpr (QT == 4) {
+                // Q4_K blocks are 16-byte multiples, so shift is 0 and the
+                // block's dwords are aligned.
+                int sumi[8], prod[4];
+                q4k_block_lanes(wbase + (shift + lane * BB) / 4, q8b, sumi, prod);
 #pragma unroll
-                for (int k = 0; k < 8; ++k) acc[k] = fmaf(d, (float)lanes[blk][k], acc[k]);
+                for (int k = 0; k < 8; ++k) out[k] = sumi[k];
+#pragma unroll
+                for (int k = 0; k < 4; ++k) out[8 + k] = prod[k];
+            } else {
+                int sumi[8];
+                q6k_block_lanes(wbase, shift + lane * BB, q8b, sumi);
+#pragma unroll
+                for (int k = 0; k < 8; ++k) out[k] = sumi[k];
             }
-            y[(size_t)t * n_out + row0 + tid] = hsum8(acc);
+        }
+        __syncthreads();
+        // Row r's lane k: one FMA per block in block order (and, for Q4_K,
+        // lanes 0..3 also run the min term's multiply-add).
+        const int r = lane >> 3, k = lane & 7;
+        if (r < nrows) {
+            float acc = 0.0f, accm = 0.0f;
+            for (int b = 0; b < nb; ++b) {
+                const int blk = r * nb + b;
+                const float yd = __builtin_bit_cast(float, q8s[b * Q8K_WORDS]);
+                const int* L = lanes + blk * LANES_LD;
+                if constexpr (QT == 4) {
+                    const uint32_t hdr = wbase[(shift + blk * BB) / 4];
+                    const float d = yd * half_bits_to_float(hdr & 0xffff);
+                    const float dmin = -yd * half_bits_to_float(hdr >> 16);
+                    if (k < 4) accm = accm + dmin * (float)L[8 + k];
+                    acc = fmaf((float)L[k], d, acc);
+                } else {
+                    const uint32_t dh = lds_word(wbase, shift + blk * BB + 208) & 0xffff;
+                    const float d = yd * half_bits_to_float(dh);
+                    acc = fmaf(d, (float)L[k], acc);
+                }
+            }
+            accs[r * NL + k] = acc;
+            if (QT == 4 && k < 4) accs[r * NL + 8 + k] = accm;
+        }
+        __syncthreads();
+        if (lane < nrows) {
+            const float* a = accs + lane * NL;
+            const float h[8] = {a[0], a[1], a[2], a[3], a[4], a[5], a[6], a[7]};
+            float o = hsum8(h);
+            if constexpr (QT == 4) o = o + ((a[8] + a[10]) + (a[9] + a[11]));
+            y[(size_t)t * n_out + row0 + lane] = o;
         }
         __syncthreads();
     }
@@ -313,34 +339,37 @@ __global__ __launch_bounds__(LQ_THREADS) void q6k_linear(const unsigned char* __
 
 }  // namespace
 
-size_t linear_q_work_bytes(int n_in, int tokens) {
-    return (size_t)tokens * (n_in / QK) * Q8K_BYTES;
-}
-
 hipError_t launch_linear_q(q35m_ctx* c, int qtype, const void* w, const float* x, float* y,
                            int n_in, int n_out, int tokens) {
     const int nb = n_in / QK;
-    unsigned char* q8 = reinterpret_cast<unsigned char*>(c->work);
+    const int rows_per_wg = min(LQ_THREADS / nb, LQ_MAX_ROWS);
+    const int grid = (n_out + rows_per_wg - 1) / rows_per_wg;
+    const int bb = qtype == 4 ? Q4K_BYTES : Q6K_BYTES;
+    const size_t lds = 16 * (size_t)lq_wchunks(rows_per_wg, nb, bb) + (size_t)nb * Q8K_WORDS * 4 +
+                       (size_t)LQ_THREADS * LANES_LD * 4 + (size_t)LQ_MAX_ROWS * 12 * 4;
+    uint32_t* q8 = reinterpret_cast<uint32_t*>(c->work);
     {
         ProfScope ps_(c, K_Q8K_QUANTIZE);
-        hipExtLaunchKernelGGL(q8k_quantize, dim3(nb, tokens), dim3(kWave), 0, c->stream, ps_.a, ps_.b, 0, x,
-                              q8, n_in);
+        hipExtLaunchKernelGGL(q8k_quantize, dim3((nb + 3) / 4, tokens), dim3(kWave), 0, c->stream, ps_.a,
+                              ps_.b, 0, x, q8, nb);
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    const int rows_per_wg = LQ_THREADS / nb;
-    const int grid = (n_out + rows_per_wg - 1) / rows_per_wg;
     const unsigned char* wb = reinterpret_cast<const unsigned char*>(w);
     if (qtype == 4) {
         ProfScope ps_(c, K_Q4K_LINEAR);
-        hipExtLaunchKernelGGL(q4k_linear, dim3(grid), dim3(LQ_THREADS), 0, c->stream, ps_.a, ps_.b, 0, wb, q8,
-                              y, n_in, n_out, tokens, rows_per_wg);
+        hipExtLaunchKernelGGL(linear_q<4>, dim3(grid), dim3(LQ_THREADS), lds, c->stream, ps_.a, ps_.b, 0, wb,
+                              q8, y, n_in, n_out, tokens, rows_per_wg);
     } else {
         ProfScope ps_(c, K_Q6K_LINEAR);
-        hipExtLaunchKernelGGL(q6k_linear, dim3(grid), dim3(LQ_THREADS), 0, c->stream, ps_.a, ps_.b, 0, wb, q8,
-                              y, n_in, n_out, tokens, rows_per_wg);
+        hipExtLaunchKernelGGL(linear_q<6>, dim3(grid), dim3(LQ_THREADS), lds, c->stream, ps_.a, ps_.b, 0, wb,
+                              q8, y, n_in, n_out, tokens, rows_per_wg);
     }
     return hipGetLastError();
+}
+
+size_t linear_q_work_bytes(int n_in, int tokens) {
+    return (size_t)tokens * (n_in / QK) * Q8K_WORDS * 4;
 }
 
 }  // namespace q35

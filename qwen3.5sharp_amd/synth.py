@@ -127,3 +127,24 @@ def kv_prefill(n_pos: int, kv_dim: int, salt: int = 0) -> tuple:
     k = normal(ID_CACHE_K + s, n_pos * kv_dim).reshape(n_pos, kv_dim)
     v = normal(ID_CACHE_V + s, n_pos * kv_dim).reshape(n_pos, kv_dim)
     return k, v
+
+
+QBLOCK_BYTES = {4: 144, 6: 210}
+
+
+def quant_weights(qtype: int, n_out: int, n_in: int, salt: int = 0) -> np.ndarray:
+    """GGUF Q4_K (qtype 4) or Q6_K (qtype 6) rows [n_out][n_in/256 blocks] as
+    bytes: every quant byte uniform, the fp16 block scales in [0.004, 0.02]
+    (finite, the size trained weights have)."""
+    nblk = n_out * (n_in // 256)
+    nb = QBLOCK_BYTES[qtype]
+    raw = splitmix64(SEED_BASE + 300 + 10 * qtype + salt, (nblk * nb + 7) // 8)
+    b = raw.view(np.uint8)[:nblk * nb].reshape(nblk, nb).copy()
+    d = uniform(301 + 10 * qtype + salt, nblk, 0.004, 0.02).astype(np.float16)
+    if qtype == 4:
+        b[:, 0:2] = d.view(np.uint8).reshape(-1, 2)
+        b[:, 2:4] = uniform(302 + 10 * qtype + salt, nblk, 0.004, 0.02).astype(np.float16) \
+            .view(np.uint8).reshape(-1, 2)
+    else:
+        b[:, 208:210] = d.view(np.uint8).reshape(-1, 2)
+    return b.ravel()
