@@ -182,6 +182,21 @@ int q35m_linear_q4k(q35m_ctx* ctx, const void* w, const float* x, float* y, int 
 int q35m_linear_q6k(q35m_ctx* ctx, const void* w, const float* x, float* y, int n_in, int n_out,
                     int tokens);
 
+/* The same in two steps, for several projections of one activation:
+ * q35m_quantize_q8k writes the Q8_K blocks of x [tokens][n_in] into a device
+ * buffer of q35m_q8k_bytes(n_in, tokens) bytes (each 292-byte BlockQ8K
+ * padded to 304 bytes), and the _prequant entry points read them.  Replaces
+ * Q8K.QuantizeRow (src/Qwen35Sharp.Kernels/Q8K.cs:12-78) followed by
+ * Qwen35Model.GemvPrequant (src/Qwen35Sharp.Model/Qwen35Model.Decode.cs:
+ * 89-112), as the reference's attention decode uses them
+ * (Qwen35Model.Decode.cs:286-292).  x, q8 and w must be 16-byte aligned. */
+size_t q35m_q8k_bytes(int n_in, int tokens);
+int q35m_quantize_q8k(q35m_ctx* ctx, const float* x, void* q8, int n_in, int tokens);
+int q35m_linear_q4k_prequant(q35m_ctx* ctx, const void* w, const void* q8, float* y, int n_in,
+                             int n_out, int tokens);
+int q35m_linear_q6k_prequant(q35m_ctx* ctx, const void* w, const void* q8, float* y, int n_in,
+                             int n_out, int tokens);
+
 /* Per-kernel HIP event timers, the device-side counterpart of the
  * reference's Qwen35Model.ProfileEnabled / Ticks* counters
  * (Qwen35Model.cs:42-72).  q35m_profile(ctx, 1) zeroes the totals and times

@@ -486,6 +486,15 @@ int q35m_attn_prefill(q35m_ctx* ctx, int layer, int seq, int T, const float* q_g
     return Q35M_OK;
 }
 
+static int check_linear_dims(int n_in, int n_out, int tokens) {
+    if (n_in < 256 || n_in > 16384 || n_in % 256)
+        return fail(Q35M_ERR_UNSUPPORTED, "n_in must be a multiple of 256 in [256, 16384] (got %d)", n_in);
+    if (n_out < 1) return fail(Q35M_ERR_INVALID, "n_out must be >= 1 (got %d)", n_out);
+    if (tokens < 1 || tokens > 65535)
+        return fail(Q35M_ERR_INVALID, "tokens must be in [1, 65535] (got %d)", tokens);
+    return Q35M_OK;
+}
+
 static int linear_q(q35m_ctx* ctx, int qtype, const void* w, const float* x, float* y, int n_in,
                     int n_out, int tokens) {
     int r = check_ctx(ctx);
@@ -493,14 +502,47 @@ static int linear_q(q35m_ctx* ctx, int qtype, const void* w, const float* x, flo
     if (!w || !x || !y) return fail(Q35M_ERR_INVALID, "null pointer");
     if (((uintptr_t)w & 15) || ((uintptr_t)x & 15))
         return fail(Q35M_ERR_INVALID, "weights and input must be 16-byte aligned");
-    if (n_in < 256 || n_in > 16384 || n_in % 256)
-        return fail(Q35M_ERR_UNSUPPORTED, "n_in must be a multiple of 256 in [256, 16384] (got %d)", n_in);
-    if (n_out < 1) return fail(Q35M_ERR_INVALID, "n_out must be >= 1 (got %d)", n_out);
-    if (tokens < 1 || tokens > 65535)
-        return fail(Q35M_ERR_INVALID, "tokens must be in [1, 65535] (got %d)", tokens);
+    if ((r = check_linear_dims(n_in, n_out, tokens))) return r;
     HIP_TRY(q35::ensure_work(ctx, q35::linear_q_work_bytes(n_in, tokens)), "workspace");
     HIP_TRY(q35::launch_linear_q(ctx, qtype, w, x, y, n_in, n_out, tokens), "linear_q");
     return Q35M_OK;
+}
+
+size_t q35m_q8k_bytes(int n_in, int tokens) {
+    return (n_in > 0 && tokens > 0) ? q35::linear_q_work_bytes(n_in, tokens) : 0;
+}
+
+int q35m_quantize_q8k(q35m_ctx* ctx, const float* x, void* q8, int n_in, int tokens) {
+    int r = check_ctx(ctx);
+    if (r) return r;
+    if (!x || !q8) return fail(Q35M_ERR_INVALID, "null pointer");
+    if (((uintptr_t)x & 15) || ((uintptr_t)q8 & 15))
+        return fail(Q35M_ERR_INVALID, "input and Q8_K buffer must be 16-byte aligned");
+    if ((r = check_linear_dims(n_in, 1, tokens))) return r;
+    HIP_TRY(q35::launch_q8k_quantize(ctx, x, q8, n_in, tokens), "quantize_q8k");
+    return Q35M_OK;
+}
+
+static int linear_q_prequant(q35m_ctx* ctx, int qtype, const void* w, const void* q8, float* y,
+                             int n_in, int n_out, int tokens) {
+    int r = check_ctx(ctx);
+    if (r) return r;
+    if (!w || !q8 || !y) return fail(Q35M_ERR_INVALID, "null pointer");
+    if (((uintptr_t)w & 15) || ((uintptr_t)q8 & 15))
+        return fail(Q35M_ERR_INVALID, "weights and Q8_K buffer must be 16-byte aligned");
+    if ((r = check_linear_dims(n_in, n_out, tokens))) return r;
+    HIP_TRY(q35::launch_linear_q_prequant(ctx, qtype, w, q8, y, n_in, n_out, tokens), "linear_q");
+    return Q35M_OK;
+}
+
+int q35m_linear_q4k_prequant(q35m_ctx* ctx, const void* w, const void* q8, float* y, int n_in,
+                             int n_out, int tokens) {
+    return linear_q_prequant(ctx, 4, w, q8, y, n_in, n_out, tokens);
+}
+
+int q35m_linear_q6k_prequant(q35m_ctx* ctx, const void* w, const void* q8, float* y, int n_in,
+                             int n_out, int tokens) {
+    return linear_q_prequant(ctx, 6, w, q8, y, n_in, n_out, tokens);
 }
 
 int q35m_linear_q4k(q35m_ctx* ctx, const void* w, const float* x, float* y, int n_in, int n_out,

@@ -204,12 +204,15 @@ __device__ __forceinline__ void q6k_block_lanes(const uint32_t* __restrict__ bas
 }
 
 // LDS bytes of one workgroup: staged weights (16-byte chunks, one of slack at
-// each end), the token's Q8_K row, the integer lanes and the fp32 partials.
-__host__ __device__ constexpr int lq_wchunks(int rows, int nb, int bytes) {
-    return (rows * nb * bytes + 31) / 16 + 1;
+// each end; Q6_K only), the token's Q8_K row, the integer lanes and the fp32
+// partials.
+__host__ __device__ constexpr int lq_wchunks(int qtype, int rows, int nb, int bytes) {
+    return qtype == 4 ? 0 : (rows * nb * bytes + 31) / 16 + 1;
 }
 
-template <int QT>
+// NB > 0 fixes the blocks per row at compile time (n_in = 256 NB), so the
+// fp32 pass unrolls and issues its LDS reads together; NB = 0 is generic.
+template <int QT, int NB>
 __global__ __launch_bounds__(LQ_THREADS) void linear_q(const unsigned char* __restrict__ w,
                                                        const uint32_t* __restrict__ q8,
                                                        float* __restrict__ y, int n_in, int n_out,
@@ -218,49 +221,59 @@ __global__ __launch_bounds__(LQ_THREADS) void linear_q(const unsigned char* __re
     constexpr int BB = QT == 4 ? Q4K_BYTES : Q6K_BYTES;
     constexpr int NL = QT == 4 ? 12 : 8;          // integer lanes per block
     extern __shared__ uint4 smem[];
-    const int nb = n_in / QK, lane = threadIdx.x;
+    const int nb = NB > 0 ? NB : n_in / QK, lane = threadIdx.x;
     const int row0 = blockIdx.x * rows_per_wg;
     const int nrows = min(rows_per_wg, n_out - row0);
     const int nblk = nrows * nb;
     uint4* wsh = smem;
-    uint32_t* q8s = reinterpret_cast<uint32_t*>(smem + lq_wchunks(rows_per_wg, nb, BB));
+    uint32_t* q8s = reinterpret_cast<uint32_t*>(smem + lq_wchunks(QT, rows_per_wg, nb, BB));
     int* lanes = reinterpret_cast<int*>(q8s + nb * Q8K_WORDS);
     float* accs = reinterpret_cast<float*>(lanes + LQ_THREADS * LANES_LD);
 
-    // The workgroup's rows are contiguous bytes starting at an even offset;
-    // they are staged from the 16-byte boundary below.  Only the weight
-    // buffer's last chunk can be partial: it is read with 2-byte loads.
-    const size_t total = (size_t)n_out * nb * BB;
-    const size_t start = (size_t)row0 * nb * BB;
-    const size_t s16 = start & ~(size_t)15;
-    const int shift = (int)(start - s16);
-    const int nchunks = (int)((start + (size_t)nblk * BB - s16 + 15) >> 4);
-    // All of a lane's weight loads are issued before the first LDS store.
-    constexpr int MAXC = (LQ_THREADS * BB + 31 + LQ_THREADS * 16 - 1) / (LQ_THREADS * 16) + 1;
-    uint4 wv[MAXC];
+    // Q4_K: each thread loads its block (16-byte aligned, 144 B) straight
+    // into registers.  Q6_K blocks are 2-byte aligned: the workgroup's rows,
+    // contiguous bytes from an even offset, are staged in LDS from the
+    // 16-byte boundary below; only the weight buffer's last chunk can be
+    // partial, and it is read with 2-byte loads.
+    uint4 wreg[QT == 4 ? Q4K_BYTES / 16 : 1];
+    const uint32_t* wbase = reinterpret_cast<const uint32_t*>(wsh);
+    int shift = 0;
+    if constexpr (QT == 4) {
+        const uint4* src = reinterpret_cast<const uint4*>(w + ((size_t)row0 * nb + min(lane, nblk - 1)) * BB);
 #pragma unroll
-    for (int c = 0; c < MAXC; ++c) {
-        const int i = lane + LQ_THREADS * c;
-        const size_t off = s16 + 16 * (size_t)i;
-        wv[c] = make_uint4(0u, 0u, 0u, 0u);
-        if (i < nchunks && off + 16 <= total) wv[c] = *reinterpret_cast<const uint4*>(w + off);
-    }
+        for (int c = 0; c < Q4K_BYTES / 16; ++c) wreg[c] = src[c];
+    } else {
+        const size_t total = (size_t)n_out * nb * BB;
+        const size_t start = (size_t)row0 * nb * BB;
+        const size_t s16 = start & ~(size_t)15;
+        shift = (int)(start - s16);
+        const int nchunks = (int)((start + (size_t)nblk * BB - s16 + 15) >> 4);
+        // All of a lane's weight loads are issued before the first LDS store.
+        constexpr int MAXC = (LQ_THREADS * BB + 31 + LQ_THREADS * 16 - 1) / (LQ_THREADS * 16) + 1;
+        uint4 wv[MAXC];
 #pragma unroll
-    for (int c = 0; c < MAXC; ++c) {
-        const int i = lane + LQ_THREADS * c;
-        const size_t off = s16 + 16 * (size_t)i;
-        if (i < nchunks) {
-            if (off + 16 <= total) {
-                wsh[i] = wv[c];
-            } else {
-                uint32_t wd[4] = {0u, 0u, 0u, 0u};
-                for (int hb = 0; hb < 8 && off + 2 * hb < total; ++hb)
-                    wd[hb >> 1] |= (uint32_t)(*reinterpret_cast<const uint16_t*>(w + off + 2 * hb)) << (16 * (hb & 1));
-                wsh[i] = make_uint4(wd[0], wd[1], wd[2], wd[3]);
+        for (int c = 0; c < MAXC; ++c) {
+            const int i = lane + LQ_THREADS * c;
+            const size_t off = s16 + 16 * (size_t)i;
+            wv[c] = make_uint4(0u, 0u, 0u, 0u);
+            if (i < nchunks && off + 16 <= total) wv[c] = *reinterpret_cast<const uint4*>(w + off);
+        }
+#pragma unroll
+        for (int c = 0; c < MAXC; ++c) {
+            const int i = lane + LQ_THREADS * c;
+            const size_t off = s16 + 16 * (size_t)i;
+            if (i < nchunks) {
+                if (off + 16 <= total) {
+                    wsh[i] = wv[c];
+                } else {
+                    uint32_t wd[4] = {0u, 0u, 0u, 0u};
+                    for (int hb = 0; hb < 8 && off + 2 * hb < total; ++hb)
+                        wd[hb >> 1] |= (uint32_t)(*reinterpret_cast<const uint16_t*>(w + off + 2 * hb)) << (16 * (hb & 1));
+                    wsh[i] = make_uint4(wd[0], wd[1], wd[2], wd[3]);
+                }
             }
         }
     }
-    const uint32_t* wbase = reinterpret_cast<const uint32_t*>(wsh);
 
     for (int t = 0; t < tokens; ++t) {
         {
@@ -285,19 +298,20 @@ __global__ __launch_bounds__(LQ_THREADS) void linear_q(const unsigned char* __re
             const uint32_t* q8b = q8s + (lane % nb) * Q8K_WORDS;
             int* out = lanes + lane * LANES_LD;
             if constexpr (QT == 4) {
-                // Q4_K blocks are 16-byte multiples, so shift is 0 and the
-                // block's dwords are aligned.
                 int sumi[8], prod[4];
-                q4k_block_lanes(wbase + (shift + lane * BB) / 4, q8b, sumi, prod);
+                const uint32_t* wb = reinterpret_cast<const uint32_t*>(wreg);
+                q4k_block_lanes(wb, q8b, sumi, prod);
 #pragma unroll
                 for (int k = 0; k < 8; ++k) out[k] = sumi[k];
 #pragma unroll
                 for (int k = 0; k < 4; ++k) out[8 + k] = prod[k];
+                out[12] = (int)wb[0];             // d, dmin of the block
             } else {
                 int sumi[8];
                 q6k_block_lanes(wbase, shift + lane * BB, q8b, sumi);
 #pragma unroll
                 for (int k = 0; k < 8; ++k) out[k] = sumi[k];
+                out[8] = (int)(lds_word(wbase, shift + lane * BB + 208) & 0xffff);   // d of the block
             }
         }
         __syncthreads();
@@ -306,19 +320,19 @@ __global__ __launch_bounds__(LQ_THREADS) void linear_q(const unsigned char* __re
         const int r = lane >> 3, k = lane & 7;
         if (r < nrows) {
             float acc = 0.0f, accm = 0.0f;
-            for (int b = 0; b < nb; ++b) {
+#pragma unroll
+            for (int b = 0; b < (NB > 0 ? NB : nb); ++b) {
                 const int blk = r * nb + b;
                 const float yd = __builtin_bit_cast(float, q8s[b * Q8K_WORDS]);
                 const int* L = lanes + blk * LANES_LD;
                 if constexpr (QT == 4) {
-                    const uint32_t hdr = wbase[(shift + blk * BB) / 4];
+                    const uint32_t hdr = (uint32_t)L[12];
                     const float d = yd * half_bits_to_float(hdr & 0xffff);
                     const float dmin = -yd * half_bits_to_float(hdr >> 16);
                     if (k < 4) accm = accm + dmin * (float)L[8 + k];
                     acc = fmaf((float)L[k], d, acc);
                 } else {
-                    const uint32_t dh = lds_word(wbase, shift + blk * BB + 208) & 0xffff;
-                    const float d = yd * half_bits_to_float(dh);
+                    const float d = yd * half_bits_to_float((uint32_t)L[8]);
                     acc = fmaf(d, (float)L[k], acc);
                 }
             }
@@ -339,33 +353,41 @@ __global__ __launch_bounds__(LQ_THREADS) void linear_q(const unsigned char* __re
 
 }  // namespace
 
-hipError_t launch_linear_q(q35m_ctx* c, int qtype, const void* w, const float* x, float* y,
-                           int n_in, int n_out, int tokens) {
+hipError_t launch_q8k_quantize(q35m_ctx* c, const float* x, void* q8, int n_in, int tokens) {
+    const int nb = n_in / QK;
+    ProfScope ps_(c, K_Q8K_QUANTIZE);
+    hipExtLaunchKernelGGL(q8k_quantize, dim3((nb + 3) / 4, tokens), dim3(kWave), 0, c->stream, ps_.a, ps_.b, 0,
+                          x, reinterpret_cast<uint32_t*>(q8), nb);
+    return hipGetLastError();
+}
+
+hipError_t launch_linear_q_prequant(q35m_ctx* c, int qtype, const void* w, const void* q8, float* y,
+                                    int n_in, int n_out, int tokens) {
     const int nb = n_in / QK;
     const int rows_per_wg = min(LQ_THREADS / nb, LQ_MAX_ROWS);
     const int grid = (n_out + rows_per_wg - 1) / rows_per_wg;
     const int bb = qtype == 4 ? Q4K_BYTES : Q6K_BYTES;
-    const size_t lds = 16 * (size_t)lq_wchunks(rows_per_wg, nb, bb) + (size_t)nb * Q8K_WORDS * 4 +
+    const size_t lds = 16 * (size_t)lq_wchunks(qtype, rows_per_wg, nb, bb) + (size_t)nb * Q8K_WORDS * 4 +
                        (size_t)LQ_THREADS * LANES_LD * 4 + (size_t)LQ_MAX_ROWS * 12 * 4;
-    uint32_t* q8 = reinterpret_cast<uint32_t*>(c->work);
-    {
-        ProfScope ps_(c, K_Q8K_QUANTIZE);
-        hipExtLaunchKernelGGL(q8k_quantize, dim3((nb + 3) / 4, tokens), dim3(kWave), 0, c->stream, ps_.a,
-                              ps_.b, 0, x, q8, nb);
-    }
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
     const unsigned char* wb = reinterpret_cast<const unsigned char*>(w);
-    if (qtype == 4) {
-        ProfScope ps_(c, K_Q4K_LINEAR);
-        hipExtLaunchKernelGGL(linear_q<4>, dim3(grid), dim3(LQ_THREADS), lds, c->stream, ps_.a, ps_.b, 0, wb,
-                              q8, y, n_in, n_out, tokens, rows_per_wg);
-    } else {
-        ProfScope ps_(c, K_Q6K_LINEAR);
-        hipExtLaunchKernelGGL(linear_q<6>, dim3(grid), dim3(LQ_THREADS), lds, c->stream, ps_.a, ps_.b, 0, wb,
-                              q8, y, n_in, n_out, tokens, rows_per_wg);
-    }
+    const uint32_t* qb = reinterpret_cast<const uint32_t*>(q8);
+    auto launch = [&](auto kern, int kid) {
+        ProfScope ps_(c, kid);
+        hipExtLaunchKernelGGL(kern, dim3(grid), dim3(LQ_THREADS), lds, c->stream, ps_.a, ps_.b, 0, wb, qb, y,
+                              n_in, n_out, tokens, rows_per_wg);
+    };
+    if (qtype == 4)
+        launch(nb == 10 ? linear_q<4, 10> : nb == 16 ? linear_q<4, 16> : linear_q<4, 0>, K_Q4K_LINEAR);
+    else
+        launch(nb == 10 ? linear_q<6, 10> : nb == 16 ? linear_q<6, 16> : linear_q<6, 0>, K_Q6K_LINEAR);
     return hipGetLastError();
+}
+
+hipError_t launch_linear_q(q35m_ctx* c, int qtype, const void* w, const float* x, float* y,
+                           int n_in, int n_out, int tokens) {
+    hipError_t e = launch_q8k_quantize(c, x, c->work, n_in, tokens);
+    if (e != hipSuccess) return e;
+    return launch_linear_q_prequant(c, qtype, w, c->work, y, n_in, n_out, tokens);
 }
 
 size_t linear_q_work_bytes(int n_in, int tokens) {

@@ -127,6 +127,9 @@ size_t attn_prefill_work_bytes(const Dims& d, int T);
 hipError_t launch_linear_q(q35m_ctx* c, int qtype, const void* w, const float* x, float* y,
                            int n_in, int n_out, int tokens);
 size_t linear_q_work_bytes(int n_in, int tokens);
+hipError_t launch_q8k_quantize(q35m_ctx* c, const float* x, void* q8, int n_in, int tokens);
+hipError_t launch_linear_q_prequant(q35m_ctx* c, int qtype, const void* w, const void* q8, float* y,
+                                    int n_in, int n_out, int tokens);
 
 // Ensures ctx->work holds at least `bytes` (synchronises before regrowing).
 hipError_t ensure_work(q35m_ctx* c, size_t bytes);

@@ -62,10 +62,15 @@ def lib() -> ctypes.CDLL:
         _lib.q35m_state_device_ptr.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
                                                ctypes.c_int, ctypes.POINTER(ctypes.c_void_p),
                                                ctypes.POINTER(ctypes.c_size_t)]
-        for name in ("q35m_linear_q4k", "q35m_linear_q6k"):
+        for name in ("q35m_linear_q4k", "q35m_linear_q6k", "q35m_linear_q4k_prequant",
+                     "q35m_linear_q6k_prequant"):
             getattr(_lib, name).argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                                             ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
                                             ctypes.c_int]
+        _lib.q35m_quantize_q8k.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                                           ctypes.c_int, ctypes.c_int]
+        _lib.q35m_q8k_bytes.restype = ctypes.c_size_t
+        _lib.q35m_q8k_bytes.argtypes = [ctypes.c_int, ctypes.c_int]
     return _lib
 
 
@@ -244,6 +249,18 @@ class Context:
 
     def bytes_array(self, data) -> DeviceBytes:
         return DeviceBytes(self, data)
+
+    def quantize_q8k(self, x, n_in, tokens) -> "DeviceBytes":
+        """Q8_K blocks of x [tokens][n_in] in a new device buffer."""
+        q8 = DeviceBytes(self, np.zeros(lib().q35m_q8k_bytes(n_in, tokens), np.uint8))
+        check(lib().q35m_quantize_q8k(ctypes.c_void_p(self.handle), ctypes.c_void_p(x.ptr),
+                                      ctypes.c_void_p(q8.ptr), n_in, tokens))
+        return q8
+
+    def linear_q_prequant(self, qtype: int, w, q8, y, n_in, n_out, tokens) -> None:
+        fn = lib().q35m_linear_q4k_prequant if qtype == 4 else lib().q35m_linear_q6k_prequant
+        check(fn(ctypes.c_void_p(self.handle), ctypes.c_void_p(w.ptr), ctypes.c_void_p(q8.ptr),
+                 ctypes.c_void_p(y.ptr), n_in, n_out, tokens))
 
     def linear_q(self, qtype: int, w, x, y, n_in, n_out, tokens) -> None:
         """y[tokens][n_out] = W x for GGUF Q4_K (qtype 4) or Q6_K (qtype 6) weight rows."""

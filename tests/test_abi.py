@@ -16,7 +16,7 @@ def declared_symbols():
     for fn in os.listdir(os.path.join(ROOT, "include")):
         if fn.endswith(".h"):
             text = open(os.path.join(ROOT, "include", fn)).read()
-            names |= set(re.findall(r"^\s*(?:int|void\*|const char\*|void)\s+(q35m_\w+)\s*\(",
+            names |= set(re.findall(r"^\s*(?:int|void\*|const char\*|void|size_t)\s+(q35m_\w+)\s*\(",
                                     text, re.M))
     return sorted(names)
 
@@ -72,6 +72,9 @@ def test_null_context_is_rejected():
     assert L.q35m_kv_len(None, 0, ctypes.byref(n)) == q35mix.ERR_INVALID
     assert L.q35m_linear_q4k(None, None, None, None, 256, 1, 1) == q35mix.ERR_INVALID
     assert L.q35m_linear_q6k(None, None, None, None, 256, 1, 1) == q35mix.ERR_INVALID
+    assert L.q35m_quantize_q8k(None, None, None, 256, 1) == q35mix.ERR_INVALID
+    assert L.q35m_linear_q4k_prequant(None, None, None, None, 256, 1, 1) == q35mix.ERR_INVALID
+    assert L.q35m_q8k_bytes(2560, 3) == 3 * 10 * 304
 
 
 def test_no_device_here_is_an_error_not_a_fallback():

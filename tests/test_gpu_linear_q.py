@@ -98,3 +98,27 @@ def test_linear_q_rejects_bad_arguments(ctx):
     assert L.q35m_linear_q6k(h, None, dx.ptr, dy.ptr, 512, 2, 1) == q35mix.ERR_INVALID
     for a in (dw, dx, dy):
         a.free()
+
+
+def test_prequant_matches_one_shot(ctx):
+    """Quantize once, three projections (the reference's attention decode:
+    Qwen35Model.Decode.cs:286-292), each bit-identical to the one-shot call
+    and to the oracle."""
+    n_in = 2560
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((2, n_in)).astype(np.float32)
+    dx = ctx.array((2, n_in), x)
+    q8 = ctx.quantize_q8k(dx, n_in, 2)
+    for qtype, n_out in ((4, 8192), (4, 1024), (6, 1024)):
+        w = qb.random_blocks(rng, qtype, n_out * n_in // 256)
+        dw = ctx.bytes_array(w)
+        dy = ctx.array((2, n_out))
+        ctx.linear_q_prequant(qtype, dw, q8, dy, n_in, n_out, 2)
+        got = dy.download()
+        want = oracle.linear_q(qtype, w, x, n_in, n_out)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), (qtype, n_out)
+        assert np.array_equal(got.view(np.uint32), run(ctx, qtype, w, x, n_in, n_out).view(np.uint32))
+        dw.free()
+        dy.free()
+    q8.free()
+    dx.free()
