@@ -184,8 +184,9 @@ int q35m_linear_q6k(q35m_ctx* ctx, const void* w, const float* x, float* y, int 
 
 /* The same in two steps, for several projections of one activation:
  * q35m_quantize_q8k writes the Q8_K blocks of x [tokens][n_in] into a device
- * buffer of q35m_q8k_bytes(n_in, tokens) bytes (each 292-byte BlockQ8K
- * padded to 304 bytes), and the _prequant entry points read them.  Replaces
+ * buffer of q35m_q8k_bytes(n_in, tokens) bytes (a BlockQ8K's fields in
+ * 304 bytes: f32 d, 12 unused bytes, i8 qs[256], i16 bsums[16]), and the
+ * _prequant entry points read them.  Replaces
  * Q8K.QuantizeRow (src/Qwen35Sharp.Kernels/Q8K.cs:12-78) followed by
  * Qwen35Model.GemvPrequant (src/Qwen35Sharp.Model/Qwen35Model.Decode.cs:
  * 89-112), as the reference's attention decode uses them

@@ -36,7 +36,10 @@ namespace {
 
 constexpr int QK = 256;
 constexpr int Q4K_BYTES = 144, Q6K_BYTES = 210;
-constexpr int Q8K_WORDS = 76;      // workspace stride of a Q8_K block: 292 B padded to 19 x 16 B
+// Workspace form of a Q8_K block, 304 bytes (19 x 16): dword 0 d, dwords 4..67
+// qs (16-byte aligned), dwords 68..75 bsums; dwords 1..3 unused.
+constexpr int Q8K_WORDS = 76;
+constexpr int Q8K_QS = 4, Q8K_BS = 68;
 constexpr int LQ_THREADS = 64;
 constexpr int LQ_MAX_ROWS = 8;     // rows per workgroup (8 threads a row in the fp32 pass)
 constexpr int LANES_LD = 13;       // padded stride of the per-block integer lanes in LDS
@@ -50,8 +53,7 @@ __device__ __forceinline__ float half_bits_to_float(uint32_t h) {
 // a lane's values are exactly one bsums group).  amax = max |x|; the scale's
 // sign is that of the first element of magnitude amax; iscale = -127 / max
 // (IEEE division), delta = 1 / iscale; q = clamp(round-half-even(x * iscale),
-// -127, 127).  Output: Q8_K blocks [tokens][nb] in the workspace, each
-// padded to 304 bytes so that rows stage with 16-byte loads.
+// -127, 127).  Output: Q8_K blocks [tokens][nb] in the workspace form above.
 __global__ __launch_bounds__(kWave) void q8k_quantize(const float* __restrict__ x,
                                                       uint32_t* __restrict__ q8, int nb) {
     const int lane = threadIdx.x, grp = lane >> 4, li = lane & 15;
@@ -93,9 +95,8 @@ __global__ __launch_bounds__(kWave) void q8k_quantize(const float* __restrict__ 
     }
     if (b < nb) {
         uint32_t* blk = q8 + ((size_t)t * nb + b) * Q8K_WORDS;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) blk[1 + 4 * li + i] = pk[i];
-        reinterpret_cast<int16_t*>(blk + 65)[li] = (int16_t)bsum;
+        *reinterpret_cast<uint4*>(blk + Q8K_QS + 4 * li) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
+        reinterpret_cast<int16_t*>(blk + Q8K_BS)[li] = (int16_t)bsum;
         if (li == 0) blk[0] = __builtin_bit_cast(uint32_t, delta);
     }
 }
@@ -110,6 +111,10 @@ __device__ __forceinline__ float hsum8(const float (&a)[8]) {
 
 // ---------------------------------------------------------------- Q4_K
 
+// Every product below has operands well inside 24 bits (6- or 8-bit scales
+// times sums of at most 4 x 63 x 127), so it uses the full-rate 24-bit
+// multiply.
+//
 // The integer lanes of one Q4_K x Q8_K block (VecDotQ4K.cs:74-117): sumi[k]
 // (scaled q4.q8 over bytes 4k..4k+3 of each 32-byte group) and prod[k]
 // (mins . pairwise bsums, _mm_madd_epi16 order).
@@ -124,8 +129,14 @@ __device__ __forceinline__ void q4k_block_lanes(const uint32_t* __restrict__ wb,
     const uint32_t u1 = (s2 & kmask2) | (((s0 >> 6) & kmask3) << 4);
     const uint32_t u0 = s0 & kmask1;
     const uint32_t su[2] = {u0, u1}, mu[2] = {u2, u3};
-    // bsums as 8 dwords of two int16 each (Q8_K byte 260 = dword 65)
-    const uint32_t* bs = q8b + 65;
+    // The block's qs (16 x 16 B) and bsums (8 dwords of two int16), all
+    // loads issued before the first product.
+    uint4 qv[16], bv[2];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) qv[i] = reinterpret_cast<const uint4*>(q8b + Q8K_QS)[i];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) bv[i] = reinterpret_cast<const uint4*>(q8b + Q8K_BS)[i];
+    const uint32_t* bs = reinterpret_cast<const uint32_t*>(bv);
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
         const uint32_t p0 = bs[2 * k], p1 = bs[2 * k + 1];
@@ -133,12 +144,12 @@ __device__ __forceinline__ void q4k_block_lanes(const uint32_t* __restrict__ wb,
         const int a1 = (int16_t)(p1 & 0xffff) + (int16_t)(p1 >> 16);
         const int m0 = (mu[k >> 1] >> (16 * (k & 1))) & 0xff;
         const int m1 = (mu[k >> 1] >> (16 * (k & 1) + 8)) & 0xff;
-        prod[k] = m0 * (int16_t)a0 + m1 * (int16_t)a1;
+        prod[k] = __mul24(m0, (int16_t)a0) + __mul24(m1, (int16_t)a1);
     }
 #pragma unroll
     for (int k = 0; k < 8; ++k) sumi[k] = 0;
-    const uint32_t* qs = wb + 4;         // 32 dwords
-    const uint32_t* q8 = q8b + 1;        // 64 dwords
+    const uint32_t* qs = wb + 4;                                  // 32 dwords
+    const uint32_t* q8 = reinterpret_cast<const uint32_t*>(qv);   // 64 dwords
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int sl = (su[j >> 1] >> (16 * (j & 1))) & 0xff;
@@ -148,7 +159,7 @@ __device__ __forceinline__ void q4k_block_lanes(const uint32_t* __restrict__ wb,
             const uint32_t w = qs[8 * j + k];
             const int pl = __builtin_amdgcn_sdot4((int)(w & 0x0f0f0f0fu), (int)q8[16 * j + k], 0, false);
             const int ph = __builtin_amdgcn_sdot4((int)((w >> 4) & 0x0f0f0f0fu), (int)q8[16 * j + 8 + k], 0, false);
-            sumi[k] += pl * sl + ph * sh;
+            sumi[k] += __mul24(pl, sl) + __mul24(ph, sh);
         }
     }
 }
@@ -176,7 +187,12 @@ __device__ __forceinline__ void q6k_block_lanes(const uint32_t* __restrict__ bas
     }
 #pragma unroll
     for (int k = 0; k < 8; ++k) sumi[k] = 0;
-    const uint32_t* q8 = q8b + 1;
+    uint4 qv[16], bv[2];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) qv[i] = reinterpret_cast<const uint4*>(q8b + Q8K_QS)[i];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) bv[i] = reinterpret_cast<const uint4*>(q8b + Q8K_BS)[i];
+    const uint32_t* q8 = reinterpret_cast<const uint32_t*>(qv);
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
 #pragma unroll
@@ -189,17 +205,17 @@ __device__ __forceinline__ void q6k_block_lanes(const uint32_t* __restrict__ bas
             const uint32_t v2 = ((a >> 4) & 0x0f0f0f0fu) | (h & 0x30303030u);
             const uint32_t v3 = ((c >> 4) & 0x0f0f0f0fu) | ((h & 0xc0c0c0c0u) >> 2);
             const int hf = k >> 2;
-            sumi[k] += sc[8 * j + hf] * __builtin_amdgcn_sdot4((int)v0, (int)q8[32 * j + k], 0, false);
-            sumi[k] += sc[8 * j + 2 + hf] * __builtin_amdgcn_sdot4((int)v1, (int)q8[32 * j + 8 + k], 0, false);
-            sumi[k] += sc[8 * j + 4 + hf] * __builtin_amdgcn_sdot4((int)v2, (int)q8[32 * j + 16 + k], 0, false);
-            sumi[k] += sc[8 * j + 6 + hf] * __builtin_amdgcn_sdot4((int)v3, (int)q8[32 * j + 24 + k], 0, false);
+            sumi[k] += __mul24(sc[8 * j + hf], __builtin_amdgcn_sdot4((int)v0, (int)q8[32 * j + k], 0, false));
+            sumi[k] += __mul24(sc[8 * j + 2 + hf], __builtin_amdgcn_sdot4((int)v1, (int)q8[32 * j + 8 + k], 0, false));
+            sumi[k] += __mul24(sc[8 * j + 4 + hf], __builtin_amdgcn_sdot4((int)v2, (int)q8[32 * j + 16 + k], 0, false));
+            sumi[k] += __mul24(sc[8 * j + 6 + hf], __builtin_amdgcn_sdot4((int)v3, (int)q8[32 * j + 24 + k], 0, false));
         }
     }
-    const uint32_t* bs = q8b + 65;
+    const uint32_t* bs = reinterpret_cast<const uint32_t*>(bv);
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
         const uint32_t p = bs[k];
-        sumi[k] -= ((int16_t)(p & 0xffff) * sc[2 * k] + (int16_t)(p >> 16) * sc[2 * k + 1]) * 32;
+        sumi[k] -= (__mul24((int16_t)(p & 0xffff), sc[2 * k]) + __mul24((int16_t)(p >> 16), sc[2 * k + 1])) * 32;
     }
 }
 
