@@ -272,22 +272,67 @@ void q35o_q6k_dequantize_row(const void* wx, float* y, int k) {
     }
 }
 
-/* MulMatQ4K.Gemv (src/Qwen35Sharp.Kernels/MulMatQ4K.cs:12-43) and
- * Q6K.Gemv/Gemm (src/Qwen35Sharp.Kernels/Q6K.cs:301-413): each token row is
- * quantized to Q8_K, then every output is one dot product.  (Q6K.Gemm's
+/* GemmQ4K.GemmAvx2Tile (src/Qwen35Sharp.Kernels/GemmQ4K.Avx2.cs:39-207), the
+ * reference's Q4_K path for more than one token (MulMatQ4K.Gemm,
+ * MulMatQ4K.cs:45-127, over the x8 panels and the BlockQ4Kx8Meta sidecar of
+ * RepackQ4K.BuildMeta, RepackQ4K.cs:90-129), for one (token, output) pair:
+ * per block b and 32-value sub-block s in order, acc = fma((float)(sc * dot),
+ * dw * dx, acc) with dot the exact integer q4 . q8 of the sub-block (its
+ * int16 partials never overflow: at most 8 * 15 * 127 each); per block,
+ * mn = fma((float)(sum_j min_j * (bsums[2j] + bsums[2j+1])), dminw * dx, mn);
+ * the result is acc - mn.  Quantize4x8 gives the same int8 values and scales
+ * as Q8K.QuantizeRow (same ScaleBlock and rounding), so q8 is the row's Q8_K
+ * blocks. */
+static float q4k_panel_dot(const blk_q4k* x, const blk_q8k* y, int n) {
+    const int nb = n / QK;
+    float acc = 0.0f, mn = 0.0f;
+    for (int i = 0; i < nb; i++) {
+        const float cs = q35o_half_to_float(x[i].d) * y[i].d;
+        const float cm = q35o_half_to_float(x[i].dmin) * y[i].d;
+        uint8_t sm[16];
+        q4k_unpack_scales(x[i].scales, sm);
+        for (int s = 0; s < 8; s++) {
+            const int g = s / 2, hi = s % 2;
+            int dot = 0;
+            for (int l = 0; l < 32; l++) {
+                const int q = hi ? (x[i].qs[32 * g + l] >> 4) : (x[i].qs[32 * g + l] & 0xf);
+                dot += q * y[i].qs[64 * g + 32 * hi + l];
+            }
+            acc = fmaf((float)(sm[s] * dot), cs, acc);
+        }
+        int m = 0;
+        for (int j = 0; j < 8; j++) m += sm[8 + j] * (y[i].bsums[2 * j] + y[i].bsums[2 * j + 1]);
+        mn = fmaf((float)m, cm, mn);
+    }
+    return acc - mn;
+}
+
+/* Qwen35Model.Linear for Q4_K / Q6_K weights: MulMatQ4K.Gemv / Gemm
+ * (src/Qwen35Sharp.Kernels/MulMatQ4K.cs:12-127) and Q6K.Gemv / Gemm
+ * (src/Qwen35Sharp.Kernels/Q6K.cs:301-413): each token row is quantized to
+ * Q8_K, then every output is one dot product (the panel order above for Q4_K
+ * with several tokens).  (Q6K.Gemm's
  * four-token DotAvx2x4 gives the same value per token as DotAvx2: the same
  * integer lanes and the same fma per block.)  type 4 = Q4_K, 6 = Q6_K. */
 void q35o_linear_q(int type, const void* w, const float* x, float* y, int n_in, int n_out,
                    int tokens) {
     const int nb = n_in / QK;
     const size_t wrow = (size_t)nb * (type == 4 ? sizeof(blk_q4k) : sizeof(blk_q6k));
+    /* Q4_K with more than one token: the panel GEMM for the first n_out & ~7
+     * outputs (MulMatQ4K.cs:104-123 sends the rest through VecDotQ4K.Dot). */
+    const int panel_rows = (type == 4 && tokens > 1) ? (n_out & ~7) : 0;
     blk_q8k q8[64];
     if (nb > 64) return;
     for (int t = 0; t < tokens; t++) {
         q35o_q8k_quantize_row(x + (size_t)t * n_in, q8, n_in);
         for (int r = 0; r < n_out; r++) {
             const void* wr = (const uint8_t*)w + (size_t)r * wrow;
-            y[(size_t)t * n_out + r] = type == 4 ? q35o_q4k_dot(wr, q8, n_in) : q35o_q6k_dot(wr, q8, n_in);
+            float v;
+            if (r < panel_rows)
+                v = q4k_panel_dot((const blk_q4k*)wr, q8, n_in);
+            else
+                v = type == 4 ? q35o_q4k_dot(wr, q8, n_in) : q35o_q6k_dot(wr, q8, n_in);
+            y[(size_t)t * n_out + r] = v;
         }
     }
 }

@@ -232,13 +232,13 @@ template <int QT, int NB>
 __global__ __launch_bounds__(LQ_THREADS) void linear_q(const unsigned char* __restrict__ w,
                                                        const uint32_t* __restrict__ q8,
                                                        float* __restrict__ y, int n_in, int n_out,
-                                                       int tokens, int rows_per_wg) {
+                                                       int tokens, int rows_per_wg, int row_base) {
 #pragma clang fp contract(off)
     constexpr int BB = QT == 4 ? Q4K_BYTES : Q6K_BYTES;
     constexpr int NL = QT == 4 ? 12 : 8;          // integer lanes per block
     extern __shared__ uint4 smem[];
     const int nb = NB > 0 ? NB : n_in / QK, lane = threadIdx.x;
-    const int row0 = blockIdx.x * rows_per_wg;
+    const int row0 = row_base + blockIdx.x * rows_per_wg;
     const int nrows = min(rows_per_wg, n_out - row0);
     const int nblk = nrows * nb;
     uint4* wsh = smem;
@@ -367,6 +367,147 @@ __global__ __launch_bounds__(LQ_THREADS) void linear_q(const unsigned char* __re
     }
 }
 
+// ---------------------------------------------------------------- Q4_K, several tokens
+
+// The reference's Q4_K path for several tokens (MulMatQ4K.Gemm,
+// MulMatQ4K.cs:45-127 -> GemmQ4K.GemmAvx2Tile, GemmQ4K.Avx2.cs:39-207) for
+// the first n_out & ~7 outputs: per (token, output row), over blocks b and
+// 32-value sub-blocks s in order, acc = fma((float)(sc_s * dot_s), dw * dx,
+// acc), with dot_s the exact integer q4 . q8 of the sub-block; per block, mn =
+// fma((float)(sum_j min_j (bsums[2j] + bsums[2j+1])), dminw * dx, mn); out =
+// acc - mn.  A workgroup takes 64 tokens x 64 rows (wave = 16 tokens x 4
+// tiles of 16 rows).  dot_s of a 16 x 16 tile is one v_mfma_i32_16x16x32_i8;
+// the min term's integer (at most 8 x 63 x 4064, exact in fp32) is two
+// v_mfma_f32_16x16x4f32 on small integers.  Blocks are double-buffered in LDS:
+// the next block's loads are in flight while the current one computes.
+constexpr int GT = 64, GR = 64;
+constexpr int GW_CHUNKS = GR * Q4K_BYTES / 16;          // 576
+constexpr int GX_CHUNKS = GT * Q8K_WORDS / 4;           // 1216
+
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+__global__ __launch_bounds__(256) void q4k_gemm(const unsigned char* __restrict__ w,
+                                                const uint32_t* __restrict__ q8,
+                                                float* __restrict__ y, int n_in, int n_rows,
+                                                int n_out, int tokens) {
+#pragma clang fp contract(off)
+    const int nb = n_in / QK;
+    const int row0 = blockIdx.x * GR, tok0 = blockIdx.y * GT;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int l16 = lane & 15, lg = lane >> 4;
+
+    __shared__ uint4 wsh[2][GW_CHUNKS];
+    __shared__ uint4 xsh[2][GX_CHUNKS];
+
+    constexpr int NW = (GW_CHUNKS + 255) / 256, NX = (GX_CHUNKS + 255) / 256;
+    uint4 pw[NW], px[NX];
+    auto issue = [&](int b) {
+#pragma unroll
+        for (int c = 0; c < NW; ++c) {
+            const int i = tid + 256 * c;
+            pw[c] = make_uint4(0u, 0u, 0u, 0u);
+            if (i < GW_CHUNKS) {
+                const int r = i / 9, k = i % 9;
+                pw[c] = reinterpret_cast<const uint4*>(
+                    w + ((size_t)min(row0 + r, n_rows - 1) * nb + b) * Q4K_BYTES)[k];
+            }
+        }
+#pragma unroll
+        for (int c = 0; c < NX; ++c) {
+            const int i = tid + 256 * c;
+            px[c] = make_uint4(0u, 0u, 0u, 0u);
+            if (i < GX_CHUNKS) {
+                const int t = i / 19, k = i % 19;
+                px[c] = reinterpret_cast<const uint4*>(
+                    q8 + ((size_t)min(tok0 + t, tokens - 1) * nb + b) * Q8K_WORDS)[k];
+            }
+        }
+    };
+    auto commit = [&](int buf) {
+#pragma unroll
+        for (int c = 0; c < NW; ++c)
+            if (tid + 256 * c < GW_CHUNKS) wsh[buf][tid + 256 * c] = pw[c];
+#pragma unroll
+        for (int c = 0; c < NX; ++c)
+            if (tid + 256 * c < GX_CHUNKS) xsh[buf][tid + 256 * c] = px[c];
+    };
+
+    float acc[4][4], mn[4][4];
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[rt][r] = mn[rt][r] = 0.0f;
+
+    issue(0);
+    commit(0);
+    __syncthreads();
+    for (int b = 0; b < nb; ++b) {
+        const int buf = b & 1;
+        if (b + 1 < nb) issue(b + 1);
+        const uint32_t* W = reinterpret_cast<const uint32_t*>(wsh[buf]);
+        const uint32_t* X = reinterpret_cast<const uint32_t*>(xsh[buf]);
+        // This lane's A rows: token 16 wave + l16; its D rows: tokens 16 wave + 4 lg + r.
+        const uint32_t* xa = X + (16 * wave + l16) * Q8K_WORDS;
+        float dx[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) dx[r] = __builtin_bit_cast(float, X[(16 * wave + 4 * lg + r) * Q8K_WORDS]);
+        // Pair sums of bsums for the min term's A operand: j = lg and lg + 4.
+        float pa[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const uint32_t p = xa[Q8K_BS + lg + 4 * h];
+            pa[h] = (float)((int)(int16_t)(p & 0xffff) + (int)(int16_t)(p >> 16));
+        }
+#pragma unroll
+        for (int rt = 0; rt < 4; ++rt) {
+            const uint32_t* wb = W + (16 * rt + l16) * (Q4K_BYTES / 4);
+            const uint32_t hdr = wb[0], S0 = wb[1], S1 = wb[2], S2 = wb[3];
+            const float dw = half_bits_to_float(hdr & 0xffff), dmw = half_bits_to_float(hdr >> 16);
+            float cs[4], cm[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                cs[r] = dw * dx[r];
+                cm[r] = dmw * dx[r];
+            }
+#pragma unroll
+            for (int sb = 0; sb < 8; ++sb) {
+                const int g = sb >> 1, hi = sb & 1;
+                const int sc = sb < 4 ? (int)((S0 >> (8 * sb)) & 63)
+                                      : (int)(((S2 >> (8 * (sb - 4))) & 15) | (((S0 >> (8 * (sb - 4) + 6)) & 3) << 4));
+                const uint32_t a0 = xa[Q8K_QS + 16 * g + 8 * hi + 2 * lg], a1 = xa[Q8K_QS + 16 * g + 8 * hi + 2 * lg + 1];
+                const uint32_t w0 = wb[4 + 8 * g + 2 * lg], w1 = wb[4 + 8 * g + 2 * lg + 1];
+                const uint32_t b0 = hi ? (w0 >> 4) & 0x0f0f0f0fu : w0 & 0x0f0f0f0fu;
+                const uint32_t b1 = hi ? (w1 >> 4) & 0x0f0f0f0fu : w1 & 0x0f0f0f0fu;
+                const long av = (long)(((unsigned long)a1 << 32) | a0);
+                const long bv = (long)(((unsigned long)b1 << 32) | b0);
+                const i32x4 dot = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, bv, i32x4{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) acc[rt][r] = fmaf((float)__mul24(sc, dot[r]), cs[r], acc[rt][r]);
+            }
+            // mins of j = lg and lg + 4 for this lane's row
+            const float m0 = (float)((S1 >> (8 * lg)) & 63);
+            const float m1 = (float)(((S2 >> (8 * lg + 4)) & 15) | (((S1 >> (8 * lg + 6)) & 3) << 4));
+            f32x4 md = __builtin_amdgcn_mfma_f32_16x16x4f32(pa[0], m0, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+            md = __builtin_amdgcn_mfma_f32_16x16x4f32(pa[1], m1, md, 0, 0, 0);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) mn[rt][r] = fmaf(md[r], cm[r], mn[rt][r]);
+        }
+        if (b + 1 < nb) commit(buf ^ 1);
+        __syncthreads();
+    }
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt) {
+        const int row = row0 + 16 * rt + l16;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int t = tok0 + 16 * wave + 4 * lg + r;
+            if (row < n_rows && t < tokens) y[(size_t)t * n_out + row] = acc[rt][r] - mn[rt][r];
+        }
+    }
+}
+
 }  // namespace
 
 hipError_t launch_q8k_quantize(q35m_ctx* c, const float* x, void* q8, int n_in, int tokens) {
@@ -380,17 +521,27 @@ hipError_t launch_q8k_quantize(q35m_ctx* c, const float* x, void* q8, int n_in, 
 hipError_t launch_linear_q_prequant(q35m_ctx* c, int qtype, const void* w, const void* q8, float* y,
                                     int n_in, int n_out, int tokens) {
     const int nb = n_in / QK;
+    const unsigned char* wb = reinterpret_cast<const unsigned char*>(w);
+    const uint32_t* qb = reinterpret_cast<const uint32_t*>(q8);
+    // Q4_K with several tokens: the panel order for the first n_out & ~7 rows
+    // (the reference's MulMatQ4K.Gemm), the GEMV for the rest.
+    const int row_base = (qtype == 4 && tokens > 1) ? (n_out & ~7) : 0;
+    if (row_base > 0) {
+        ProfScope ps_(c, K_Q4K_GEMM);
+        hipExtLaunchKernelGGL(q4k_gemm, dim3((row_base + GR - 1) / GR, (tokens + GT - 1) / GT), dim3(256), 0,
+                              c->stream, ps_.a, ps_.b, 0, wb, qb, y, n_in, row_base, n_out, tokens);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess || row_base == n_out) return e;
+    }
     const int rows_per_wg = min(LQ_THREADS / nb, LQ_MAX_ROWS);
-    const int grid = (n_out + rows_per_wg - 1) / rows_per_wg;
+    const int grid = (n_out - row_base + rows_per_wg - 1) / rows_per_wg;
     const int bb = qtype == 4 ? Q4K_BYTES : Q6K_BYTES;
     const size_t lds = 16 * (size_t)lq_wchunks(qtype, rows_per_wg, nb, bb) + (size_t)nb * Q8K_WORDS * 4 +
                        (size_t)LQ_THREADS * LANES_LD * 4 + (size_t)LQ_MAX_ROWS * 12 * 4;
-    const unsigned char* wb = reinterpret_cast<const unsigned char*>(w);
-    const uint32_t* qb = reinterpret_cast<const uint32_t*>(q8);
     auto launch = [&](auto kern, int kid) {
         ProfScope ps_(c, kid);
         hipExtLaunchKernelGGL(kern, dim3(grid), dim3(LQ_THREADS), lds, c->stream, ps_.a, ps_.b, 0, wb, qb, y,
-                              n_in, n_out, tokens, rows_per_wg);
+                              n_in, n_out, tokens, rows_per_wg, row_base);
     };
     if (qtype == 4)
         launch(nb == 10 ? linear_q<4, 10> : nb == 16 ? linear_q<4, 16> : linear_q<4, 0>, K_Q4K_LINEAR);

@@ -1,6 +1,8 @@
 """Quantized projections (q35m_linear_q4k / q35m_linear_q6k) through the C ABI
 against the oracle: bit-exact (the kernels keep the reference's integer lanes
-and fp32 accumulation order), at the projection shapes of the 4B mixers
+and fp32 accumulation order: the AVX2 GEMV for one token and for Q6_K, the
+panel GEMM for Q4_K with several tokens plus the GEMV for its last
+n_out % 8 outputs), at the projection shapes of the 4B mixers
 (hidden 2560: qkv 8192, gate 4096, beta/alpha 32, ssm_out and attn_output
 4096 -> 2560, attn k/v 1024), ragged small shapes, several tokens, zero and
 extreme activation blocks, and weight buffers whose size is not a multiple of
@@ -43,7 +45,8 @@ def run(ctx, qtype, w, x, n_in, n_out):
 
 
 SHAPES = [(2560, 8192, 1), (2560, 4096, 1), (2560, 32, 1), (4096, 2560, 1), (2560, 1024, 1),
-          (256, 7, 1), (512, 33, 5), (2560, 1024, 3), (16384, 19, 2)]
+          (256, 7, 1), (512, 33, 5), (2560, 1024, 3), (16384, 19, 2), (2560, 520, 70),
+          (4096, 136, 130)]
 
 
 @pytest.mark.parametrize("qtype", [4, 6])

@@ -147,3 +147,30 @@ def test_linear_q_against_fp64(qtype):
         exact = wd @ xd
         scale = np.abs(wd) @ np.abs(xd)
         assert np.all(np.abs(y[t] - exact) <= 2e-6 * scale)
+
+
+def test_q4k_several_tokens_panel_rows_and_gemv_tail():
+    """Several tokens: the first n_out & ~7 outputs follow the panel GEMM order,
+    the rest the GEMV; one token is the GEMV throughout.  All within fp32
+    rounding of the exact value, and the two orders really differ."""
+    rng = np.random.default_rng(91)
+    n_in, n_out = 1024, 13
+    w = qb.random_blocks(rng, 4, n_out * n_in // 256)
+    x = rng.standard_normal((3, n_in)).astype(np.float32)
+    y = oracle.linear_q(4, w, x, n_in, n_out)
+    wd = qb.dequant_f64(4, w).reshape(n_out, n_in)
+    rows = w.reshape(n_out, -1)
+    differ = 0
+    for t in range(3):
+        q8 = oracle.q8k_quantize(x[t])
+        gemv = np.array([oracle.q4k_dot(rows[r], q8, n_in) for r in range(n_out)], np.float32)
+        assert np.array_equal(y[t, 8:].view(np.uint32), gemv[8:].view(np.uint32))
+        differ += int(np.sum(y[t, :8].view(np.uint32) != gemv[:8].view(np.uint32)))
+        d, q, _ = qb.parse_q8k(q8)
+        xd = (d[:, None].astype(np.float64) * q).ravel()
+        assert np.all(np.abs(y[t] - wd @ xd) <= 2e-6 * (np.abs(wd) @ np.abs(xd)))
+    assert differ > 0
+    y1 = oracle.linear_q(4, w, x[:1], n_in, n_out)
+    q8 = oracle.q8k_quantize(x[0])
+    gemv = np.array([oracle.q4k_dot(rows[r], q8, n_in) for r in range(n_out)], np.float32)
+    assert np.array_equal(y1[0].view(np.uint32), gemv.view(np.uint32))
