@@ -33,6 +33,7 @@ import synth  # noqa: E402
 
 HBM_PEAK = 8.0e12          # B/s, MI355X datasheet
 FP32_PEAK = 157.3e12       # FLOP/s, MI355X dense fp32 (matrix = vector)
+INT8_PEAK = 5.0e15         # OP/s, MI355X dense int8 matrix
 NK, NV, DK = 16, 32, 128
 NH, NKV, HD = 16, 4, 256
 CONV_DIM = 2 * NK * DK + NV * DK
@@ -192,17 +193,17 @@ def bench_attn_prefill(steps, warmup, T=2048):
     return ms, kt
 
 
-def bench_linear_q(qtype, n_in, n_out, steps, warmup, copies):
-    """One-token projection (the decode GEMV) rotating over `copies` weight
-    copies, more bytes than the 256 MB MALL."""
+def bench_linear_q(qtype, n_in, n_out, steps, warmup, copies, tokens=1):
+    """Projection of `tokens` rows (1: the decode GEMV) rotating over `copies`
+    weight copies, more bytes than the 256 MB MALL."""
     ctx = q35mix.Context(q35mix.qwen35_config(num_layers=1, is_recurrent=[1]), 1, 16)
     w = synth.quant_weights(qtype, n_out, n_in)
     ws = [ctx.bytes_array(w) for _ in range(copies)]
-    x = ctx.array((1, n_in), synth.normal(310, n_in))
-    y = ctx.array((1, n_out))
+    x = ctx.array((tokens, n_in), synth.normal(310, tokens * n_in))
+    y = ctx.array((tokens, n_out))
 
     def step(i):
-        ctx.linear_q(qtype, ws[i % copies], x, y, n_in, n_out, 1)
+        ctx.linear_q(qtype, ws[i % copies], x, y, n_in, n_out, tokens)
 
     ms = time_calls(ctx, step, steps, warmup)
     kt = kernel_times(ctx, step, steps)
@@ -448,6 +449,15 @@ def main():
             "kernels_ms": {k: v[0] for k, v in kt.items()}}
         log(f"[bench] GQA prefill: {workloads['attn_prefill_2048']}")
 
+    if want("linear_q"):
+        log("[bench] Q4_K projection 2560 -> 8192, 2048 tokens ...")
+        ms, kt, by = bench_linear_q(4, 2560, 8192, K, W, 1, tokens=2048)
+        macs = 2048 * 2560 * 8192
+        workloads["linear_q4k_2560x8192_t2048"] = {
+            "ms": ms, "tokens_per_s": 2048 / (ms / 1e3),
+            "int8_mfma_frac": 2 * macs / (ms / 1e3) / INT8_PEAK,
+            "kernels_ms": {k: v[0] for k, v in kt.items()}}
+        log(f"[bench] linear_q4k_2560x8192_t2048: {workloads['linear_q4k_2560x8192_t2048']}")
     for qtype, n_in, n_out, copies in ((4, 2560, 8192, 32), (6, 4096, 2560, 40)):
         if not want("linear_q"):
             break

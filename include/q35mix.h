@@ -172,11 +172,11 @@ int q35m_device_count(int* count);
  * (src/Qwen35Sharp.Model/Qwen35Model.Decode.cs:22-88) over MulMatQ4K.Gemv
  * (src/Qwen35Sharp.Kernels/MulMatQ4K.cs:12-43) and Q6K.Gemv / Q6K.Gemm
  * (src/Qwen35Sharp.Kernels/Q6K.cs:301-353): results are bit-identical to the
- * reference's AVX2 GEMV; for Q4_K with tokens > 1 the reference switches to
- * its packed panel GEMM (MulMatQ4K.Gemm, MulMatQ4K.cs:45-127), whose fp32
- * accumulation order differs, while this entry point keeps the GEMV order
- * per token.  w and x must be 16-byte aligned; n_in a multiple of 256 up to
- * 16384. */
+ * reference's AVX2 GEMV, and for Q4_K with tokens > 1 to its packed panel
+ * GEMM (MulMatQ4K.Gemm, MulMatQ4K.cs:45-127 -> GemmQ4K.GemmAvx2Tile,
+ * GemmQ4K.Avx2.cs:39-207) for the first n_out & ~7 outputs and the GEMV for
+ * the rest, as the reference splits them.  w and x must be 16-byte aligned;
+ * n_in a multiple of 256 up to 16384. */
 int q35m_linear_q4k(q35m_ctx* ctx, const void* w, const float* x, float* y, int n_in, int n_out,
                     int tokens);
 int q35m_linear_q6k(q35m_ctx* ctx, const void* w, const float* x, float* y, int n_in, int n_out,
