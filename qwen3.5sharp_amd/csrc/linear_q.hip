@@ -375,22 +375,31 @@ __global__ __launch_bounds__(LQ_THREADS) void linear_q(const unsigned char* __re
 // 32-value sub-blocks s in order, acc = fma((float)(sc_s * dot_s), dw * dx,
 // acc), with dot_s the exact integer q4 . q8 of the sub-block; per block, mn =
 // fma((float)(sum_j min_j (bsums[2j] + bsums[2j+1])), dminw * dx, mn); out =
-// acc - mn.  A workgroup takes 64 tokens x 64 rows (wave = 16 tokens x 4
-// tiles of 16 rows).  dot_s of a 16 x 16 tile is one v_mfma_i32_16x16x32_i8;
-// the min term's integer (at most 8 x 63 x 4064, exact in fp32) is two
-// v_mfma_f32_16x16x4f32 on small integers.  Blocks are double-buffered in LDS:
-// the next block's loads are in flight while the current one computes.
-constexpr int GT = 64, GR = 64;
-constexpr int GW_CHUNKS = GR * Q4K_BYTES / 16;          // 576
+// acc - mn.  A workgroup of 8 waves takes 64 tokens x 128 rows (wave = 64
+// tokens x 16 rows: 4 tiles of 16 x 16).  dot_s of a tile is one
+// v_mfma_i32_16x16x32_i8 whose accumulator starts at the bits of 1.5 * 2^23,
+// so the result read as fp32 is exactly 1.5 * 2^23 + dot_s (|dot_s| <= 60960
+// < 2^22) and (float)(sc * dot_s) = fma(that, sc, -1.5 * 2^23 * sc) exactly
+// (the exact value is an integer below 2^24): two VALU operations an output
+// per sub-block, the floor the reference's order sets.  The min term's
+// integer (at most 8 x 63 x 4064, exact in fp32) is two
+// v_mfma_f32_16x16x4f32 on small integers.  Blocks are double-buffered in
+// LDS; the next block's activations are loaded during sub-blocks 0-3 and its
+// weights during 4-7, so at most three 16-byte chunks a thread are staged.
+constexpr int GT = 64, GR = 128;
+constexpr int GW_CHUNKS = GR * Q4K_BYTES / 16;          // 1152
 constexpr int GX_CHUNKS = GT * Q8K_WORDS / 4;           // 1216
+constexpr int GTHREADS = 512, GRT = GR / 16 / (GTHREADS / 64);   // row tiles a wave: 1
+constexpr int GNW = (GW_CHUNKS + GTHREADS - 1) / GTHREADS, GNX = (GX_CHUNKS + GTHREADS - 1) / GTHREADS;
+constexpr int kMagic = 0x4B400000;                      // bits of 1.5 * 2^23
+constexpr float kMagicF = 12582912.0f;
 
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
-__global__ __launch_bounds__(256) void q4k_gemm(const unsigned char* __restrict__ w,
-                                                const uint32_t* __restrict__ q8,
-                                                float* __restrict__ y, int n_in, int n_rows,
-                                                int n_out, int tokens) {
+__global__ __launch_bounds__(GTHREADS) __attribute__((amdgpu_waves_per_eu(2)))
+void q4k_gemm(const unsigned char* __restrict__ w, const uint32_t* __restrict__ q8,
+              float* __restrict__ y, int n_in, int n_rows, int n_out, int tokens) {
 #pragma clang fp contract(off)
     const int nb = n_in / QK;
     const int row0 = blockIdx.x * GR, tok0 = blockIdx.y * GT;
@@ -401,22 +410,11 @@ __global__ __launch_bounds__(256) void q4k_gemm(const unsigned char* __restrict_
     __shared__ uint4 wsh[2][GW_CHUNKS];
     __shared__ uint4 xsh[2][GX_CHUNKS];
 
-    constexpr int NW = (GW_CHUNKS + 255) / 256, NX = (GX_CHUNKS + 255) / 256;
-    uint4 pw[NW], px[NX];
-    auto issue = [&](int b) {
+    uint4 px[GNX], pw[GNW];
+    auto issue_x = [&](int b) {
 #pragma unroll
-        for (int c = 0; c < NW; ++c) {
-            const int i = tid + 256 * c;
-            pw[c] = make_uint4(0u, 0u, 0u, 0u);
-            if (i < GW_CHUNKS) {
-                const int r = i / 9, k = i % 9;
-                pw[c] = reinterpret_cast<const uint4*>(
-                    w + ((size_t)min(row0 + r, n_rows - 1) * nb + b) * Q4K_BYTES)[k];
-            }
-        }
-#pragma unroll
-        for (int c = 0; c < NX; ++c) {
-            const int i = tid + 256 * c;
+        for (int c = 0; c < GNX; ++c) {
+            const int i = tid + GTHREADS * c;
             px[c] = make_uint4(0u, 0u, 0u, 0u);
             if (i < GX_CHUNKS) {
                 const int t = i / 19, k = i % 19;
@@ -425,87 +423,159 @@ __global__ __launch_bounds__(256) void q4k_gemm(const unsigned char* __restrict_
             }
         }
     };
-    auto commit = [&](int buf) {
+    auto issue_w = [&](int b) {
 #pragma unroll
-        for (int c = 0; c < NW; ++c)
-            if (tid + 256 * c < GW_CHUNKS) wsh[buf][tid + 256 * c] = pw[c];
+        for (int c = 0; c < GNW; ++c) {
+            const int i = tid + GTHREADS * c;
+            pw[c] = make_uint4(0u, 0u, 0u, 0u);
+            if (i < GW_CHUNKS) {
+                const int r = i / 9, k = i % 9;
+                pw[c] = reinterpret_cast<const uint4*>(
+                    w + ((size_t)min(row0 + r, n_rows - 1) * nb + b) * Q4K_BYTES)[k];
+            }
+        }
+    };
+    auto commit_x = [&](int buf) {
 #pragma unroll
-        for (int c = 0; c < NX; ++c)
-            if (tid + 256 * c < GX_CHUNKS) xsh[buf][tid + 256 * c] = px[c];
+        for (int c = 0; c < GNX; ++c)
+            if (tid + GTHREADS * c < GX_CHUNKS) xsh[buf][tid + GTHREADS * c] = px[c];
+    };
+    auto commit_w = [&](int buf) {
+#pragma unroll
+        for (int c = 0; c < GNW; ++c)
+            if (tid + GTHREADS * c < GW_CHUNKS) wsh[buf][tid + GTHREADS * c] = pw[c];
     };
 
-    float acc[4][4], mn[4][4];
+    float acc[4][GRT][4], mn[4][GRT][4];
 #pragma unroll
-    for (int rt = 0; rt < 4; ++rt)
+    for (int tt = 0; tt < 4; ++tt)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) acc[rt][r] = mn[rt][r] = 0.0f;
+        for (int rt = 0; rt < GRT; ++rt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[tt][rt][r] = mn[tt][rt][r] = 0.0f;
+    const i32x4 magic = {kMagic, kMagic, kMagic, kMagic};
 
-    issue(0);
-    commit(0);
+    issue_x(0);
+    issue_w(0);
+    commit_x(0);
+    commit_w(0);
     __syncthreads();
     for (int b = 0; b < nb; ++b) {
         const int buf = b & 1;
-        if (b + 1 < nb) issue(b + 1);
+        const bool more = b + 1 < nb;
+        if (more) issue_x(b + 1);
         const uint32_t* W = reinterpret_cast<const uint32_t*>(wsh[buf]);
         const uint32_t* X = reinterpret_cast<const uint32_t*>(xsh[buf]);
-        // This lane's A rows: token 16 wave + l16; its D rows: tokens 16 wave + 4 lg + r.
-        const uint32_t* xa = X + (16 * wave + l16) * Q8K_WORDS;
-        float dx[4];
+        // D rows of tile tt: tokens 16 tt + 4 lg + r; A rows: token 16 tt + l16.
+        float dx[4][4];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) dx[r] = __builtin_bit_cast(float, X[(16 * wave + 4 * lg + r) * Q8K_WORDS]);
-        // Pair sums of bsums for the min term's A operand: j = lg and lg + 4.
-        float pa[2];
+        for (int tt = 0; tt < 4; ++tt)
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const uint32_t p = xa[Q8K_BS + lg + 4 * h];
-            pa[h] = (float)((int)(int16_t)(p & 0xffff) + (int)(int16_t)(p >> 16));
+            for (int r = 0; r < 4; ++r)
+                dx[tt][r] = __builtin_bit_cast(float, X[(16 * tt + 4 * lg + r) * Q8K_WORDS]);
+        const uint32_t* wr[GRT];
+        float dw[GRT], dmw[GRT];
+        uint32_t sl[GRT], sh[GRT], s1[GRT], s2[GRT];
+#pragma unroll
+        for (int rt = 0; rt < GRT; ++rt) {
+            wr[rt] = W + (16 * GRT * wave + 16 * rt + l16) * (Q4K_BYTES / 4);
+            const uint32_t hdr = wr[rt][0], S0 = wr[rt][1];
+            s1[rt] = wr[rt][2];
+            s2[rt] = wr[rt][3];
+            dw[rt] = half_bits_to_float(hdr & 0xffff);
+            dmw[rt] = half_bits_to_float(hdr >> 16);
+            sl[rt] = S0 & 0x3f3f3f3fu;                                   // scales 0-3
+            sh[rt] = (s2[rt] & 0x0f0f0f0fu) | ((S0 >> 2) & 0x30303030u);  // scales 4-7
         }
+        float cs[4][GRT][4];
 #pragma unroll
-        for (int rt = 0; rt < 4; ++rt) {
-            const uint32_t* wb = W + (16 * rt + l16) * (Q4K_BYTES / 4);
-            const uint32_t hdr = wb[0], S0 = wb[1], S1 = wb[2], S2 = wb[3];
-            const float dw = half_bits_to_float(hdr & 0xffff), dmw = half_bits_to_float(hdr >> 16);
-            float cs[4], cm[4];
+        for (int tt = 0; tt < 4; ++tt)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                cs[r] = dw * dx[r];
-                cm[r] = dmw * dx[r];
+            for (int rt = 0; rt < GRT; ++rt)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) cs[tt][rt][r] = dw[rt] * dx[tt][r];
+        uint32_t wq[GRT][2] = {};
+#pragma unroll
+        for (int sb = 0; sb < 8; ++sb) {
+            const int g = sb >> 1, hi = sb & 1;
+            if (!hi) {
+#pragma unroll
+                for (int rt = 0; rt < GRT; ++rt) {
+                    wq[rt][0] = wr[rt][4 + 8 * g + 2 * lg];
+                    wq[rt][1] = wr[rt][4 + 8 * g + 2 * lg + 1];
+                }
+            }
+            long bv[GRT];
+            float scf[GRT], negc[GRT];
+#pragma unroll
+            for (int rt = 0; rt < GRT; ++rt) {
+                const uint32_t b0 = hi ? (wq[rt][0] >> 4) & 0x0f0f0f0fu : wq[rt][0] & 0x0f0f0f0fu;
+                const uint32_t b1 = hi ? (wq[rt][1] >> 4) & 0x0f0f0f0fu : wq[rt][1] & 0x0f0f0f0fu;
+                bv[rt] = (long)(((unsigned long)b1 << 32) | b0);
+                scf[rt] = (float)(((sb < 4 ? sl[rt] : sh[rt]) >> (8 * (sb & 3))) & 0xffu);
+                negc[rt] = scf[rt] * -kMagicF;
             }
 #pragma unroll
-            for (int sb = 0; sb < 8; ++sb) {
-                const int g = sb >> 1, hi = sb & 1;
-                const int sc = sb < 4 ? (int)((S0 >> (8 * sb)) & 63)
-                                      : (int)(((S2 >> (8 * (sb - 4))) & 15) | (((S0 >> (8 * (sb - 4) + 6)) & 3) << 4));
-                const uint32_t a0 = xa[Q8K_QS + 16 * g + 8 * hi + 2 * lg], a1 = xa[Q8K_QS + 16 * g + 8 * hi + 2 * lg + 1];
-                const uint32_t w0 = wb[4 + 8 * g + 2 * lg], w1 = wb[4 + 8 * g + 2 * lg + 1];
-                const uint32_t b0 = hi ? (w0 >> 4) & 0x0f0f0f0fu : w0 & 0x0f0f0f0fu;
-                const uint32_t b1 = hi ? (w1 >> 4) & 0x0f0f0f0fu : w1 & 0x0f0f0f0fu;
-                const long av = (long)(((unsigned long)a1 << 32) | a0);
-                const long bv = (long)(((unsigned long)b1 << 32) | b0);
-                const i32x4 dot = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, bv, i32x4{0, 0, 0, 0}, 0, 0, 0);
+            for (int tt = 0; tt < 4; ++tt) {
+                const uint2 a = *reinterpret_cast<const uint2*>(X + (16 * tt + l16) * Q8K_WORDS + Q8K_QS + 8 * sb + 2 * lg);
+                const long av = (long)(((unsigned long)a.y << 32) | a.x);
 #pragma unroll
-                for (int r = 0; r < 4; ++r) acc[rt][r] = fmaf((float)__mul24(sc, dot[r]), cs[r], acc[rt][r]);
+                for (int rt = 0; rt < GRT; ++rt) {
+                    const i32x4 d = __builtin_amdgcn_mfma_i32_16x16x32_i8(av, bv[rt], magic, 0, 0, 0);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        // __int_as_float of the element's value: __builtin_bit_cast on a
+                        // vector element reads the vector's first word.
+                        const float t = fmaf(__int_as_float(d[r]), scf[rt], negc[rt]);
+                        acc[tt][rt][r] = fmaf(t, cs[tt][rt][r], acc[tt][rt][r]);
+                    }
+                }
             }
-            // mins of j = lg and lg + 4 for this lane's row
-            const float m0 = (float)((S1 >> (8 * lg)) & 63);
-            const float m1 = (float)(((S2 >> (8 * lg + 4)) & 15) | (((S1 >> (8 * lg + 6)) & 3) << 4));
-            f32x4 md = __builtin_amdgcn_mfma_f32_16x16x4f32(pa[0], m0, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-            md = __builtin_amdgcn_mfma_f32_16x16x4f32(pa[1], m1, md, 0, 0, 0);
-#pragma unroll
-            for (int r = 0; r < 4; ++r) mn[rt][r] = fmaf(md[r], cm[r], mn[rt][r]);
+            if (sb == 3 && more) {
+                commit_x(buf ^ 1);
+                issue_w(b + 1);
+            }
+            // keep each sub-block's MFMA results to its own four quads
+            __builtin_amdgcn_sched_barrier(0);
         }
-        if (b + 1 < nb) commit(buf ^ 1);
+        // Min term: j = lg and lg + 4 of this lane's row (B) and token (A).
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt) {
+            const uint32_t* xa = X + (16 * tt + l16) * Q8K_WORDS + Q8K_BS;
+            float pa[2];
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const uint32_t p = xa[lg + 4 * h];
+                pa[h] = (float)((int)(int16_t)(p & 0xffff) + (int)(int16_t)(p >> 16));
+            }
+#pragma unroll
+            for (int rt = 0; rt < GRT; ++rt) {
+                const float m0 = (float)((s1[rt] >> (8 * lg)) & 63);
+                const float m1 = (float)(((s2[rt] >> (8 * lg + 4)) & 15) | (((s1[rt] >> (8 * lg + 6)) & 3) << 4));
+                f32x4 md = __builtin_amdgcn_mfma_f32_16x16x4f32(pa[0], m0, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                md = __builtin_amdgcn_mfma_f32_16x16x4f32(pa[1], m1, md, 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    // dx again from LDS rather than live across the sub-blocks
+                    const float dxr = __builtin_bit_cast(float, X[(16 * tt + 4 * lg + r) * Q8K_WORDS]);
+                    mn[tt][rt][r] = fmaf(md[r], dmw[rt] * dxr, mn[tt][rt][r]);
+                }
+            }
+        }
+        if (more) commit_w(buf ^ 1);
         __syncthreads();
     }
 #pragma unroll
-    for (int rt = 0; rt < 4; ++rt) {
-        const int row = row0 + 16 * rt + l16;
+    for (int tt = 0; tt < 4; ++tt)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            const int t = tok0 + 16 * wave + 4 * lg + r;
-            if (row < n_rows && t < tokens) y[(size_t)t * n_out + row] = acc[rt][r] - mn[rt][r];
+        for (int rt = 0; rt < GRT; ++rt) {
+            const int row = row0 + 16 * GRT * wave + 16 * rt + l16;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int t = tok0 + 16 * tt + 4 * lg + r;
+                if (row < n_rows && t < tokens) y[(size_t)t * n_out + row] = acc[tt][rt][r] - mn[tt][rt][r];
+            }
         }
-    }
 }
 
 }  // namespace
@@ -528,7 +598,7 @@ hipError_t launch_linear_q_prequant(q35m_ctx* c, int qtype, const void* w, const
     const int row_base = (qtype == 4 && tokens > 1) ? (n_out & ~7) : 0;
     if (row_base > 0) {
         ProfScope ps_(c, K_Q4K_GEMM);
-        hipExtLaunchKernelGGL(q4k_gemm, dim3((row_base + GR - 1) / GR, (tokens + GT - 1) / GT), dim3(256), 0,
+        hipExtLaunchKernelGGL(q4k_gemm, dim3((row_base + GR - 1) / GR, (tokens + GT - 1) / GT), dim3(GTHREADS), 0,
                               c->stream, ps_.a, ps_.b, 0, wb, qb, y, n_in, row_base, n_out, tokens);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess || row_base == n_out) return e;
