@@ -135,7 +135,7 @@ const char* kernel_name(int id) {
         "dn_chunk_scan",          "dn_chunk_out",            "attn_decode_partial",
         "attn_decode_merge",      "attn_prefill_prep",       "attn_prefill_flash",
         "q8k_quantize",           "linear_q<4>",             "linear_q<6>",
-        "q4k_gemm"};
+        "q4k_gemm", "q6k_gemm"};
     return (id >= 0 && id < K_COUNT) ? names[id] : nullptr;
 }
 

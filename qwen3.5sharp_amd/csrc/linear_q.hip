@@ -578,6 +578,177 @@ void q4k_gemm(const unsigned char* __restrict__ w, const uint32_t* __restrict__ 
         }
 }
 
+
+// ---------------------------------------------------------------- Q6_K, several tokens
+
+// The reference's Q6_K path for several tokens keeps the GEMV's arithmetic
+// per (token, output row) (Q6K.Gemm, Q6K.cs:301-413, over Q6K.DotAvx2,
+// Q6K.cs:87-165): per block, 8 integer lanes sumi[k] = sum over j < 2, m < 4,
+// i < 4 of scales[8j + 2m + k/4] * v * q8 (v the unsigned 6-bit value of byte
+// b = 4k + i of part j, m), minus 32 (bsums[2k] scales[2k] + bsums[2k+1]
+// scales[2k+1]); acc[k] = fma(dx * dw, (float)sumi[k], acc[k]); out =
+// hsum8(acc).  Each sumi[k] is exact in int32, so it is formed on
+// v_mfma_i32_16x16x32_i8: K runs over lane k's 32 bytes (j, m, i), with the
+// weights scales * v (|.| <= 8064) split into two int8 planes, 128 hi + lo;
+// a second K-chunk of 32 adds the bsums term as q8[32k .. 32k + 31] times
+// -32 * scales[2k + (value / 16 odd)], split the same way.  sumi = (D_hi << 7)
+// + D_lo.  A workgroup takes 64 tokens x 32 rows; a wave 32 tokens x 16 rows
+// (8 fp32 lane accumulators an output, as the reference keeps them).  Q6_K
+// blocks are 2-byte aligned: each is staged into LDS realigned to 4 bytes.
+constexpr int SGT = 64, SGR = 32;
+constexpr int S_WD = 53;                                // dwords of a realigned block (212 B)
+constexpr int SX_CHUNKS = SGT * Q8K_WORDS / 4;          // 1216
+constexpr int SNX = (SX_CHUNKS + 255) / 256;
+
+typedef short s16x2 __attribute__((ext_vector_type(2)));
+
+// Four unsigned 6-bit values (bytes of v) times sc, as the low (& 127) and
+// high (>> 7) int8 planes of the products.
+__device__ __forceinline__ void q6k_split(uint32_t v, int sc, uint32_t& lo, uint32_t& hi) {
+    const s16x2 s2 = {(short)sc, (short)sc};
+    const s16x2 a = __builtin_bit_cast(s16x2, __builtin_amdgcn_perm(0u, v, 0x0c010c00u)) * s2;
+    const s16x2 b = __builtin_bit_cast(s16x2, __builtin_amdgcn_perm(0u, v, 0x0c030c02u)) * s2;
+    const uint32_t al = __builtin_bit_cast(uint32_t, a) & 0x007f007fu, bl = __builtin_bit_cast(uint32_t, b) & 0x007f007fu;
+    const uint32_t ah = __builtin_bit_cast(uint32_t, a >> (short)7), bh = __builtin_bit_cast(uint32_t, b >> (short)7);
+    lo = __builtin_amdgcn_perm(bl, al, 0x06040200u);
+    hi = __builtin_amdgcn_perm(bh, ah, 0x06040200u);
+}
+
+__global__ __launch_bounds__(256) void q6k_gemm(const unsigned char* __restrict__ w,
+                                                const uint32_t* __restrict__ q8,
+                                                float* __restrict__ y, int n_in, int n_out, int tokens) {
+#pragma clang fp contract(off)
+    const int nb = n_in / QK;
+    const int row0 = blockIdx.x * SGR, tok0 = blockIdx.y * SGT;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int l16 = lane & 15, lg = lane >> 4;
+    const int rt = wave & 1, tp = wave >> 1;                // row tile; token tiles 2 tp, 2 tp + 1
+
+    __shared__ uint4 xsh[2][SX_CHUNKS];
+    __shared__ uint32_t wsh[2][SGR * S_WD];
+
+    const size_t total = (size_t)n_out * nb * Q6K_BYTES;
+    const int wrow = tid >> 3, wpart = tid & 7;             // staging: row, dwords 7 wpart .. +6
+    uint4 px[SNX];
+    uint32_t pw[8];
+    int wshift = 0;
+    auto issue = [&](int b) {
+#pragma unroll
+        for (int c = 0; c < SNX; ++c) {
+            const int i = tid + 256 * c;
+            px[c] = make_uint4(0u, 0u, 0u, 0u);
+            if (i < SX_CHUNKS) {
+                const int t = i / 19, k = i % 19;
+                px[c] = reinterpret_cast<const uint4*>(
+                    q8 + ((size_t)min(tok0 + t, tokens - 1) * nb + b) * Q8K_WORDS)[k];
+            }
+        }
+        const size_t s = ((size_t)min(row0 + wrow, n_out - 1) * nb + b) * Q6K_BYTES;
+        const size_t s4 = s & ~(size_t)3;
+        wshift = (int)(s - s4);
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+            const int d = 7 * wpart + c;
+            const size_t off = s4 + 4 * (size_t)d;
+            pw[c] = 0u;
+            if (d <= S_WD) {
+                if (off + 4 <= total) pw[c] = *reinterpret_cast<const uint32_t*>(w + off);
+                else if (off < total) pw[c] = *reinterpret_cast<const uint16_t*>(w + off);
+            }
+        }
+    };
+    auto commit = [&](int buf) {
+#pragma unroll
+        for (int c = 0; c < SNX; ++c)
+            if (tid + 256 * c < SX_CHUNKS) xsh[buf][tid + 256 * c] = px[c];
+#pragma unroll
+        for (int c = 0; c < 7; ++c) {
+            const int a = 7 * wpart + c;
+            if (a < S_WD) wsh[buf][wrow * S_WD + a] = __builtin_amdgcn_alignbyte(pw[c + 1], pw[c], wshift);
+        }
+    };
+
+    float acc[2][8][4];
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[tt][k][r] = 0.0f;
+    const i32x4 zero = {0, 0, 0, 0};
+    const int j = lg >> 1, odd = lg & 1;
+
+    issue(0);
+    commit(0);
+    __syncthreads();
+    for (int b = 0; b < nb; ++b) {
+        const int buf = b & 1;
+        if (b + 1 < nb) issue(b + 1);
+        const uint32_t* X = reinterpret_cast<const uint32_t*>(xsh[buf]);
+        const uint32_t* WB = wsh[buf] + (16 * rt + l16) * S_WD;
+        const float dw = half_bits_to_float(WB[52] & 0xffff);
+        float d[2][4];
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                d[tt][r] = __builtin_bit_cast(float, X[(16 * (2 * tp + tt) + 4 * lg + r) * Q8K_WORDS]) * dw;
+        uint32_t scw[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) scw[q] = WB[48 + q];
+        auto scale = [&](int idx) { return (int)(int8_t)((scw[idx >> 2] >> (8 * (idx & 3))) & 0xff); };
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const int half = k >> 2;
+            // this lane's K values: (j, m0, 4k..4k+3) and (j, m0 + 1, 4k..4k+3), m0 = 2 odd
+            const uint32_t qa = WB[16 * j + k], qb = WB[16 * j + 8 + k], qh = WB[32 + 8 * j + k];
+            const uint32_t v0 = odd ? ((qa >> 4) & 0x0f0f0f0fu) | (qh & 0x30303030u)
+                                    : (qa & 0x0f0f0f0fu) | ((qh & 0x03030303u) << 4);
+            const uint32_t v1 = odd ? ((qb >> 4) & 0x0f0f0f0fu) | ((qh & 0xc0c0c0c0u) >> 2)
+                                    : (qb & 0x0f0f0f0fu) | ((qh & 0x0c0c0c0cu) << 2);
+            const int m0 = 2 * odd;
+            uint32_t l0, h0, l1, h1;
+            q6k_split(v0, scale(8 * j + 2 * m0 + half), l0, h0);
+            q6k_split(v1, scale(8 * j + 2 * m0 + 2 + half), l1, h1);
+            const long blo = (long)(((unsigned long)l1 << 32) | l0), bhi = (long)(((unsigned long)h1 << 32) | h0);
+            // bsums term: values 32k + 8 lg .. +7 lie in sub-block 2k + j
+            const int c = -32 * scale(2 * k + j);
+            const uint32_t elo = (uint32_t)(c & 127) * 0x01010101u, ehi = (uint32_t)((c >> 7) & 0xff) * 0x01010101u;
+            const long eblo = (long)(((unsigned long)elo << 32) | elo), ebhi = (long)(((unsigned long)ehi << 32) | ehi);
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt) {
+                const uint32_t* xt = X + (16 * (2 * tp + tt) + l16) * Q8K_WORDS + Q8K_QS;
+                const long am = (long)(((unsigned long)xt[32 * j + 8 * (m0 + 1) + k] << 32) | xt[32 * j + 8 * m0 + k]);
+                const uint2 e = *reinterpret_cast<const uint2*>(xt + 8 * k + 2 * lg);
+                const long ae = (long)(((unsigned long)e.y << 32) | e.x);
+                i32x4 dh = __builtin_amdgcn_mfma_i32_16x16x32_i8(am, bhi, zero, 0, 0, 0);
+                dh = __builtin_amdgcn_mfma_i32_16x16x32_i8(ae, ebhi, dh, 0, 0, 0);
+                i32x4 dl = __builtin_amdgcn_mfma_i32_16x16x32_i8(am, blo, zero, 0, 0, 0);
+                dl = __builtin_amdgcn_mfma_i32_16x16x32_i8(ae, eblo, dl, 0, 0, 0);
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int hr = dh[r], lr = dl[r];
+                    const int sumi = (int)((unsigned)hr << 7) + lr;
+                    acc[tt][k][r] = fmaf(d[tt][r], (float)sumi, acc[tt][k][r]);
+                }
+            }
+        }
+        if (b + 1 < nb) commit(buf ^ 1);
+        __syncthreads();
+    }
+    const int row = row0 + 16 * rt + l16;
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int t = tok0 + 16 * (2 * tp + tt) + 4 * lg + r;
+            const float h[8] = {acc[tt][0][r], acc[tt][1][r], acc[tt][2][r], acc[tt][3][r],
+                                acc[tt][4][r], acc[tt][5][r], acc[tt][6][r], acc[tt][7][r]};
+            if (row < n_out && t < tokens) y[(size_t)t * n_out + row] = hsum8(h);
+        }
+}
+
 }  // namespace
 
 hipError_t launch_q8k_quantize(q35m_ctx* c, const float* x, void* q8, int n_in, int tokens) {
@@ -602,6 +773,12 @@ hipError_t launch_linear_q_prequant(q35m_ctx* c, int qtype, const void* w, const
                               c->stream, ps_.a, ps_.b, 0, wb, qb, y, n_in, row_base, n_out, tokens);
         hipError_t e = hipGetLastError();
         if (e != hipSuccess || row_base == n_out) return e;
+    }
+    if (qtype == 6 && tokens > 1) {
+        ProfScope ps_(c, K_Q6K_GEMM);
+        hipExtLaunchKernelGGL(q6k_gemm, dim3((n_out + SGR - 1) / SGR, (tokens + SGT - 1) / SGT), dim3(256), 0,
+                              c->stream, ps_.a, ps_.b, 0, wb, qb, y, n_in, n_out, tokens);
+        return hipGetLastError();
     }
     const int rows_per_wg = min(LQ_THREADS / nb, LQ_MAX_ROWS);
     const int grid = (n_out - row_base + rows_per_wg - 1) / rows_per_wg;

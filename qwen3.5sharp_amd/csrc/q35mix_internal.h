@@ -70,6 +70,7 @@ enum KernelId {
     K_Q4K_LINEAR,
     K_Q6K_LINEAR,
     K_Q4K_GEMM,
+    K_Q6K_GEMM,
     K_COUNT
 };
 const char* kernel_name(int id);
