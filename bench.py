@@ -458,6 +458,14 @@ def main():
             "int8_mfma_frac": 2 * macs / (ms / 1e3) / INT8_PEAK,
             "kernels_ms": {k: v[0] for k, v in kt.items()}}
         log(f"[bench] linear_q4k_2560x8192_t2048: {workloads['linear_q4k_2560x8192_t2048']}")
+        log("[bench] Q6_K projection 4096 -> 2560, 2048 tokens ...")
+        ms, kt, by = bench_linear_q(6, 4096, 2560, K, W, 1, tokens=2048)
+        macs = 2048 * 4096 * 2560
+        workloads["linear_q6k_4096x2560_t2048"] = {
+            "ms": ms, "tokens_per_s": 2048 / (ms / 1e3),
+            "int8_mfma_frac": 2 * macs / (ms / 1e3) / INT8_PEAK,
+            "kernels_ms": {k: v[0] for k, v in kt.items()}}
+        log(f"[bench] linear_q6k_4096x2560_t2048: {workloads['linear_q6k_4096x2560_t2048']}")
     for qtype, n_in, n_out, copies in ((4, 2560, 8192, 32), (6, 4096, 2560, 40)):
         if not want("linear_q"):
             break
