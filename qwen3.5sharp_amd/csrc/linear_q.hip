@@ -774,7 +774,10 @@ hipError_t launch_linear_q_prequant(q35m_ctx* c, int qtype, const void* w, const
         hipError_t e = hipGetLastError();
         if (e != hipSuccess || row_base == n_out) return e;
     }
-    if (qtype == 6 && tokens > 1) {
+    // Q6_K: the tiled kernel from 16 tokens (one workgroup row of 64 tokens
+    // costs about 44 us at 4096 -> 2560, what 16 per-token GEMV passes take);
+    // both keep the same per-token arithmetic, so the results are identical.
+    if (qtype == 6 && tokens >= 16) {
         ProfScope ps_(c, K_Q6K_GEMM);
         hipExtLaunchKernelGGL(q6k_gemm, dim3((n_out + SGR - 1) / SGR, (tokens + SGT - 1) / SGT), dim3(256), 0,
                               c->stream, ps_.a, ps_.b, 0, wb, qb, y, n_in, n_out, tokens);

@@ -46,7 +46,7 @@ def run(ctx, qtype, w, x, n_in, n_out):
 
 SHAPES = [(2560, 8192, 1), (2560, 4096, 1), (2560, 32, 1), (4096, 2560, 1), (2560, 1024, 1),
           (256, 7, 1), (512, 33, 5), (2560, 1024, 3), (16384, 19, 2), (2560, 520, 70),
-          (4096, 136, 130)]
+          (4096, 136, 130), (512, 40, 16), (1024, 72, 15)]
 
 
 @pytest.mark.parametrize("qtype", [4, 6])
