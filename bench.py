@@ -211,6 +211,26 @@ def bench_linear_q(qtype, n_in, n_out, steps, warmup, copies, tokens=1):
     return ms, kt, w.nbytes + 4 * (n_in + n_out)
 
 
+def bench_boundary(dim, tokens, steps, warmup):
+    """The layer boundary: hidden += delta, y = RmsNormZeroCentered(hidden, w)
+    and its Q8_K blocks, over `tokens` rows of dim."""
+    ctx = q35mix.Context(q35mix.qwen35_config(num_layers=1, is_recurrent=[1]), 1, 16)
+    h = ctx.array((tokens, dim), synth.normal(41, tokens * dim))
+    d = ctx.array((tokens, dim), synth.normal(42, tokens * dim))
+    w = ctx.array((dim,), 0.02 * synth.normal(43, dim))
+    y = ctx.array((tokens, dim))
+    q8 = q35mix.DeviceBytes(ctx, np.zeros(q35mix.lib().q35m_q8k_bytes(dim, tokens), np.uint8))
+
+    def step(i):
+        ctx.add_rmsnorm(h, d, w, y, q8, dim, tokens, 1e-6)
+
+    ms = time_calls(ctx, step, steps, warmup)
+    kt = kernel_times(ctx, step, steps)
+    ctx.close()
+    # read hidden, delta and w; write hidden, y and the Q8_K blocks
+    return ms, kt, 16 * tokens * dim + 4 * dim + q35mix.lib().q35m_q8k_bytes(dim, tokens)
+
+
 def bench_stack(n_steps=128, warmup=4, n_seqs=8, ctx_len=32768, n_layers=32):
     """32-layer mixer stack, 8 sequences decoding from context 32640 to 32768."""
     is_rec = [(i + 1) % 4 != 0 for i in range(n_layers)]
@@ -466,6 +486,13 @@ def main():
             "int8_mfma_frac": 2 * macs / (ms / 1e3) / INT8_PEAK,
             "kernels_ms": {k: v[0] for k, v in kt.items()}}
         log(f"[bench] linear_q6k_4096x2560_t2048: {workloads['linear_q6k_4096x2560_t2048']}")
+    if want("boundary"):
+        log("[bench] layer boundary (add + RMSNorm + Q8_K), 2048 x 2560 ...")
+        ms, kt, by = bench_boundary(2560, 2048, K, W)
+        workloads["boundary_2048x2560"] = {
+            "us": ms * 1e3, "bytes": by, "hbm_frac_call": by / (ms / 1e3) / HBM_PEAK,
+            "kernels_us": {k: v[0] * 1e3 for k, v in kt.items()}}
+        log(f"[bench] boundary_2048x2560: {workloads['boundary_2048x2560']}")
     for qtype, n_in, n_out, copies in ((4, 2560, 8192, 32), (6, 4096, 2560, 40)):
         if not want("linear_q"):
             break

@@ -182,6 +182,23 @@ int q35m_linear_q4k(q35m_ctx* ctx, const void* w, const float* x, float* y, int 
 int q35m_linear_q6k(q35m_ctx* ctx, const void* w, const float* x, float* y, int n_in, int n_out,
                     int tokens);
 
+/* The layer boundary around a mixer: hidden[t] += delta[t] (fp32 adds,
+ * written back; delta NULL: no add), then y[t] = RmsNormZeroCentered(hidden[t],
+ * weight) = (h * scale) * (1 + weight) with scale = 1 / sqrt(mean(h^2) + eps),
+ * the sum of squares in the reference's order (8 FMA lanes, horizontal sum,
+ * dim % 8 tail) (weight NULL: 0).  When q8 is non-NULL y is also written as
+ * Q8_K blocks (q35m_q8k_bytes(dim, tokens) bytes, as q35m_quantize_q8k writes
+ * them) for the projection that follows; y may then be NULL.  All rows
+ * [tokens][dim] fp32 in device memory, buffers 16-byte aligned; dim a multiple
+ * of 4 up to 16384 (of 256 with q8).  Replaces Ops.AddInPlace
+ * (src/Qwen35Sharp.Model/Ops.cs:677-710) followed by
+ * Qwen35Ops.RmsNormZeroCentered (src/Qwen35Sharp.Model/Qwen35Ops.cs:22-64), as
+ * Qwen35Model.DecodeBlock uses them (Qwen35Model.Decode.cs:226-235: attn_norm
+ * with delta NULL, then the residual add and post_attention_norm); results
+ * are bit-identical to the reference's. */
+int q35m_add_rmsnorm(q35m_ctx* ctx, float* hidden, const float* delta, const float* weight, float* y, void* q8,
+                     int dim, int tokens, float eps);
+
 /* The same in two steps, for several projections of one activation:
  * q35m_quantize_q8k writes the Q8_K blocks of x [tokens][n_in] into a device
  * buffer of q35m_q8k_bytes(n_in, tokens) bytes (a BlockQ8K's fields in

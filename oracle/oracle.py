@@ -288,3 +288,16 @@ def linear_q(qtype: int, w, x, n_in, n_out) -> np.ndarray:
     lib().q35o_linear_q(ctypes.c_int(qtype), w.ctypes.data_as(_U8), _p(x), _p(y),
                         ctypes.c_int(n_in), ctypes.c_int(n_out), ctypes.c_int(x.shape[0]))
     return y
+
+
+def add_rmsnorm(hidden, delta, w, dim, eps=1e-6):
+    """Ops.AddInPlace then Qwen35Ops.RmsNormZeroCentered over rows of dim:
+    returns (hidden after the add, y).  delta / w may be None."""
+    h = _f32(hidden).reshape(-1, dim).copy()
+    rows = h.shape[0]
+    d = None if delta is None else _f32(delta).reshape(rows, dim).copy()
+    ww = None if w is None else _f32(w).ravel().copy()
+    y = np.empty_like(h)
+    lib().q35o_add_rmsnorm(_p(h), None if d is None else _p(d), None if ww is None else _p(ww), _p(y),
+                           ctypes.c_int(dim), ctypes.c_int(rows), ctypes.c_float(eps))
+    return h, y

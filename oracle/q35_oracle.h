@@ -99,4 +99,8 @@ void q35o_linear_q(int type, const void* w, const float* x, float* y, int n_in, 
 #ifdef __cplusplus
 }
 #endif
+/* Ops.AddInPlace + Qwen35Ops.RmsNormZeroCentered (q35_oracle_norm.c). */
+void q35o_add_rmsnorm(float* hidden, const float* delta, const float* w, float* y, int dim, int rows,
+                      float eps);
+
 #endif

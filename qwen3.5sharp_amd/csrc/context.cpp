@@ -135,7 +135,7 @@ const char* kernel_name(int id) {
         "dn_chunk_scan",          "dn_chunk_out",            "attn_decode_partial",
         "attn_decode_merge",      "attn_prefill_prep",       "attn_prefill_flash",
         "q8k_quantize",           "linear_q<4>",             "linear_q<6>",
-        "q4k_gemm", "q6k_gemm"};
+        "q4k_gemm", "q6k_gemm", "add_rmsnorm"};
     return (id >= 0 && id < K_COUNT) ? names[id] : nullptr;
 }
 
@@ -521,6 +521,21 @@ int q35m_quantize_q8k(q35m_ctx* ctx, const float* x, void* q8, int n_in, int tok
         return fail(Q35M_ERR_INVALID, "input and Q8_K buffer must be 16-byte aligned");
     if ((r = check_linear_dims(n_in, 1, tokens))) return r;
     HIP_TRY(q35::launch_q8k_quantize(ctx, x, q8, n_in, tokens), "quantize_q8k");
+    return Q35M_OK;
+}
+
+int q35m_add_rmsnorm(q35m_ctx* ctx, float* hidden, const float* delta, const float* weight, float* y, void* q8,
+                     int dim, int tokens, float eps) {
+    int r = check_ctx(ctx);
+    if (r) return r;
+    if (!hidden || (!y && !q8)) return fail(Q35M_ERR_INVALID, "null hidden, or neither y nor q8 given");
+    if (((uintptr_t)hidden | (uintptr_t)delta | (uintptr_t)weight | (uintptr_t)y | (uintptr_t)q8) & 15)
+        return fail(Q35M_ERR_INVALID, "buffers must be 16-byte aligned");
+    if (tokens < 1 || dim < 4) return fail(Q35M_ERR_INVALID, "dim %d, tokens %d", dim, tokens);
+    if (dim % 4 || dim > 16384) return fail(Q35M_ERR_UNSUPPORTED, "dim %d: a multiple of 4 up to 16384", dim);
+    if (q8 && dim % 256) return fail(Q35M_ERR_UNSUPPORTED, "Q8_K output needs dim a multiple of 256 (%d)", dim);
+    if (!(eps >= 0.0f)) return fail(Q35M_ERR_INVALID, "eps must be >= 0");
+    HIP_TRY(q35::launch_add_rmsnorm(ctx, hidden, delta, weight, y, q8, dim, tokens, eps), "add_rmsnorm");
     return Q35M_OK;
 }
 

@@ -48,23 +48,11 @@ __device__ __forceinline__ float half_bits_to_float(uint32_t h) {
     return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(h)));
 }
 
-// Q8K.QuantizeRow / ScaleBlock (Q8K.cs:12-146), four 256-value blocks of one
-// token per wave: a 16-lane group per block, 16 consecutive values a lane (so
-// a lane's values are exactly one bsums group).  amax = max |x|; the scale's
-// sign is that of the first element of magnitude amax; iscale = -127 / max
-// (IEEE division), delta = 1 / iscale; q = clamp(round-half-even(x * iscale),
-// -127, 127).  Output: Q8_K blocks [tokens][nb] in the workspace form above.
-__global__ __launch_bounds__(kWave) void q8k_quantize(const float* __restrict__ x,
-                                                      uint32_t* __restrict__ q8, int nb) {
-    const int lane = threadIdx.x, grp = lane >> 4, li = lane & 15;
-    const int t = blockIdx.y, b = 4 * blockIdx.x + grp, bb = min(b, nb - 1);
-    const float4* src = reinterpret_cast<const float4*>(x + ((size_t)t * nb + bb) * QK + 16 * li);
-    float v[16];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const float4 f = src[i];
-        v[4 * i] = f.x; v[4 * i + 1] = f.y; v[4 * i + 2] = f.z; v[4 * i + 3] = f.w;
-    }
+// The Q8_K block of 256 values held 16 a lane by a 16-lane group (lane li of
+// the group: values 16 li .. 16 li + 15, one bsums group); every lane of the
+// wave takes part in the shuffles.  blk null: nothing is written.
+__device__ __forceinline__ void q8k_from16(const float (&v)[16], int lane, uint32_t* blk) {
+    const int li = lane & 15;
     float amax = 0.0f;
 #pragma unroll
     for (int i = 0; i < 16; ++i) amax = fmaxf(amax, fabsf(v[i]));
@@ -93,12 +81,31 @@ __global__ __launch_bounds__(kWave) void q8k_quantize(const float* __restrict__ 
             pk[i >> 2] |= (uint32_t)(q & 0xff) << (8 * (i & 3));
         }
     }
-    if (b < nb) {
-        uint32_t* blk = q8 + ((size_t)t * nb + b) * Q8K_WORDS;
+    if (blk) {
         *reinterpret_cast<uint4*>(blk + Q8K_QS + 4 * li) = make_uint4(pk[0], pk[1], pk[2], pk[3]);
         reinterpret_cast<int16_t*>(blk + Q8K_BS)[li] = (int16_t)bsum;
         if (li == 0) blk[0] = __builtin_bit_cast(uint32_t, delta);
     }
+}
+
+// Q8K.QuantizeRow / ScaleBlock (Q8K.cs:12-146), four 256-value blocks of one
+// token per wave: a 16-lane group per block, 16 consecutive values a lane (so
+// a lane's values are exactly one bsums group).  amax = max |x|; the scale's
+// sign is that of the first element of magnitude amax; iscale = -127 / max
+// (IEEE division), delta = 1 / iscale; q = clamp(round-half-even(x * iscale),
+// -127, 127).  Output: Q8_K blocks [tokens][nb] in the workspace form above.
+__global__ __launch_bounds__(kWave) void q8k_quantize(const float* __restrict__ x,
+                                                      uint32_t* __restrict__ q8, int nb) {
+    const int lane = threadIdx.x, grp = lane >> 4, li = lane & 15;
+    const int t = blockIdx.y, b = 4 * blockIdx.x + grp, bb = min(b, nb - 1);
+    const float4* src = reinterpret_cast<const float4*>(x + ((size_t)t * nb + bb) * QK + 16 * li);
+    float v[16];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float4 f = src[i];
+        v[4 * i] = f.x; v[4 * i + 1] = f.y; v[4 * i + 2] = f.z; v[4 * i + 3] = f.w;
+    }
+    q8k_from16(v, lane, b < nb ? q8 + ((size_t)t * nb + b) * Q8K_WORDS : nullptr);
 }
 
 // VecDotQ4K.HorizontalSum (VecDotQ4K.cs:145-151).
@@ -749,6 +756,77 @@ __global__ __launch_bounds__(256) void q6k_gemm(const unsigned char* __restrict_
         }
 }
 
+
+// ---------------------------------------------------------------- layer boundary
+
+// Ops.AddInPlace (Ops.cs:677-710) then Qwen35Ops.RmsNormZeroCentered
+// (Qwen35Ops.cs:22-64), as Qwen35Model.DecodeBlock chains them around a mixer
+// (Qwen35Model.Decode.cs:226-235); one wave per row of dim.  h = hidden +
+// delta (fp32 adds, written back), staged in LDS; lanes 0-7 run the
+// reference's 8 FMA lanes over the whole 8-element groups in order, then its
+// horizontal sum and the dim % 8 tail one element at a time; scale = 1 /
+// sqrt(sum / dim + eps) (IEEE); y = (h * scale) * (1 + w).  Q8: y is also
+// written as Q8_K blocks (the Q8K.QuantizeRow of the projection that
+// follows), formed from the same values.  y may alias hidden (the reference
+// normalizes in place): every row is read into LDS before y is written.
+template <bool ADD, bool Q8>
+__global__ __launch_bounds__(kWave) void add_rmsnorm(float* hidden, const float* __restrict__ delta,
+                                                     const float* __restrict__ w, float* y,
+                                                     uint32_t* __restrict__ q8, int dim, float eps) {
+#pragma clang fp contract(off)
+    extern __shared__ float4 rowv[];
+    const float* row = reinterpret_cast<const float*>(rowv);
+    const int lane = threadIdx.x, t = blockIdx.x, n4 = dim >> 2;
+    float4* h4 = reinterpret_cast<float4*>(hidden + (size_t)t * dim);
+    for (int i = lane; i < n4; i += kWave) {
+        float4 v = h4[i];
+        if constexpr (ADD) {
+            const float4 d = reinterpret_cast<const float4*>(delta + (size_t)t * dim)[i];
+            v.x = v.x + d.x; v.y = v.y + d.y; v.z = v.z + d.z; v.w = v.w + d.w;
+            h4[i] = v;
+        }
+        rowv[i] = v;
+    }
+    __syncthreads();
+    float acc = 0.0f;
+    if (lane < 8)
+        for (int j = 0; j < (dim >> 3); ++j) {
+            const float x = row[8 * j + lane];
+            acc = fmaf(x, x, acc);
+        }
+    float a[8];
+#pragma unroll
+    for (int l = 0; l < 8; ++l) a[l] = __shfl(acc, l, kWave);
+    float sum = hsum8(a);
+    for (int i = dim & ~7; i < dim; ++i) {
+        const float sq = row[i] * row[i];
+        sum = sum + sq;
+    }
+    const float scale = 1.0f / sqrtf(sum / (float)dim + eps);
+    if (y) {
+        float4* y4 = reinterpret_cast<float4*>(y + (size_t)t * dim);
+        for (int i = lane; i < n4; i += kWave) {
+            const float4 v = rowv[i];
+            const float4 g = w ? reinterpret_cast<const float4*>(w)[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+            y4[i] = make_float4((v.x * scale) * (1.0f + g.x), (v.y * scale) * (1.0f + g.y),
+                                (v.z * scale) * (1.0f + g.z), (v.w * scale) * (1.0f + g.w));
+        }
+    }
+    if constexpr (Q8) {
+        const int nb = dim / QK, grp = lane >> 4, li = lane & 15;
+        for (int p = 0; p < nb; p += 4) {
+            const int b = p + grp, bb = min(b, nb - 1);
+            float v[16];
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                const int k = bb * QK + 16 * li + i;
+                v[i] = (row[k] * scale) * (1.0f + (w ? w[k] : 0.0f));
+            }
+            q8k_from16(v, lane, b < nb ? q8 + ((size_t)t * nb + b) * Q8K_WORDS : nullptr);
+        }
+    }
+}
+
 }  // namespace
 
 hipError_t launch_q8k_quantize(q35m_ctx* c, const float* x, void* q8, int n_in, int tokens) {
@@ -805,6 +883,20 @@ hipError_t launch_linear_q(q35m_ctx* c, int qtype, const void* w, const float* x
     hipError_t e = launch_q8k_quantize(c, x, c->work, n_in, tokens);
     if (e != hipSuccess) return e;
     return launch_linear_q_prequant(c, qtype, w, c->work, y, n_in, n_out, tokens);
+}
+
+hipError_t launch_add_rmsnorm(q35m_ctx* c, float* hidden, const float* delta, const float* w, float* y, void* q8,
+                              int dim, int tokens, float eps) {
+    ProfScope ps_(c, K_ADD_RMSNORM);
+    uint32_t* qb = reinterpret_cast<uint32_t*>(q8);
+    const size_t lds = (size_t)dim * sizeof(float);
+    auto go = [&](auto kern) {
+        hipExtLaunchKernelGGL(kern, dim3(tokens), dim3(kWave), lds, c->stream, ps_.a, ps_.b, 0, hidden, delta, w, y,
+                              qb, dim, eps);
+    };
+    if (delta) q8 ? go(add_rmsnorm<true, true>) : go(add_rmsnorm<true, false>);
+    else q8 ? go(add_rmsnorm<false, true>) : go(add_rmsnorm<false, false>);
+    return hipGetLastError();
 }
 
 size_t linear_q_work_bytes(int n_in, int tokens) {

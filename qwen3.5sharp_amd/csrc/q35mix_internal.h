@@ -71,6 +71,7 @@ enum KernelId {
     K_Q6K_LINEAR,
     K_Q4K_GEMM,
     K_Q6K_GEMM,
+    K_ADD_RMSNORM,
     K_COUNT
 };
 const char* kernel_name(int id);
@@ -128,6 +129,8 @@ hipError_t launch_attn_prefill(q35m_ctx* c, int layer, int seq, int start, int T
 size_t attn_prefill_work_bytes(const Dims& d, int T);
 hipError_t launch_linear_q(q35m_ctx* c, int qtype, const void* w, const float* x, float* y,
                            int n_in, int n_out, int tokens);
+hipError_t launch_add_rmsnorm(q35m_ctx* c, float* hidden, const float* delta, const float* w, float* y, void* q8,
+                              int dim, int tokens, float eps);
 size_t linear_q_work_bytes(int n_in, int tokens);
 hipError_t launch_q8k_quantize(q35m_ctx* c, const float* x, void* q8, int n_in, int tokens);
 hipError_t launch_linear_q_prequant(q35m_ctx* c, int qtype, const void* w, const void* q8, float* y,

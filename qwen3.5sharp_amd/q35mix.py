@@ -67,6 +67,8 @@ def lib() -> ctypes.CDLL:
             getattr(_lib, name).argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                                             ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
                                             ctypes.c_int]
+        _lib.q35m_add_rmsnorm.argtypes = [ctypes.c_void_p] * 6 + [ctypes.c_int, ctypes.c_int, ctypes.c_float]
+        _lib.q35m_add_rmsnorm.restype = ctypes.c_int
         _lib.q35m_quantize_q8k.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                                            ctypes.c_int, ctypes.c_int]
         _lib.q35m_q8k_bytes.restype = ctypes.c_size_t
@@ -151,6 +153,11 @@ class DeviceBytes(DeviceArray):
         check(lib().q35m_malloc(ctypes.byref(p), max(self.nbytes, 4)))
         self.ptr = p.value
         check(lib().q35m_copy_h2d(self.ctx.handle, self.ptr, a.ctypes.data, a.nbytes))
+
+    def download(self) -> np.ndarray:
+        a = np.empty(self.nbytes, np.uint8)
+        check(lib().q35m_copy_d2h(self.ctx.handle, a.ctypes.data, self.ptr, a.nbytes))
+        return a
 
     def __del__(self):
         try:
@@ -256,6 +263,13 @@ class Context:
         check(lib().q35m_quantize_q8k(ctypes.c_void_p(self.handle), ctypes.c_void_p(x.ptr),
                                       ctypes.c_void_p(q8.ptr), n_in, tokens))
         return q8
+
+    def add_rmsnorm(self, hidden, delta, w, y, q8, dim, tokens, eps=1e-6) -> None:
+        """hidden += delta (delta may be None), y = RmsNormZeroCentered(hidden, w)
+        (w may be None), optionally also as Q8_K blocks into q8 (may be None)."""
+        ptr = lambda a: None if a is None else ctypes.c_void_p(a.ptr)  # noqa: E731
+        check(lib().q35m_add_rmsnorm(ctypes.c_void_p(self.handle), ctypes.c_void_p(hidden.ptr), ptr(delta),
+                                     ptr(w), ptr(y), ptr(q8), dim, tokens, eps))
 
     def linear_q_prequant(self, qtype: int, w, q8, y, n_in, n_out, tokens) -> None:
         fn = lib().q35m_linear_q4k_prequant if qtype == 4 else lib().q35m_linear_q6k_prequant
