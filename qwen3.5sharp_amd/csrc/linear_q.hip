@@ -789,7 +789,9 @@ __global__ __launch_bounds__(kWave) void add_rmsnorm(float* hidden, const float*
     }
     __syncthreads();
     float acc = 0.0f;
+    // unrolled so the LDS reads run ahead of the (strictly ordered) FMA chain
     if (lane < 8)
+#pragma unroll 32
         for (int j = 0; j < (dim >> 3); ++j) {
             const float x = row[8 * j + lane];
             acc = fmaf(x, x, acc);
@@ -803,7 +805,7 @@ __global__ __launch_bounds__(kWave) void add_rmsnorm(float* hidden, const float*
         sum = sum + sq;
     }
     const float scale = 1.0f / sqrtf(sum / (float)dim + eps);
-    if (y) {
+    if (!Q8 && y) {
         float4* y4 = reinterpret_cast<float4*>(y + (size_t)t * dim);
         for (int i = lane; i < n4; i += kWave) {
             const float4 v = rowv[i];
@@ -816,11 +818,22 @@ __global__ __launch_bounds__(kWave) void add_rmsnorm(float* hidden, const float*
         const int nb = dim / QK, grp = lane >> 4, li = lane & 15;
         for (int p = 0; p < nb; p += 4) {
             const int b = p + grp, bb = min(b, nb - 1);
+            // this lane's 16 values, as float4s; y written from here too
+            const int k4 = (bb * QK + 16 * li) >> 2;
             float v[16];
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const int k = bb * QK + 16 * li + i;
-                v[i] = (row[k] * scale) * (1.0f + (w ? w[k] : 0.0f));
+            for (int i = 0; i < 4; ++i) {
+                const float4 r = rowv[k4 + i];
+                const float4 g = w ? reinterpret_cast<const float4*>(w)[k4 + i] : make_float4(0.f, 0.f, 0.f, 0.f);
+                v[4 * i] = (r.x * scale) * (1.0f + g.x);
+                v[4 * i + 1] = (r.y * scale) * (1.0f + g.y);
+                v[4 * i + 2] = (r.z * scale) * (1.0f + g.z);
+                v[4 * i + 3] = (r.w * scale) * (1.0f + g.w);
+            }
+            if (y && b < nb) {
+                float4* y4 = reinterpret_cast<float4*>(y + (size_t)t * dim) + k4;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) y4[i] = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
             }
             q8k_from16(v, lane, b < nb ? q8 + ((size_t)t * nb + b) * Q8K_WORDS : nullptr);
         }
