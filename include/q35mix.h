@@ -95,6 +95,30 @@ int q35m_reset(q35m_ctx* ctx, int seq);
 int q35m_truncate(q35m_ctx* ctx, int seq, int length);
 /* `_cacheLen += seq` at the end of Qwen35Model.Forward (Qwen35Model.cs:287). */
 int q35m_advance(q35m_ctx* ctx, int seq, int n);
+/* KV growth: Qwen35Model.EnsureCache (Qwen35Model.cs:293-353) grows the
+ * caches by doubling when a forward pass would pass the capacity; here the
+ * caller grows the context to kv_capacity rows (every sequence, every GQA
+ * layer; the rows held and the lengths are kept, the RoPE table is extended).
+ * Synchronises the stream; a smaller capacity is Q35M_ERR_RANGE. */
+int q35m_grow(q35m_ctx* ctx, int kv_capacity);
+/* Linear-state snapshot, so a truncation can roll the recurrent state back
+ * too (the reference cannot: TruncateCache moves the KV length only,
+ * Qwen35Model.cs:214-222).  save copies sequence seq's DeltaNet state and
+ * conv window of every linear layer into a device buffer of
+ * q35m_snapshot_bytes() bytes and fills info (length, epoch); restore copies
+ * them back and sets the length to info->kv_len.  K/V rows are not copied:
+ * restore needs the rows below that length unchanged since the save, and
+ * refuses (Q35M_ERR_RANGE) after a reset, a truncate below the current length
+ * or a K/V state write of that sequence, and when the sequence is shorter than
+ * the snapshot.  Copies are asynchronous on the context stream. */
+typedef struct q35m_snapshot_info {
+    int kv_len;
+    unsigned int epoch;
+} q35m_snapshot_info;
+size_t q35m_snapshot_bytes(const q35m_ctx* ctx);
+int q35m_snapshot_save(q35m_ctx* ctx, int seq, void* dev, size_t bytes, q35m_snapshot_info* info);
+int q35m_snapshot_restore(q35m_ctx* ctx, int seq, const void* dev, size_t bytes,
+                          const q35m_snapshot_info* info);
 int q35m_kv_len(const q35m_ctx* ctx, int seq, int* length);
 
 /* ---- weights (host -> HBM once; Qwen35Model.LoadWeights F32 tensors,

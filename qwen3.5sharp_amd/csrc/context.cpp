@@ -269,6 +269,7 @@ int q35m_create(const q35m_config* cfg, int n_seqs, int kv_capacity, q35m_ctx** 
         c->is_recurrent[l] = cfg->is_recurrent ? (cfg->is_recurrent[l] != 0)
                                                : ((l + 1) % cfg->full_attention_interval != 0);
     c->kv_len.assign(n_seqs, 0);
+    c->epoch.assign(n_seqs, 0u);
 
     int r = Q35M_OK;
     hipError_t e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
@@ -349,6 +350,7 @@ int q35m_reset(q35m_ctx* ctx, int seq) {
                 "reset");
     }
     ctx->kv_len[seq] = 0;
+    ctx->epoch[seq]++;
     return Q35M_OK;
 }
 
@@ -359,6 +361,7 @@ int q35m_truncate(q35m_ctx* ctx, int seq, int length) {
     if (length < 0) return fail(Q35M_ERR_INVALID, "negative length %d", length);
     if (length > ctx->kv_len[seq])
         return fail(Q35M_ERR_RANGE, "cannot extend cache from %d to %d", ctx->kv_len[seq], length);
+    if (length < ctx->kv_len[seq]) ctx->epoch[seq]++;
     ctx->kv_len[seq] = length;
     return Q35M_OK;
 }
@@ -524,6 +527,139 @@ int q35m_quantize_q8k(q35m_ctx* ctx, const float* x, void* q8, int n_in, int tok
     return Q35M_OK;
 }
 
+static void free_alloc(q35m_ctx* c, void* p) {
+    for (size_t i = 0; i < c->allocations.size(); i++)
+        if (c->allocations[i] == p) {
+            c->allocations.erase(c->allocations.begin() + (long)i);
+            break;
+        }
+    (void)hipFree(p);
+}
+
+int q35m_grow(q35m_ctx* ctx, int kv_capacity) {
+    int r = check_ctx(ctx);
+    if (r) return r;
+    if (kv_capacity < ctx->cap)
+        return fail(Q35M_ERR_RANGE, "cannot shrink the KV capacity from %d to %d", ctx->cap, kv_capacity);
+    if (kv_capacity == ctx->cap) return Q35M_OK;
+    const q35::Dims& d = ctx->d;
+    HIP_TRY(hipStreamSynchronize(ctx->stream), "grow");
+    // New caches first; the context keeps the old ones until every copy is done.
+    std::vector<float*> fresh;
+    const size_t row = (size_t)q35::kHd * sizeof(float);
+    const size_t kv_bytes = (size_t)ctx->n_seqs * kv_capacity * d.kv_dim * sizeof(float);
+    hipError_t e = hipSuccess;
+    for (int l = 0; l < ctx->cfg.num_layers && !r && e == hipSuccess; l++) {
+        if (ctx->is_recurrent[l]) continue;
+        for (float* old : {ctx->full[l].k_cache, ctx->full[l].v_cache}) {
+            float* p = nullptr;
+            if ((r = alloc_zero(ctx, (void**)&p, kv_bytes))) break;
+            fresh.push_back(p);
+            // [seq][kv_head] blocks of [capacity][head_dim]: one strided copy
+            e = hipMemcpy2DAsync(p, row * kv_capacity, old, row * ctx->cap, row * ctx->cap,
+                                 (size_t)ctx->n_seqs * d.nkv, hipMemcpyDeviceToDevice, ctx->stream);
+            if (e != hipSuccess) break;
+        }
+    }
+    float *rc = nullptr, *rs = nullptr;
+    if (!r && e == hipSuccess && kv_capacity > ctx->rope_cap) {
+        std::vector<float> cs, sn;
+        build_rope_table(kv_capacity, q35::kRopeHalf, ctx->cfg.rope_base, cs, sn);
+        const size_t tb = cs.size() * sizeof(float);
+        r = alloc_zero(ctx, (void**)&rc, tb);
+        if (!r) r = alloc_zero(ctx, (void**)&rs, tb);
+        if (!r) e = hipMemcpyAsync(rc, cs.data(), tb, hipMemcpyHostToDevice, ctx->stream);
+        if (!r && e == hipSuccess) e = hipMemcpyAsync(rs, sn.data(), tb, hipMemcpyHostToDevice, ctx->stream);
+    }
+    hipError_t es = hipStreamSynchronize(ctx->stream);
+    if (e == hipSuccess) e = es;
+    if (r || e != hipSuccess) {
+        for (float* p : fresh) free_alloc(ctx, p);
+        if (rc) free_alloc(ctx, rc);
+        if (rs) free_alloc(ctx, rs);
+        return r ? r : hip_fail(e, "grow");
+    }
+    size_t k = 0;
+    for (int l = 0; l < ctx->cfg.num_layers; l++) {
+        if (ctx->is_recurrent[l]) continue;
+        free_alloc(ctx, ctx->full[l].k_cache);
+        free_alloc(ctx, ctx->full[l].v_cache);
+        ctx->full[l].k_cache = fresh[k++];
+        ctx->full[l].v_cache = fresh[k++];
+    }
+    if (rc) {
+        free_alloc(ctx, ctx->rope_cos);
+        free_alloc(ctx, ctx->rope_sin);
+        ctx->rope_cos = rc;
+        ctx->rope_sin = rs;
+        ctx->rope_cap = kv_capacity;
+    }
+    ctx->cap = kv_capacity;
+    return Q35M_OK;
+}
+
+size_t q35m_snapshot_bytes(const q35m_ctx* ctx) {
+    if (!ctx) return 0;
+    const q35::Dims& d = ctx->d;
+    const size_t per = ((size_t)d.nv * q35::kDk * q35::kDk + (size_t)d.conv_dim * q35::kConvState) * sizeof(float);
+    size_t n = 0;
+    for (int l = 0; l < ctx->cfg.num_layers; l++) n += ctx->is_recurrent[l] ? 1 : 0;
+    return n * per;
+}
+
+// One sequence's recurrent state and current conv window of every DeltaNet
+// layer, in layer order, to or from a device buffer (asynchronous copies on
+// the context stream).
+static int snapshot_copy(q35m_ctx* ctx, int seq, char* dev, bool save) {
+    const q35::Dims& d = ctx->d;
+    const size_t sb = (size_t)d.nv * q35::kDk * q35::kDk * sizeof(float);
+    const size_t cb = (size_t)d.conv_dim * q35::kConvState * sizeof(float);
+    for (int l = 0; l < ctx->cfg.num_layers; l++) {
+        if (!ctx->is_recurrent[l]) continue;
+        char* st = (char*)ctx->lin[l].state + sb * seq;
+        char* cw = (char*)ctx->lin[l].conv_window(seq, ctx->n_seqs, d.conv_dim);
+        HIP_TRY(hipMemcpyAsync(save ? dev : st, save ? st : dev, sb, hipMemcpyDeviceToDevice, ctx->stream),
+                "snapshot");
+        dev += sb;
+        HIP_TRY(hipMemcpyAsync(save ? dev : cw, save ? cw : dev, cb, hipMemcpyDeviceToDevice, ctx->stream),
+                "snapshot");
+        dev += cb;
+    }
+    return Q35M_OK;
+}
+
+static int snapshot_check(q35m_ctx* ctx, int seq, const void* dev, size_t bytes, const void* info) {
+    int r = check_ctx(ctx);
+    if (!r) r = check_seq(ctx, seq);
+    if (r) return r;
+    const size_t need = q35m_snapshot_bytes(ctx);
+    if (!info || (!dev && need)) return fail(Q35M_ERR_INVALID, "null pointer");
+    if (bytes < need) return fail(Q35M_ERR_INVALID, "snapshot buffer of %zu bytes, %zu needed", bytes, need);
+    return Q35M_OK;
+}
+
+int q35m_snapshot_save(q35m_ctx* ctx, int seq, void* dev, size_t bytes, q35m_snapshot_info* info) {
+    int r = snapshot_check(ctx, seq, dev, bytes, info);
+    if (r) return r;
+    if ((r = snapshot_copy(ctx, seq, (char*)dev, true))) return r;
+    info->kv_len = ctx->kv_len[seq];
+    info->epoch = ctx->epoch[seq];
+    return Q35M_OK;
+}
+
+int q35m_snapshot_restore(q35m_ctx* ctx, int seq, const void* dev, size_t bytes,
+                          const q35m_snapshot_info* info) {
+    int r = snapshot_check(ctx, seq, dev, bytes, info);
+    if (r) return r;
+    if (info->epoch != ctx->epoch[seq] || info->kv_len > ctx->kv_len[seq])
+        return fail(Q35M_ERR_RANGE,
+                    "snapshot at length %d no longer matches sequence %d at length %d (reset, truncate "
+                    "or K/V write since the save)", info->kv_len, seq, ctx->kv_len[seq]);
+    if ((r = snapshot_copy(ctx, seq, const_cast<char*>((const char*)dev), false))) return r;
+    ctx->kv_len[seq] = info->kv_len;
+    return Q35M_OK;
+}
+
 int q35m_add_rmsnorm(q35m_ctx* ctx, float* hidden, const float* delta, const float* weight, float* y, void* q8,
                      int dim, int tokens, float eps) {
     int r = check_ctx(ctx);
@@ -647,6 +783,7 @@ int q35m_state_write(q35m_ctx* ctx, int layer, int seq, int kind, const void* ho
     int r = state_locate(ctx, layer, seq, kind, &base, &cap_bytes);
     if (r) return r;
     if (!host) return fail(Q35M_ERR_INVALID, "null host buffer");
+    if (is_kv(kind)) ctx->epoch[seq]++;
     if (bytes > cap_bytes)
         return fail(Q35M_ERR_INVALID, "write of %zu bytes exceeds the %zu-byte state", bytes,
                     cap_bytes);

@@ -98,6 +98,7 @@ struct q35m_ctx {
     std::vector<q35::DeltaNetLayer> lin;   // indexed by layer (empty for GQA layers)
     std::vector<q35::AttnLayer> full;      // indexed by layer (empty for DeltaNet layers)
     std::vector<int> kv_len;           // per seq
+    std::vector<unsigned> epoch;       // per seq: bumped when cached K/V rows may change below the length
     float* rope_cos = nullptr;         // [rope_cap][32]
     float* rope_sin = nullptr;
     int rope_cap = 0;

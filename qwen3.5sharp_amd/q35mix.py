@@ -67,6 +67,12 @@ def lib() -> ctypes.CDLL:
             getattr(_lib, name).argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                                             ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
                                             ctypes.c_int]
+        _lib.q35m_grow.argtypes = [ctypes.c_void_p, ctypes.c_int]
+        _lib.q35m_snapshot_bytes.restype = ctypes.c_size_t
+        _lib.q35m_snapshot_bytes.argtypes = [ctypes.c_void_p]
+        for name in ("q35m_snapshot_save", "q35m_snapshot_restore"):
+            getattr(_lib, name).argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t,
+                                            ctypes.POINTER(SnapshotInfo)]
         _lib.q35m_add_rmsnorm.argtypes = [ctypes.c_void_p] * 6 + [ctypes.c_int, ctypes.c_int, ctypes.c_float]
         _lib.q35m_add_rmsnorm.restype = ctypes.c_int
         _lib.q35m_quantize_q8k.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
@@ -139,6 +145,11 @@ class DeviceArray:
         if self.ptr:
             lib().q35m_free(self.ptr)
             self.ptr = None
+
+
+class SnapshotInfo(ctypes.Structure):
+    """q35m_snapshot_info: the length and epoch a snapshot was taken at."""
+    _fields_ = [("kv_len", ctypes.c_int), ("epoch", ctypes.c_uint)]
 
 
 class DeviceBytes(DeviceArray):
@@ -263,6 +274,22 @@ class Context:
         check(lib().q35m_quantize_q8k(ctypes.c_void_p(self.handle), ctypes.c_void_p(x.ptr),
                                       ctypes.c_void_p(q8.ptr), n_in, tokens))
         return q8
+
+    def grow(self, kv_capacity: int) -> None:
+        check(lib().q35m_grow(ctypes.c_void_p(self.handle), kv_capacity))
+
+    def snapshot_save(self, seq: int):
+        """(device buffer, SnapshotInfo) of seq's linear state."""
+        n = lib().q35m_snapshot_bytes(ctypes.c_void_p(self.handle))
+        buf = DeviceBytes(self, np.zeros(max(n, 1), np.uint8))
+        info = SnapshotInfo()
+        check(lib().q35m_snapshot_save(ctypes.c_void_p(self.handle), seq, ctypes.c_void_p(buf.ptr), n,
+                                       ctypes.byref(info)))
+        return buf, info
+
+    def snapshot_restore(self, seq: int, buf, info) -> None:
+        check(lib().q35m_snapshot_restore(ctypes.c_void_p(self.handle), seq, ctypes.c_void_p(buf.ptr),
+                                          buf.nbytes, ctypes.byref(info)))
 
     def add_rmsnorm(self, hidden, delta, w, y, q8, dim, tokens, eps=1e-6) -> None:
         """hidden += delta (delta may be None), y = RmsNormZeroCentered(hidden, w)

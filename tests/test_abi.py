@@ -76,6 +76,11 @@ def test_null_context_is_rejected():
     assert L.q35m_linear_q4k_prequant(None, None, None, None, 256, 1, 1) == q35mix.ERR_INVALID
     assert L.q35m_q8k_bytes(2560, 3) == 3 * 10 * 304
     assert L.q35m_add_rmsnorm(None, None, None, None, None, None, 2560, 1, 1e-6) == q35mix.ERR_INVALID
+    assert L.q35m_grow(None, 64) == q35mix.ERR_INVALID
+    assert L.q35m_snapshot_bytes(None) == 0
+    info = q35mix.SnapshotInfo()
+    assert L.q35m_snapshot_save(None, 0, None, 0, ctypes.byref(info)) == q35mix.ERR_INVALID
+    assert L.q35m_snapshot_restore(None, 0, None, 0, ctypes.byref(info)) == q35mix.ERR_INVALID
 
 
 def test_no_device_here_is_an_error_not_a_fallback():
