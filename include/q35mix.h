@@ -30,6 +30,7 @@
 #define Q35MIX_H
 
 #include <stddef.h>
+#include <stdint.h>
 
 #ifdef __cplusplus
 extern "C" {
@@ -168,6 +169,37 @@ int q35m_attn_decode(q35m_ctx* ctx, int layer, int n, const int* seqs, const flo
  * out [T][heads*head_dim].  Does not advance the length. */
 int q35m_attn_prefill(q35m_ctx* ctx, int layer, int seq, int T, const float* q_gate,
                       const float* k, const float* v, float* out);
+
+/* ---- GGUF weights (GgufFile, src/Qwen35Sharp.Gguf/GgufFile.cs:27-170) ---- */
+
+/* Opens (memory-maps, read-only) and parses a GGUF v2/v3 file: metadata,
+ * tensor infos, the data section at general.alignment (default 32, a power of
+ * two), as GgufFile does.  Bad magic or layout: Q35M_ERR_INVALID; another
+ * version: Q35M_ERR_UNSUPPORTED.  Needs no device. */
+typedef struct q35m_gguf q35m_gguf;
+int q35m_gguf_open(const char* path, q35m_gguf** out);
+int q35m_gguf_close(q35m_gguf* g);
+/* A tensor's ggml type, dims (GGUF order, innermost first; unused dims 1),
+ * host pointer into the mapping and byte size (0 for a type this reader does
+ * not size; F32, F16, Q8_0, Q4_K, Q5_K, Q6_K, Q8_K and IQ4_XS are sized).
+ * Unknown name: Q35M_ERR_RANGE.  Any pointer but g and name may be NULL. */
+int q35m_gguf_tensor(const q35m_gguf* g, const char* name, int* type, int64_t dims[4], int* n_dims,
+                     const void** data, size_t* bytes);
+/* Metadata values (GgufFile.GetInt32/GetUint32, GetFloat32, GetString);
+ * strings stay valid until q35m_gguf_close.  Missing key: Q35M_ERR_RANGE. */
+int q35m_gguf_int(const q35m_gguf* g, const char* key, int64_t* value);
+int q35m_gguf_float(const q35m_gguf* g, const char* key, double* value);
+int q35m_gguf_string(const q35m_gguf* g, const char* key, const char** value);
+/* The F32 branch of Qwen35Model.LoadWeights (Qwen35Model.cs:463-474) for the
+ * token mixers: per layer, blk.N.ssm_conv1d.weight [4][conv_dim],
+ * blk.N.ssm_a, blk.N.ssm_dt.bias [n_v_heads], blk.N.ssm_norm.weight
+ * [v_head_dim] (linear layers) or blk.N.attn_q_norm.weight,
+ * blk.N.attn_k_norm.weight [head_dim] (GQA layers), uploaded with
+ * q35m_set_deltanet_weights / q35m_set_attn_weights.  A missing tensor is
+ * Q35M_ERR_RANGE, a non-F32 one Q35M_ERR_UNSUPPORTED, a wrong size
+ * Q35M_ERR_INVALID. */
+int q35m_load_mixer_weights(q35m_ctx* ctx, const q35m_gguf* g, int num_layers, const unsigned char* is_recurrent,
+                            int conv_dim, int n_v_heads, int v_head_dim, int head_dim);
 
 /* ---- state I/O in the reference layouts (snapshot / restore / parity) -- */
 

@@ -127,6 +127,10 @@ int build_seq_batch(const q35m_ctx* c, int n, const int* seqs, bool with_pos, q3
 
 }  // namespace
 
+// Sets the thread's last error from another translation unit.
+int q35_set_error(int code, const char* msg) { return fail(code, "%s", msg); }
+
+
 namespace q35 {
 
 const char* kernel_name(int id) {

@@ -68,6 +68,16 @@ def lib() -> ctypes.CDLL:
                                             ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
                                             ctypes.c_int]
         _lib.q35m_grow.argtypes = [ctypes.c_void_p, ctypes.c_int]
+        _lib.q35m_gguf_open.argtypes = [ctypes.c_char_p, ctypes.POINTER(ctypes.c_void_p)]
+        _lib.q35m_gguf_close.argtypes = [ctypes.c_void_p]
+        _lib.q35m_gguf_tensor.argtypes = [ctypes.c_void_p, ctypes.c_char_p, ctypes.POINTER(ctypes.c_int),
+                                          ctypes.POINTER(ctypes.c_int64), ctypes.POINTER(ctypes.c_int),
+                                          ctypes.POINTER(ctypes.c_void_p), ctypes.POINTER(ctypes.c_size_t)]
+        _lib.q35m_gguf_int.argtypes = [ctypes.c_void_p, ctypes.c_char_p, ctypes.POINTER(ctypes.c_int64)]
+        _lib.q35m_gguf_float.argtypes = [ctypes.c_void_p, ctypes.c_char_p, ctypes.POINTER(ctypes.c_double)]
+        _lib.q35m_gguf_string.argtypes = [ctypes.c_void_p, ctypes.c_char_p, ctypes.POINTER(ctypes.c_char_p)]
+        _lib.q35m_load_mixer_weights.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_char_p,
+                                                 ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int]
         _lib.q35m_snapshot_bytes.restype = ctypes.c_size_t
         _lib.q35m_snapshot_bytes.argtypes = [ctypes.c_void_p]
         for name in ("q35m_snapshot_save", "q35m_snapshot_restore"):
@@ -145,6 +155,45 @@ class DeviceArray:
         if self.ptr:
             lib().q35m_free(self.ptr)
             self.ptr = None
+
+
+class Gguf:
+    """A GGUF file opened by the library (q35m_gguf_open); tensors are views
+    of the read-only mapping."""
+
+    def __init__(self, path: str):
+        h = ctypes.c_void_p()
+        check(lib().q35m_gguf_open(str(path).encode(), ctypes.byref(h)))
+        self.handle = h.value
+
+    def close(self) -> None:
+        if self.handle:
+            check(lib().q35m_gguf_close(ctypes.c_void_p(self.handle)))
+            self.handle = None
+
+    def tensor(self, name: str):
+        """(ggml type, dims innermost first, raw bytes)."""
+        t, nd, p, nb = ctypes.c_int(), ctypes.c_int(), ctypes.c_void_p(), ctypes.c_size_t()
+        dims = (ctypes.c_int64 * 4)()
+        check(lib().q35m_gguf_tensor(ctypes.c_void_p(self.handle), name.encode(), ctypes.byref(t), dims,
+                                     ctypes.byref(nd), ctypes.byref(p), ctypes.byref(nb)))
+        raw = ctypes.string_at(p.value, nb.value) if nb.value else b""
+        return t.value, tuple(dims[:nd.value]), raw
+
+    def int(self, key: str) -> int:
+        v = ctypes.c_int64()
+        check(lib().q35m_gguf_int(ctypes.c_void_p(self.handle), key.encode(), ctypes.byref(v)))
+        return v.value
+
+    def float(self, key: str) -> float:
+        v = ctypes.c_double()
+        check(lib().q35m_gguf_float(ctypes.c_void_p(self.handle), key.encode(), ctypes.byref(v)))
+        return v.value
+
+    def string(self, key: str) -> str:
+        v = ctypes.c_char_p()
+        check(lib().q35m_gguf_string(ctypes.c_void_p(self.handle), key.encode(), ctypes.byref(v)))
+        return v.value.decode()
 
 
 class SnapshotInfo(ctypes.Structure):
@@ -274,6 +323,17 @@ class Context:
         check(lib().q35m_quantize_q8k(ctypes.c_void_p(self.handle), ctypes.c_void_p(x.ptr),
                                       ctypes.c_void_p(q8.ptr), n_in, tokens))
         return q8
+
+    def load_mixer_weights(self, gguf: "Gguf") -> None:
+        """The mixers' F32 tensors of every layer from a GGUF file."""
+        c = self.cfg
+        if c.is_recurrent:
+            rec = bytes(int(bool(c.is_recurrent[i])) for i in range(c.num_layers))
+        else:
+            rec = bytes(int((i + 1) % c.full_attention_interval != 0) for i in range(c.num_layers))
+        check(lib().q35m_load_mixer_weights(ctypes.c_void_p(self.handle), ctypes.c_void_p(gguf.handle),
+                                            c.num_layers, rec, self.conv_dim, c.ssm_time_step_rank,
+                                            c.ssm_state_size, c.head_dim))
 
     def grow(self, kv_capacity: int) -> None:
         check(lib().q35m_grow(ctypes.c_void_p(self.handle), kv_capacity))

@@ -77,6 +77,8 @@ def test_null_context_is_rejected():
     assert L.q35m_q8k_bytes(2560, 3) == 3 * 10 * 304
     assert L.q35m_add_rmsnorm(None, None, None, None, None, None, 2560, 1, 1e-6) == q35mix.ERR_INVALID
     assert L.q35m_grow(None, 64) == q35mix.ERR_INVALID
+    assert L.q35m_load_mixer_weights(None, None, 1, b"\x01", 1, 1, 1, 1) == q35mix.ERR_INVALID
+    assert L.q35m_gguf_close(None) == q35mix.ERR_INVALID
     assert L.q35m_snapshot_bytes(None) == 0
     info = q35mix.SnapshotInfo()
     assert L.q35m_snapshot_save(None, 0, None, 0, ctypes.byref(info)) == q35mix.ERR_INVALID

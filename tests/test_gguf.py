@@ -1,0 +1,56 @@
+"""The GGUF reader (q35m_gguf_*) on files written to the published layout by
+tests/gguf_writer.py: metadata of every scalar type, arrays skipped, tensor
+infos and data at the default (32) and a custom alignment, and the errors
+GgufFile raises (GgufFile.cs:110-170: magic, version 2-3, non-power-of-two
+alignment, a data section past the end).  Runs without a device."""
+import numpy as np
+import pytest
+
+import gguf_writer as gw
+import q35mix
+
+
+def test_metadata_and_tensors(tmp_path):
+    p = tmp_path / "a.gguf"
+    w = np.arange(24, dtype=np.float32).reshape(4, 6)
+    q = np.arange(144 * 2, dtype=np.uint8)
+    kv = [("general.architecture", gw.STRING, "qwen35"), ("qwen35.block_count", gw.U32, 2),
+          ("x.i8", gw.I8, -5), ("x.u64", gw.U64, 1 << 40), ("x.f32", gw.F32, 0.5), ("x.f64", gw.F64, -2.25),
+          ("x.bool", gw.BOOL, 1), ("x.arr", gw.ARRAY, (gw.I32, [1, 2, 3])),
+          ("x.strs", gw.ARRAY, (gw.STRING, ["a", "bc"]))]
+    for align in (None, 64):
+        gw.write(p, kv, [gw.f32("blk.0.ssm_a", w), ("blk.0.q", 12, (512,), q.tobytes())], alignment=align)
+        g = q35mix.Gguf(p)
+        assert g.string("general.architecture") == "qwen35"
+        assert g.int("qwen35.block_count") == 2 and g.int("x.i8") == -5 and g.int("x.u64") == 1 << 40
+        assert g.int("x.bool") == 1
+        assert g.float("x.f32") == 0.5 and g.float("x.f64") == -2.25
+        t, dims, raw = g.tensor("blk.0.ssm_a")
+        assert t == 0 and dims == (6, 4) and np.array_equal(np.frombuffer(raw, np.float32).reshape(4, 6), w)
+        t, dims, raw = g.tensor("blk.0.q")
+        assert t == 12 and dims == (512,) and raw == q.tobytes()
+        with pytest.raises(q35mix.Q35Error) as e:
+            g.tensor("nope")
+        assert e.value.code == q35mix.ERR_RANGE
+        with pytest.raises(q35mix.Q35Error):
+            g.int("x.f32")
+        g.close()
+
+
+@pytest.mark.parametrize("case,code", [("magic", "INVALID"), ("version", "UNSUPPORTED"),
+                                       ("align", "INVALID"), ("short", "INVALID")])
+def test_rejects_bad_files(tmp_path, case, code):
+    p = tmp_path / "b.gguf"
+    t = [gw.f32("t", np.ones(8, np.float32))]
+    if case == "magic":
+        gw.write(p, [], t, magic=b"GGUX")
+    elif case == "version":
+        gw.write(p, [], t, version=4)
+    elif case == "align":
+        gw.write(p, [], t, alignment=48)
+    else:
+        gw.write(p, [("k", gw.STRING, "v" * 100)], t)
+        p.write_bytes(p.read_bytes()[:60])
+    with pytest.raises(q35mix.Q35Error) as e:
+        q35mix.Gguf(p)
+    assert e.value.code == getattr(q35mix, "ERR_" + code)
