@@ -159,8 +159,12 @@ static int parse(q35m_gguf* g) {
     }
     uint64_t alignment = kDefaultAlignment;
     auto a = g->kv.find("general.alignment");
-    if (a != g->kv.end() && a->second.type >= U8 && a->second.type != F32 && a->second.type != STRING)
+    if (a != g->kv.end()) {
+        const int t = a->second.type;
+        if (t == F32 || t == F64 || t == STRING || t == ARRAY || t == BOOL || a->second.i < 0)
+            return fail(Q35M_ERR_INVALID, "GGUF general.alignment is not an unsigned integer");
         alignment = (uint64_t)a->second.i;
+    }
     if (alignment == 0 || (alignment & (alignment - 1)))
         return fail(Q35M_ERR_INVALID, "GGUF alignment %llu is not a power of two", (unsigned long long)alignment);
     for (uint64_t i = 0; i < n_tensors; i++) {

@@ -38,7 +38,7 @@ def test_metadata_and_tensors(tmp_path):
 
 
 @pytest.mark.parametrize("case,code", [("magic", "INVALID"), ("version", "UNSUPPORTED"),
-                                       ("align", "INVALID"), ("short", "INVALID")])
+                                       ("align", "INVALID"), ("short", "INVALID"), ("falign", "INVALID")])
 def test_rejects_bad_files(tmp_path, case, code):
     p = tmp_path / "b.gguf"
     t = [gw.f32("t", np.ones(8, np.float32))]
@@ -48,6 +48,8 @@ def test_rejects_bad_files(tmp_path, case, code):
         gw.write(p, [], t, version=4)
     elif case == "align":
         gw.write(p, [], t, alignment=48)
+    elif case == "falign":
+        gw.write(p, [("general.alignment", gw.F64, 32.0)], t)
     else:
         gw.write(p, [("k", gw.STRING, "v" * 100)], t)
         p.write_bytes(p.read_bytes()[:60])
