@@ -788,6 +788,17 @@ __global__ __launch_bounds__(kWave) void add_rmsnorm(float* hidden, const float*
         rowv[i] = v;
     }
     __syncthreads();
+    // Q8: the first pass's weights are loaded before the sum of squares, each
+    // later pass's during the one before.
+    const int grp = lane >> 4, li = lane & 15, nbq = Q8 ? dim / QK : 0;
+    float4 wn[4];
+    auto load_w = [&](int p) {
+        const int k4 = (min(p + grp, nbq - 1) * QK + 16 * li) >> 2;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            wn[i] = w ? reinterpret_cast<const float4*>(w)[k4 + i] : make_float4(0.f, 0.f, 0.f, 0.f);
+    };
+    if constexpr (Q8) load_w(0);
     float acc = 0.0f;
     // unrolled so the LDS reads run ahead of the (strictly ordered) FMA chain
     if (lane < 8)
@@ -815,16 +826,20 @@ __global__ __launch_bounds__(kWave) void add_rmsnorm(float* hidden, const float*
         }
     }
     if constexpr (Q8) {
-        const int nb = dim / QK, grp = lane >> 4, li = lane & 15;
+        const int nb = nbq;
         for (int p = 0; p < nb; p += 4) {
             const int b = p + grp, bb = min(b, nb - 1);
             // this lane's 16 values, as float4s; y written from here too
             const int k4 = (bb * QK + 16 * li) >> 2;
+            float4 wc[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) wc[i] = wn[i];
+            if (p + 4 < nb) load_w(p + 4);
             float v[16];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const float4 r = rowv[k4 + i];
-                const float4 g = w ? reinterpret_cast<const float4*>(w)[k4 + i] : make_float4(0.f, 0.f, 0.f, 0.f);
+                const float4 g = wc[i];
                 v[4 * i] = (r.x * scale) * (1.0f + g.x);
                 v[4 * i + 1] = (r.y * scale) * (1.0f + g.y);
                 v[4 * i + 2] = (r.z * scale) * (1.0f + g.z);
