@@ -9,7 +9,12 @@
  * state [H_v][dk][dv] and conv state [conv_dim][K-1] of every linear layer,
  * and the K/V cache of every full-attention layer (the reference's
  * [capacity][kv_heads*head_dim] rows, held head-major on the device), per
- * sequence.  Paths in citations are relative to the reference repository
+ * sequence.  Around the mixers it also offers what the reference runs on
+ * either side of them: the quantized projections (Q4_K / Q6_K weights,
+ * activations quantized to Q8_K), the layer boundary (residual add +
+ * zero-centred RMSNorm, optionally emitting Q8_K), KV growth and a
+ * linear-state snapshot, and a GGUF reader that uploads the mixers' F32
+ * weights.  Paths in citations are relative to the reference repository
  * root.
  *
  * Conventions
