@@ -94,3 +94,22 @@ def test_grow_keeps_rows_and_lengths():
         assert bits_equal(a.state_read(1, s, q35mix.STATE_KEYS, 40), b.state_read(1, s, q35mix.STATE_KEYS, 40))
     a.close()
     b.close()
+
+
+def test_grow_extends_rope_table():
+    """Growing past the 4096 positions the RoPE table starts with rebuilds it:
+    a decode at position 4100 matches a context created with 8192 rows."""
+    say("grow 4096 -> 8192 (RoPE table rebuilt)")
+    a, b = make_ctx(4096, n_seqs=1), make_ctx(8192, n_seqs=1)
+    a.grow(8192)
+    k, v = synth.kv_prefill(4100, a.kv_dim, salt=91)
+    for c in (a, b):
+        c.state_write(1, 0, q35mix.STATE_KEYS, k)
+        c.state_write(1, 0, q35mix.STATE_VALUES, v)
+        c.advance(0, 4100)
+    xd = synth.deltanet_inputs(2, NK, NV, 128, salt=92)
+    xa = synth.attn_inputs(2, NH, NKV, HD, salt=93)
+    for i in range(2):
+        assert all(bits_equal(u, w) for u, w in zip(step(a, 0, xd, xa, i), step(b, 0, xd, xa, i)))
+    a.close()
+    b.close()
