@@ -95,6 +95,22 @@ def time_calls(ctx, fn, steps, warmup):
     return ms / steps
 
 
+def time_calls_median(ctx, fn, steps, warmup):
+    """Per-call times from one event between consecutive calls (calls stay
+    back to back on the stream): (median ms, mean ms)."""
+    for i in range(warmup):
+        fn(i)
+    ctx.sync()
+    ev = [q35mix.Event() for _ in range(steps + 1)]
+    ev[0].record(ctx.stream)
+    for i in range(steps):
+        fn(warmup + i)
+        ev[i + 1].record(ctx.stream)
+    ev[-1].synchronize()
+    per = [ev[i].elapsed_ms(ev[i + 1]) for i in range(steps)]
+    return float(np.median(per)), float(np.mean(per))
+
+
 def kernel_times(ctx, fn, steps):
     ctx.profile(True)
     for i in range(steps):
@@ -145,7 +161,7 @@ def bench_dn_decode(steps, warmup, n_layers=160):
     def step(i):
         ctx.deltanet_decode(i % n_layers, [0], qkv, z, b, a, out)
 
-    ms = time_calls(ctx, step, steps, warmup)
+    ms = time_calls_median(ctx, step, steps, warmup)
     kt = kernel_times(ctx, step, steps)
     ctx.close()
     return ms, kt
@@ -170,7 +186,7 @@ def bench_attn_decode(steps, warmup, n_layers=8, pos=8192):
     def step(i):
         ctx.attn_decode(i % n_layers, [0], qg, kk, vv, out)
 
-    ms = time_calls(ctx, step, steps, warmup)
+    ms = time_calls_median(ctx, step, steps, warmup)
     kt = kernel_times(ctx, step, steps)
     ctx.close()
     return ms, kt
@@ -313,9 +329,120 @@ def bench_stack(n_steps=128, warmup=4, n_seqs=8, ctx_len=32768, n_layers=32):
 # CPU restatement timed beside the GPU
 # --------------------------------------------------------------------------
 
-def cpu_baseline_prefill(x, T=2048):
+def _oracle():
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle
+    return oracle
+
+
+def cpu_threads():
+    """Worker threads for the CPU attention: the reference's pool default, one
+    per physical core (CpuThreadPool.cs:27-29), of the cores this process may
+    use, at most 16 (work is split by q head).  Returns (threads, logical
+    CPUs available, hardware threads per core)."""
+    avail = len(os.sched_getaffinity(0))
+    tpc = 1
+    try:
+        sib = cores = None
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("siblings") and sib is None:
+                sib = int(line.split(":")[1])
+            elif line.startswith("cpu cores") and cores is None:
+                cores = int(line.split(":")[1])
+        if sib and cores:
+            tpc = max(1, sib // cores)
+    except (OSError, ValueError):
+        pass
+    return max(1, min(16, avail // tpc)), avail, tpc
+
+
+def _median_s(fn, reps=20, warm=3):
+    for _ in range(warm):
+        fn()
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return float(np.median(ts))
+
+
+def cpu_baseline_dn_decode():
+    """One DeltaNet decode token through one layer on one thread (the
+    reference passes no pool to the recurrence, GatedDeltaNetOps.cs:107-120):
+    median of 20 after 3 warm-up runs, in microseconds."""
+    oracle = _oracle()
+    d = oracle.dims()
+    w = synth.deltanet_weights(NK, NV, DK)
+    st = synth.deltanet_state(NK, NV, DK)
+    x = synth.deltanet_inputs(1, NK, NV, DK)
+    sec = _median_s(lambda: oracle.deltanet_decode(d, x["qkv"][0], x["z"][0], x["b"][0], x["a"][0], w,
+                                                   st["conv_state"], st["state"]))
+    return sec * 1e6
+
+
+def cpu_baseline_attn_decode(threads, pos=8192):
+    """One GQA decode token at 8193 rows, scores/softmax/combine on `threads`
+    workers (Ops.cs:353-356): median of 20 after 3 warm-up runs, in us."""
+    oracle = _oracle()
+    d = oracle.dims()
+    k, v = synth.kv_prefill(pos, KV_DIM)
+    ck = np.zeros((pos + 1, KV_DIM), np.float32)
+    cv = np.zeros_like(ck)
+    ck[:pos], cv[:pos] = k, v
+    x = synth.attn_inputs(1, NH, NKV, HD)
+    wts = synth.attn_weights(HD)
+    sec = _median_s(lambda: oracle.attn_decode(d, pos, x["q_gate"][0], x["k"][0], x["v"][0], wts, ck, cv,
+                                               n_threads=threads, inplace=True))
+    return sec * 1e6
+
+
+def cpu_baseline_attn_prefill(threads, T=2048):
+    """One causal GQA prefill of 2048 tokens on `threads` workers, one run:
+    tokens/s and seconds."""
+    oracle = _oracle()
+    d = oracle.dims()
+    x = synth.attn_inputs(T, NH, NKV, HD)
+    wts = synth.attn_weights(HD)
+    z = np.zeros((T, KV_DIM), np.float32)
+    t0 = time.perf_counter()
+    oracle.attn_prefill(d, 0, T, x["q_gate"], x["k"], x["v"], wts, z, z, n_threads=threads)
+    dt = time.perf_counter() - t0
+    return T / dt, dt
+
+
+def cpu_baseline_stack(threads, n_steps=4, n_seqs=8, ctx_len=32768, n_layers=32, total_steps=128):
+    """The 32-layer mixer stack on the CPU restatement: n_steps decode steps of
+    8 sequences (24 DeltaNet layers on one thread, 8 GQA layers on `threads`
+    workers over caches of ~32K rows), extrapolated linearly to 128 steps.
+    One K/V cache pair is shared by every (layer, sequence): the CPU cost does
+    not depend on the values.  Returns (us per token, seconds measured)."""
+    oracle = _oracle()
+    d = oracle.dims()
+    start = ctx_len - total_steps
+    block = synth.normal(1234, 4 << 20)
+    ck = np.resize(block, (ctx_len, KV_DIM)).astype(np.float32)
+    cv = np.ascontiguousarray(ck[::-1])
+    wd, wa = synth.deltanet_weights(NK, NV, DK), synth.attn_weights(HD)
+    st = synth.deltanet_state(NK, NV, DK)
+    xd = synth.deltanet_inputs(n_seqs, NK, NV, DK, salt=500)
+    xa = synth.attn_inputs(n_seqs, NH, NKV, HD, salt=600)
+    t0 = time.perf_counter()
+    for step in range(n_steps):
+        for layer in range(n_layers):
+            for s in range(n_seqs):
+                if (layer + 1) % 4 != 0:
+                    oracle.deltanet_decode(d, xd["qkv"][s], xd["z"][s], xd["b"][s], xd["a"][s], wd,
+                                           st["conv_state"], st["state"])
+                else:
+                    oracle.attn_decode(d, start + step, xa["q_gate"][s], xa["k"][s], xa["v"][s], wa, ck, cv,
+                                       n_threads=threads, inplace=True)
+    dt = time.perf_counter() - t0
+    return dt / n_steps * total_steps / (total_steps * n_seqs) * 1e6, dt
+
+
+def cpu_baseline_prefill(x, T=2048):
+    oracle = _oracle()
     d = oracle.dims()
     w = synth.deltanet_weights(NK, NV, DK)
     st = np.zeros((NV, DK, DK), np.float32)
@@ -440,24 +567,41 @@ def main():
                   "roofline": roof, "cpu_baseline": cpu,
                   "prefill_dn_mflop_frac": DN_PREFILL_FLOP / (ms / 1e3) / FP32_PEAK}
 
+    threads, avail, tpc = cpu_threads()
+    model, _ = cpu_info()
+    cpu_desc = f"{model}, {avail} logical CPUs available, {tpc} threads per core"
+
     if want("dn_decode"):
         log("[bench] DeltaNet decode batch 1 ...")
-        ms, kt = bench_dn_decode(max(K, 100), max(W, 20))
+        (ms, mean_ms), kt = bench_dn_decode(max(K, 100), max(W, 20))
         kname, kms = dominant(kt)
         workloads["deltanet_decode_b1"] = {
-            "us_per_token": ms * 1e3, "hbm_frac_call": DN_DECODE_BYTES / (ms / 1e3) / HBM_PEAK,
+            "us_per_token": ms * 1e3, "us_per_token_mean": mean_ms * 1e3,
+            "hbm_frac_call": DN_DECODE_BYTES / (ms / 1e3) / HBM_PEAK,
             "kernel": kname, "kernel_us": kms * 1e3,
             "hbm_frac_kernel": DN_DECODE_BYTES / (kms / 1e3) / HBM_PEAK}
+        if not args.no_cpu:
+            us = cpu_baseline_dn_decode()
+            workloads["deltanet_decode_b1"]["cpu_baseline"] = {
+                "value": us, "unit": "us/token", "cores": 1, "kind": "port",
+                "sample": f"median of 20 single-token decodes of one layer, one thread as the reference "
+                          f"({cpu_desc})"}
         log(f"[bench] DeltaNet decode: {workloads['deltanet_decode_b1']}")
 
     if want("attn_decode"):
         log("[bench] GQA decode at 8193 rows ...")
-        ms, kt = bench_attn_decode(max(K, 100), max(W, 20))
+        (ms, mean_ms), kt = bench_attn_decode(max(K, 100), max(W, 20))
         by = attn_decode_bytes(8193)
-        kname, kms = dominant(kt)
         workloads["attn_decode_8193"] = {
-            "us_per_token": ms * 1e3, "hbm_frac_call": by / (ms / 1e3) / HBM_PEAK,
+            "us_per_token": ms * 1e3, "us_per_token_mean": mean_ms * 1e3,
+            "hbm_frac_call": by / (ms / 1e3) / HBM_PEAK,
             "kernels_us": {k: v[0] * 1e3 for k, v in kt.items()}}
+        if not args.no_cpu:
+            us = cpu_baseline_attn_decode(threads)
+            workloads["attn_decode_8193"]["cpu_baseline"] = {
+                "value": us, "unit": "us/token", "cores": threads, "kind": "port",
+                "sample": f"median of 20 single-token decodes at 8193 rows, attention on {threads} "
+                          f"workers, one per physical core as the reference's pool ({cpu_desc})"}
         log(f"[bench] GQA decode: {workloads['attn_decode_8193']}")
 
     if want("attn_prefill"):
@@ -467,6 +611,12 @@ def main():
             "tokens_per_s": 2048 / (ms / 1e3), "ms": ms,
             "mfma_frac": ATTN_PREFILL_FLOP / (ms / 1e3) / FP32_PEAK,
             "kernels_ms": {k: v[0] for k, v in kt.items()}}
+        if not args.no_cpu:
+            tok_s_cpu, sec = cpu_baseline_attn_prefill(threads)
+            workloads["attn_prefill_2048"]["cpu_baseline"] = {
+                "value": tok_s_cpu, "unit": "tokens/s", "cores": threads, "kind": "port",
+                "sample": f"one causal 2048-token prefill of one layer ({sec:.2f} s) on {threads} "
+                          f"workers ({cpu_desc})"}
         log(f"[bench] GQA prefill: {workloads['attn_prefill_2048']}")
 
     if want("linear_q"):
@@ -513,6 +663,14 @@ def main():
             "us_per_token": ms * 1e3 / (128 * 8), "ms_per_step": ms / 128,
             "hbm_frac": by / (ms / 1e3) / HBM_PEAK, "gb_per_step": by / 128 / 1e9,
             "kernels_us": {k: v[0] * 1e3 for k, v in kt.items()}}
+        if not args.no_cpu:
+            log("[bench] CPU restatement, 4 steps of the stack ...")
+            us, sec = cpu_baseline_stack(threads)
+            workloads["stack_decode_8x32k"]["cpu_baseline"] = {
+                "value": us, "unit": "us/token", "cores": threads, "kind": "port",
+                "sample": f"4 decode steps of the 32-layer stack x 8 sequences at ~32K rows ({sec:.1f} s), "
+                          f"extrapolated linearly to 128 steps; DeltaNet on one thread, attention on "
+                          f"{threads} workers ({cpu_desc})"}
         log(f"[bench] stack: {workloads['stack_decode_8x32k']}")
 
     if result is None:

@@ -114,9 +114,13 @@ int q35m_grow(q35m_ctx* ctx, int kv_capacity);
  * q35m_snapshot_bytes() bytes and fills info (length, epoch); restore copies
  * them back and sets the length to info->kv_len.  K/V rows are not copied:
  * restore needs the rows below that length unchanged since the save, and
- * refuses (Q35M_ERR_RANGE) after a reset, a truncate below the current length
- * or a K/V state write of that sequence, and when the sequence is shorter than
- * the snapshot.  Copies are asynchronous on the context stream. */
+ * refuses (Q35M_ERR_RANGE) after a reset, a truncate below the current length,
+ * a restore to a shorter length or a K/V state write of that sequence, and
+ * when the sequence is shorter than the snapshot.  A restore that shortens the
+ * sequence starts a new epoch (the rows above the restored length will be
+ * written again, so snapshots taken at a longer length must no longer be
+ * accepted) and writes it into *info, which keeps the snapshot just restored
+ * usable.  Copies are asynchronous on the context stream. */
 typedef struct q35m_snapshot_info {
     int kv_len;
     unsigned int epoch;
@@ -124,7 +128,7 @@ typedef struct q35m_snapshot_info {
 size_t q35m_snapshot_bytes(const q35m_ctx* ctx);
 int q35m_snapshot_save(q35m_ctx* ctx, int seq, void* dev, size_t bytes, q35m_snapshot_info* info);
 int q35m_snapshot_restore(q35m_ctx* ctx, int seq, const void* dev, size_t bytes,
-                          const q35m_snapshot_info* info);
+                          q35m_snapshot_info* info);
 int q35m_kv_len(const q35m_ctx* ctx, int seq, int* length);
 
 /* ---- weights (host -> HBM once; Qwen35Model.LoadWeights F32 tensors,
@@ -202,7 +206,8 @@ int q35m_gguf_string(const q35m_gguf* g, const char* key, const char** value);
  * blk.N.attn_k_norm.weight [head_dim] (GQA layers), uploaded with
  * q35m_set_deltanet_weights / q35m_set_attn_weights.  A missing tensor is
  * Q35M_ERR_RANGE, a non-F32 one Q35M_ERR_UNSUPPORTED, a wrong size
- * Q35M_ERR_INVALID. */
+ * Q35M_ERR_INVALID.  num_layers, is_recurrent and the dims must be the
+ * context's (Q35M_ERR_INVALID otherwise). */
 int q35m_load_mixer_weights(q35m_ctx* ctx, const q35m_gguf* g, int num_layers, const unsigned char* is_recurrent,
                             int conv_dim, int n_v_heads, int v_head_dim, int head_dim);
 

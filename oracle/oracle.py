@@ -210,9 +210,15 @@ def deltanet_prefill(d: Dims, T, qkv, z, b, a, w: dict, state, conv_state=None):
     return out, cs, st, core
 
 
-def attn_decode(d: Dims, start, q_gate, k, v, w: dict, cache_k, cache_v, n_threads=1):
-    """Returns (out [n_heads*head_dim], cache_k', cache_v') with row `start` written."""
-    ck, cv = _f32(cache_k).copy(), _f32(cache_v).copy()
+def attn_decode(d: Dims, start, q_gate, k, v, w: dict, cache_k, cache_v, n_threads=1, inplace=False):
+    """Returns (out [n_heads*head_dim], cache_k', cache_v') with row `start` written.
+    inplace: write the row into cache_k / cache_v themselves (contiguous fp32
+    arrays) instead of into copies, for caches of many rows."""
+    if inplace:
+        assert all(a.dtype == np.float32 and a.flags.c_contiguous for a in (cache_k, cache_v))
+        ck, cv = cache_k, cache_v
+    else:
+        ck, cv = _f32(cache_k).copy(), _f32(cache_v).copy()
     out = np.empty(d.n_heads * d.head_dim, np.float32)
     lib().q35o_attn_decode(ctypes.byref(d), start, _p(_f32(q_gate)), _p(_f32(k)), _p(_f32(v)),
                            _p(_f32(w["q_norm"])), _p(_f32(w["k_norm"])), _p(ck), _p(cv),

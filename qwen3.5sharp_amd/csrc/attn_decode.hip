@@ -9,21 +9,28 @@
 // Ops.cs:281-357), causal softmax (Ops.SoftmaxCausal, Ops.cs:163-252),
 // P.V (Ops.AttentionCombine, Ops.cs:360-415), times sigmoid(gate).
 //
+// A sequence at length pos attends over pos + 1 rows: the pos cached rows
+// [0, pos) and the new row, which comes from the inputs.
+//
 // Pass 1 (attn_decode_partial): one workgroup per (sequence, kv head, chunk c
-// of NSUB 64-row sub-chunks).  Chunk c holds the sub-chunks c, c + nchunks,
-// c + 2 nchunks, ... so the workgroups of one cache that run together stream
-// adjacent rows.  The 4 q heads of the kv head share every K/V row it reads,
-// so each cache byte is read once per token.  A sub-chunk is processed with
+// of NSUB 64-row sub-chunks of the cached rows).  Chunk c holds the
+// sub-chunks c, c + nchunks, c + 2 nchunks, ... so the workgroups of one
+// cache that run together stream adjacent rows; the cached rows are split
+// exactly, so the grid has no second round of workgroups that each hold a
+// single row.  The 4 q heads of the kv head share every K/V row it reads, so
+// each cache byte is read once per token.  A sub-chunk is processed with
 // every K and V load issued before any arithmetic (64 KiB of K and 64 KiB of
 // V in flight per workgroup), which is what keeps HBM busy; the first
 // sub-chunk's loads go out before the q preparation, so that preparation
 // (each workgroup rotates and norms the 4 q rows, 4 KiB of input) costs no
-// memory round trip of its own.  The workgroup that holds the new position
-// also rotates/norms the new K row, writes K and V into the cache (single
-// writer) and takes them from LDS.  It emits, per q head, the chunk's max
-// score m, sum of exp l and unnormalised o = sum exp(s - m) v.
-// Pass 2 (attn_decode_merge): per (sequence, q head) the chunks are merged by
-// log-sum-exp rescaling and the sigmoid gate is applied.
+// memory round trip of its own.  Chunk 0 also rotates/norms the new K row,
+// writes K and V into the cache row pos (single writer; no workgroup reads
+// that row from memory) and folds the new row into its softmax from LDS
+// after its cached rows.  Every chunk emits, per q head, its max score m,
+// sum of exp l and unnormalised o = sum exp(s - m) v.
+// Pass 2 (attn_decode_merge): per (sequence, q head, 32-dim slice) the chunk
+// partials are merged by log-sum-exp rescaling in one round of loads and the
+// sigmoid gate is applied.
 //
 // Online softmax is the two-pass softmax regrouped; it omits the reference's
 // -80 floor on shifted logits, which only touches weights below e^-80
@@ -37,10 +44,6 @@ namespace {
 constexpr int NT = 256;
 constexpr int SUB = 64;   // positions per sub-chunk
 
-__device__ __forceinline__ float4 sel4(bool c, float4 a, float4 b) {
-    return make_float4(c ? a.x : b.x, c ? a.y : b.y, c ? a.z : b.z, c ? a.w : b.w);
-}
-
 template <int NSUB>
 __global__ __launch_bounds__(NT, 2) void attn_decode_partial(
     const float* __restrict__ q_gate, const float* __restrict__ knew,
@@ -50,10 +53,11 @@ __global__ __launch_bounds__(NT, 2) void attn_decode_partial(
     float* __restrict__ part_o, float* __restrict__ part_ml, int nkv, int cap, int nchunks,
     float eps, SeqBatch sb) {
     const int c = blockIdx.x, kvh = blockIdx.y, i = blockIdx.z;
-    const int pos = sb.pos[i];
-    // Workgroup c takes the sub-chunks c, c + nchunks, c + 2 nchunks, ...: the
-    // workgroups of one cache that run together read adjacent rows.
-    if (c * SUB > pos) return;
+    const int pos = sb.pos[i];               // cached rows [0, pos); the new row is pos
+    const bool has_rows = c * SUB < pos;     // uniform
+    const bool owner = c == 0;               // holds the new row
+    if (!has_rows && !owner) return;
+    const int last = pos - 1;                // last cached row (read only when has_rows)
     const int nh = nkv * kGqaGroup;
     const int kv_dim = nkv * kHd;
     // Cache of one (sequence, kv head): [cap][256], head-major.
@@ -69,6 +73,7 @@ __global__ __launch_bounds__(NT, 2) void attn_decode_partial(
     // parity so two barriers per sub-chunk suffice.
     __shared__ float sc[2][kGqaGroup][SUB];
     __shared__ float al_s[2][kGqaGroup];
+    __shared__ float nr_s[kGqaGroup][2];      // new row: rescale factor, weight
     __shared__ float ml_s[kGqaGroup][2];
     __shared__ float4 obuf[4][kGqaGroup][kHd / 4];
 
@@ -77,7 +82,6 @@ __global__ __launch_bounds__(NT, 2) void attn_decode_partial(
     // P.V layout: thread holds dims 4*d4..+3 of all 4 heads, positions ps + 4m.
     const int team = tid >> 4, l16 = tid & 15;
     const int d4 = tid & 63, ps = tid >> 6;
-    const bool owner = (pos / SUB) % nchunks == c;   // holds the new position
 
     // Operands of the q / new-row preparation, loaded before the first
     // sub-chunk's K/V so that their latency hides behind it: wave w prepares
@@ -93,19 +97,18 @@ __global__ __launch_bounds__(NT, 2) void attn_decode_partial(
     const float4 wk = *reinterpret_cast<const float4*>(k_norm + 4 * lane);
 
     // K/V rows of sub-chunk `S0` into kk / vv, all loads unconditional: rows
-    // past pos read row pos instead (its scores are masked, its V rows are
-    // zeroed before P.V), and row pos itself, which this launch writes, is
-    // replaced by the new row from LDS.
+    // past the last cached row read that row instead (their scores are masked
+    // to weight 0).
 #define Q35_LOAD_K(S0)                                                                           \
     _Pragma("unroll") for (int m = 0; m < 4; ++m) {                                              \
         const float4* krow = reinterpret_cast<const float4*>(                                    \
-            K + (size_t)min((S0) + team + 16 * m, pos) * kHd);                                   \
+            K + (size_t)min((S0) + team + 16 * m, last) * kHd);                                  \
         _Pragma("unroll") for (int j = 0; j < 4; ++j) kk[m][j] = krow[l16 + 16 * j];             \
     }
 #define Q35_LOAD_V(S0)                                                                           \
     _Pragma("unroll") for (int m = 0; m < 16; ++m) {                                             \
         const float4* vrow = reinterpret_cast<const float4*>(                                    \
-            V + (size_t)min((S0) + ps + 4 * m, pos) * kHd);                                      \
+            V + (size_t)min((S0) + ps + 4 * m, last) * kHd);                                     \
         vv[m] = vrow[d4];                                                                        \
     }
 
@@ -115,13 +118,6 @@ __global__ __launch_bounds__(NT, 2) void attn_decode_partial(
     // weight buffers alternate by sub-chunk parity PAR.
 #define Q35_SCORES(PAR)                                                                          \
     {                                                                                            \
-        if (owner) {                           /* uniform: the new K row from LDS */             \
-            _Pragma("unroll") for (int j = 0; j < 4; ++j) {                                      \
-                const float4 kn = knew_s[l16 + 16 * j];                                          \
-                _Pragma("unroll") for (int m = 0; m < 4; ++m)                                    \
-                    kk[m][j] = sel4(s0 + team + 16 * m == pos, kn, kk[m][j]);                    \
-            }                                                                                    \
-        }                                                                                        \
         float a[4][kGqaGroup];                                                                   \
         _Pragma("unroll") for (int h = 0; h < kGqaGroup; ++h) {                                  \
             float4 qh[4];                                                                        \
@@ -141,7 +137,7 @@ __global__ __launch_bounds__(NT, 2) void attn_decode_partial(
     }
 #define Q35_SOFTMAX_PV(PAR)                                                                      \
     {                                                                                            \
-        const int np = min(SUB, pos + 1 - s0);                                                   \
+        const int np = min(SUB, pos - s0);                                                       \
         lds_barrier();                                                                           \
         {                                                                                        \
             const float s = lane < np ? sc[PAR][wave][lane] : -INFINITY;                         \
@@ -158,14 +154,7 @@ __global__ __launch_bounds__(NT, 2) void attn_decode_partial(
             const float alpha = al_s[PAR][h];                                                    \
             acc[h].x *= alpha; acc[h].y *= alpha; acc[h].z *= alpha; acc[h].w *= alpha;          \
         }                                                                                        \
-        if (owner || np < SUB) {               /* uniform: rows past pos, the new V row */        \
-            const float4 vn = vnew_s[d4];                                                        \
-            _Pragma("unroll") for (int m = 0; m < 16; ++m) {                                     \
-                const int pp = ps + 4 * m;                                                       \
-                vv[m] = sel4(pp >= np, make_float4(0.f, 0.f, 0.f, 0.f),                          \
-                             sel4(s0 + pp == pos, vn, vv[m]));                                   \
-            }                                                                                    \
-        }                                                                                        \
+        /* masked positions carry weight exactly 0 (their V rows are row last) */               \
         _Pragma("unroll") for (int m = 0; m < 16; ++m) {                                         \
             const int pp = ps + 4 * m;                                                           \
             _Pragma("unroll") for (int h = 0; h < kGqaGroup; ++h) {                              \
@@ -187,8 +176,10 @@ __global__ __launch_bounds__(NT, 2) void attn_decode_partial(
     int s0 = c * SUB;
     float4 kk[4][4];
     float4 vv[16];
-    Q35_LOAD_K(s0)
-    Q35_LOAD_V(s0)
+    if (has_rows) {
+        Q35_LOAD_K(s0)
+        Q35_LOAD_V(s0)
+    }
     // q rows (the attention scale 1/sqrt(256) folded in); the owner also
     // rotates/norms the new K row and writes K and V into the cache.
     q_s[wave][lane] = rope_norm_regs(xq, rc, rs, wq, lane, eps, 1.0f / sqrtf((float)kHd));
@@ -204,22 +195,22 @@ __global__ __launch_bounds__(NT, 2) void attn_decode_partial(
         }
     }
     lds_barrier();
-    // Software pipeline: the next sub-chunk's K loads go out once the scores
-    // have consumed kk, its V loads once P.V has consumed vv.
-    // The last sub-chunk runs after the loop, without loads for a next one.
-    int sub = 0;
-    for (;;) {
-        const int s1 = s0 + nchunks * SUB;
-        if (sub + 1 == NSUB || s1 > pos) break;     // uniform across the workgroup
-        const int par = sub & 1;
-        Q35_SCORES(par)
-        Q35_LOAD_K(s1)
-        Q35_SOFTMAX_PV(par)
-        Q35_LOAD_V(s1)
-        ++sub;
-        s0 = s1;
-    }
-    {
+    if (has_rows) {
+        // Software pipeline: the next sub-chunk's K loads go out once the
+        // scores have consumed kk, its V loads once P.V has consumed vv.  The
+        // last sub-chunk runs after the loop, without loads for a next one.
+        int sub = 0;
+        for (;;) {
+            const int s1 = s0 + nchunks * SUB;
+            if (sub + 1 == NSUB || s1 >= pos) break;     // uniform across the workgroup
+            const int par = sub & 1;
+            Q35_SCORES(par)
+            Q35_LOAD_K(s1)
+            Q35_SOFTMAX_PV(par)
+            Q35_LOAD_V(s1)
+            ++sub;
+            s0 = s1;
+        }
         const int par = sub & 1;
         Q35_SCORES(par)
         Q35_SOFTMAX_PV(par)
@@ -228,6 +219,34 @@ __global__ __launch_bounds__(NT, 2) void attn_decode_partial(
 #undef Q35_LOAD_V
 #undef Q35_SCORES
 #undef Q35_SOFTMAX_PV
+
+    if (owner) {
+        // The new row, from LDS: wave h scores it against q of head h and
+        // folds it into head h's running softmax (m_run = -inf when the
+        // sequence has no cached rows: alpha = 0).
+        const float4 qh = q_s[wave][lane], kn = knew_s[lane];
+        const float s = wave_sum(qh.x * kn.x + qh.y * kn.y + qh.z * kn.z + qh.w * kn.w);
+        const float mx = fmaxf(m_run, s);
+        const float alpha = __expf(m_run - mx);
+        const float e = __expf(s - mx);
+        l_run = l_run * alpha + e;
+        m_run = mx;
+        if (lane == 0) {
+            nr_s[wave][0] = alpha;
+            nr_s[wave][1] = e;
+        }
+        lds_barrier();
+        const float4 vn = vnew_s[d4];
+#pragma unroll
+        for (int h = 0; h < kGqaGroup; ++h) {
+            const float al = nr_s[h][0];
+            const float en = ps == 0 ? nr_s[h][1] : 0.0f;    // added once per dim
+            acc[h].x = acc[h].x * al + en * vn.x;
+            acc[h].y = acc[h].y * al + en * vn.y;
+            acc[h].z = acc[h].z * al + en * vn.z;
+            acc[h].w = acc[h].w * al + en * vn.w;
+        }
+    }
 
 #pragma unroll
     for (int h = 0; h < kGqaGroup; ++h) obuf[ps][h][d4] = acc[h];
@@ -253,14 +272,29 @@ __global__ __launch_bounds__(NT, 2) void attn_decode_partial(
     }
 }
 
-// Merge of the chunk partials of one (sequence, q head, 64-dim slice): 256
-// threads; thread holds 4 dims (d4 = t % 16) of the slice and folds the
-// chunks c = t / 16 (mod 16) into a running (m, l, o) by log-sum-exp
-// rescaling, MU chunks per round with all their loads issued together; the 16
-// running triples of a column are then folded the same way through LDS.  One
-// memory round trip per MU chunks (the gate is loaded up front).
+// Log-sum-exp fold of the partial (m2, l2, o2) into (m, l, o).  An empty
+// partial has m = -inf and l = o = 0; two empty ones stay empty (no NaN).
+__device__ __forceinline__ void lse_fold(float& m, float& l, float4& o, float m2, float l2,
+                                         const float4& o2) {
+    const float mn = fmaxf(m, m2);
+    const float a = m == mn ? 1.0f : __expf(m - mn);
+    const float b = m2 == mn ? 1.0f : __expf(m2 - mn);
+    l = l * a + l2 * b;
+    o.x = o.x * a + o2.x * b;
+    o.y = o.y * a + o2.y * b;
+    o.z = o.z * a + o2.z * b;
+    o.w = o.w * a + o2.w * b;
+    m = mn;
+}
+
+// Merge of the chunk partials of one (sequence, q head, 32-dim slice): 256
+// threads, thread t holds 4 dims (d4 = t % 8) of the slice and folds the
+// chunks t / 8, t / 8 + 32, ... into a running (m, l, o): up to MU chunks per
+// thread with all their loads issued together, so up to 128 chunks take one
+// memory round trip.  The 32 running triples of a column are folded by
+// butterfly within each wave (8 per wave) and then across the 4 waves in LDS.
 constexpr int MT = 256;
-constexpr int MSLICE = 64;                 // dims per merge workgroup
+constexpr int MSLICE = 32;                 // dims per merge workgroup
 constexpr int MD4 = MSLICE / 4;            // float4 columns per slice
 constexpr int MG = MT / MD4;               // chunk groups
 constexpr int MU = 4;                      // chunks per thread per round
@@ -269,17 +303,18 @@ __global__ __launch_bounds__(MT) void attn_decode_merge(
     const float* __restrict__ part_o, const float* __restrict__ part_ml,
     const float* __restrict__ q_gate, float* __restrict__ out, int nkv, int nchunks, SeqBatch sb) {
     const int h = blockIdx.x / (kHd / MSLICE), slice = blockIdx.x % (kHd / MSLICE);
-    const int i = blockIdx.y, t = threadIdx.x;
+    const int i = blockIdx.y, t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int nh = nkv * kGqaGroup;
     const int kvh = h / kGqaGroup, hl = h % kGqaGroup;
-    const int nc = min(nchunks, sb.pos[i] / SUB + 1);
+    const int pos = sb.pos[i];
+    const int nc = max(1, min(nchunks, (pos + SUB - 1) / SUB));   // chunks that ran
     const size_t base = ((size_t)i * nkv + kvh) * nchunks;
-    __shared__ float4 obuf[MG][MD4];
-    __shared__ float mbuf[MG], lbuf[MG];
+    __shared__ float4 obuf[4][MD4];
+    __shared__ float mbuf[4], lbuf[4];
 
     const int d4 = t % MD4, g = t / MD4;
     const int col = slice * MD4 + d4;
-    // Gate of this thread's 4 output dims (used by threads t < MD4).
+    // Gate of this thread's 4 output dims (used by wave 0's first MD4 lanes).
     const int dim = slice * MSLICE + 4 * d4;
     const float4 gt = *reinterpret_cast<const float4*>(
         q_gate + (size_t)i * 2 * nh * kHd + (size_t)h * 2 * kHd + kHd + dim);
@@ -297,82 +332,88 @@ __global__ __launch_bounds__(MT) void attn_decode_merge(
             oc[u] = reinterpret_cast<const float4*>(part_o + pidx * kHd)[col];
         }
 #pragma unroll
-        for (int u = 0; u < MU; ++u) {
-            const bool valid = c0 + u * MG < nc;
-            const float mn = valid ? fmaxf(m, mc[u]) : m;
-            const float a = __expf(m - mn);             // 0 while m is -inf
-            const float b = valid ? __expf(mc[u] - mn) : 0.0f;
-            l = l * a + lc[u] * b;
-            o.x = o.x * a + oc[u].x * b;
-            o.y = o.y * a + oc[u].y * b;
-            o.z = o.z * a + oc[u].z * b;
-            o.w = o.w * a + oc[u].w * b;
-            m = mn;
-        }
+        for (int u = 0; u < MU; ++u)
+            if (c0 + u * MG < nc) lse_fold(m, l, o, mc[u], lc[u], oc[u]);
     }
-    obuf[g][d4] = o;
-    if (d4 == 0) {
-        mbuf[g] = m;
-        lbuf[g] = l;
+    // Butterfly over the 8 groups of each wave (lanes d4 + 8 k share a column).
+#pragma unroll
+    for (int k = MD4; k < kWave; k <<= 1) {
+        const float m2 = __shfl_xor(m, k, kWave), l2 = __shfl_xor(l, k, kWave);
+        float4 o2;
+        o2.x = __shfl_xor(o.x, k, kWave);
+        o2.y = __shfl_xor(o.y, k, kWave);
+        o2.z = __shfl_xor(o.z, k, kWave);
+        o2.w = __shfl_xor(o.w, k, kWave);
+        lse_fold(m, l, o, m2, l2, o2);
+    }
+    if (lane < MD4) {
+        obuf[wave][lane] = o;
+        if (lane == 0) {
+            mbuf[wave] = m;
+            lbuf[wave] = l;
+        }
     }
     __syncthreads();
     if (t < MD4) {
-        float M = mbuf[0];
 #pragma unroll
-        for (int w = 1; w < MG; ++w) M = fmaxf(M, mbuf[w]);
-        float4 s = make_float4(0.f, 0.f, 0.f, 0.f);
-        float L = 0.0f;
-#pragma unroll
-        for (int w = 0; w < MG; ++w) {
-            const float f = __expf(mbuf[w] - M);        // 0 for groups without chunks
-            const float4 ow = obuf[w][t];
-            s.x += ow.x * f; s.y += ow.y * f; s.z += ow.z * f; s.w += ow.w * f;
-            L += lbuf[w] * f;
-        }
-        const float inv = 1.0f / L;
+        for (int w = 1; w < 4; ++w) lse_fold(m, l, o, mbuf[w], lbuf[w], obuf[w][t]);
+        const float inv = 1.0f / l;
         float4 r;
-        r.x = s.x * inv * (1.0f / (1.0f + expf(-gt.x)));
-        r.y = s.y * inv * (1.0f / (1.0f + expf(-gt.y)));
-        r.z = s.z * inv * (1.0f / (1.0f + expf(-gt.z)));
-        r.w = s.w * inv * (1.0f / (1.0f + expf(-gt.w)));
+        r.x = o.x * inv * (1.0f / (1.0f + expf(-gt.x)));
+        r.y = o.y * inv * (1.0f / (1.0f + expf(-gt.y)));
+        r.z = o.z * inv * (1.0f / (1.0f + expf(-gt.z)));
+        r.w = o.w * inv * (1.0f / (1.0f + expf(-gt.w)));
         *reinterpret_cast<float4*>(out + (size_t)i * nh * kHd + (size_t)h * kHd + dim) = r;
     }
 }
 
-// Sub-chunks per workgroup: as many as keep >= 1024 workgroups (4 per CU),
-// at most 8, so partials stay small next to the cache they summarise.
-int pick_nsub(int n, int nkv, int max_len) {
-    for (int ns = 8; ns > 1; ns >>= 1)
-        if ((long)n * nkv * ((max_len + SUB * ns - 1) / (SUB * ns)) >= 1024) return ns;
-    return 1;
+// Sub-chunks of the longest cached range in the batch.
+int max_subchunks(const SeqBatch& sb) {
+    int m = 0;
+    for (int i = 0; i < sb.n; ++i) m = max(m, (sb.pos[i] + SUB - 1) / SUB);
+    return m;
 }
+
+// Sub-chunks per workgroup: the fewest that keep the grid within one round of
+// resident workgroups (2 per CU), at most 8 (beyond, longer workgroups were
+// not faster, and the partials stay small next to the cache they summarise).
+int pick_nsub(int n, int nkv, int max_subs, int n_cu) {
+    const long slots = 2L * n_cu;
+    for (int ns = 1; ns < 8; ns <<= 1)
+        if ((long)n * nkv * max(1, (max_subs + ns - 1) / ns) <= slots) return ns;
+    return 8;
+}
+
+int nchunks_for(int max_subs, int nsub) { return max(1, (max_subs + nsub - 1) / nsub); }
 
 }  // namespace
 
-size_t attn_decode_work_bytes(const Dims& d, int n, int max_kv_len) {
-    const int chunk = SUB * pick_nsub(n, d.nkv, max_kv_len);
-    const size_t nchunks = (max_kv_len + chunk - 1) / chunk;
-    return (size_t)n * d.nkv * nchunks * kGqaGroup * (kHd + 2) * sizeof(float);
+size_t attn_decode_work_bytes(const q35m_ctx* c, const SeqBatch& sb) {
+    const int max_subs = max_subchunks(sb);
+    const int nsub = pick_nsub(sb.n, c->d.nkv, max_subs, c->n_cu);
+    const size_t nchunks = nchunks_for(max_subs, nsub);
+    return (size_t)sb.n * c->d.nkv * nchunks * kGqaGroup * (kHd + 2) * sizeof(float);
 }
 
 hipError_t launch_attn_decode(q35m_ctx* c, int layer, const SeqBatch& sb, const float* q_gate,
-                              const float* k, const float* v, float* out) {
+                              const float* k, const float* v, float* out, float* work) {
     const Dims& d = c->d;
     const AttnLayer& L = c->full[layer];
-    int max_len = 0;
-    for (int i = 0; i < sb.n; ++i) max_len = max(max_len, sb.pos[i] + 1);
-    const int nsub = pick_nsub(sb.n, d.nkv, max_len);
-    const int chunk = SUB * nsub;
-    const int nchunks = (max_len + chunk - 1) / chunk;
-    float* part_o = c->work;
+    const int max_subs = max_subchunks(sb);
+    const int nsub = pick_nsub(sb.n, d.nkv, max_subs, c->n_cu);
+    const int nchunks = nchunks_for(max_subs, nsub);
+    float* part_o = work;
     float* part_ml = part_o + (size_t)sb.n * d.nkv * nchunks * kGqaGroup * kHd;
     const dim3 grid(nchunks, d.nkv, sb.n);
     {
-        ProfScope ps_(c, K_ATTN_DECODE_PARTIAL);
+        const int kid = nsub == 8 ? K_ATTN_DECODE_PARTIAL8
+                      : nsub == 4 ? K_ATTN_DECODE_PARTIAL4
+                      : nsub == 2 ? K_ATTN_DECODE_PARTIAL2 : K_ATTN_DECODE_PARTIAL1;
+        ProfScope ps_(c, kid);
 #define Q35_PARTIAL(NS)                                                                          \
-    hipExtLaunchKernelGGL(attn_decode_partial<NS>, grid, dim3(NT), 0, c->stream, ps_.a, ps_.b, 0, q_gate, k, v,      \
-                       L.q_norm, L.k_norm, L.k_cache, L.v_cache, c->rope_cos, c->rope_sin,       \
-                       part_o, part_ml, d.nkv, c->cap, nchunks, d.eps, sb)
+    hipExtLaunchKernelGGL(attn_decode_partial<NS>, grid, dim3(NT), 0, c->stream, ps_.a, ps_.b, 0, \
+                          q_gate, k, v, L.q_norm, L.k_norm, L.k_cache, L.v_cache, c->rope_cos,   \
+                          c->rope_sin, part_o, part_ml, d.nkv, c->cap, nchunks, d.eps, sb)
         if (nsub == 8) Q35_PARTIAL(8);
         else if (nsub == 4) Q35_PARTIAL(4);
         else if (nsub == 2) Q35_PARTIAL(2);
@@ -383,8 +424,8 @@ hipError_t launch_attn_decode(q35m_ctx* c, int layer, const SeqBatch& sb, const 
     if (e != hipSuccess) return e;
     {
         ProfScope ps_(c, K_ATTN_DECODE_MERGE);
-        hipExtLaunchKernelGGL(attn_decode_merge, dim3(d.nh * (kHd / MSLICE), sb.n), dim3(MT), 0, c->stream, ps_.a, ps_.b, 0, part_o,
-                           part_ml, q_gate, out, d.nkv, nchunks, sb);
+        hipExtLaunchKernelGGL(attn_decode_merge, dim3(d.nh * (kHd / MSLICE), sb.n), dim3(MT), 0, c->stream,
+                              ps_.a, ps_.b, 0, part_o, part_ml, q_gate, out, d.nkv, nchunks, sb);
     }
     return hipGetLastError();
 }

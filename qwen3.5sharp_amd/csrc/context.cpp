@@ -130,13 +130,31 @@ int build_seq_batch(const q35m_ctx* c, int n, const int* seqs, bool with_pos, q3
 // Sets the thread's last error from another translation unit.
 int q35_set_error(int code, const char* msg) { return fail(code, "%s", msg); }
 
+// The mixer dims a weight loader was given must be the context's: the
+// weight setters copy context-sized byte counts.
+int q35_check_mixer_dims(const q35m_ctx* c, int num_layers, const unsigned char* is_recurrent, int conv_dim,
+                         int n_v_heads, int v_head_dim, int head_dim) {
+    if (num_layers != c->cfg.num_layers)
+        return fail(Q35M_ERR_INVALID, "num_layers %d, the context has %d", num_layers, c->cfg.num_layers);
+    for (int l = 0; l < num_layers; l++)
+        if ((is_recurrent[l] != 0) != (c->is_recurrent[l] != 0))
+            return fail(Q35M_ERR_INVALID, "layer %d: is_recurrent %d, the context's layer is %s", l,
+                        is_recurrent[l] != 0, c->is_recurrent[l] ? "Gated-DeltaNet" : "full-attention");
+    if (conv_dim != c->d.conv_dim || n_v_heads != c->d.nv || v_head_dim != q35::kDk || head_dim != q35::kHd)
+        return fail(Q35M_ERR_INVALID,
+                    "dims conv %d, v heads %d, v head dim %d, head dim %d; the context has %d, %d, %d, %d",
+                    conv_dim, n_v_heads, v_head_dim, head_dim, c->d.conv_dim, c->d.nv, q35::kDk, q35::kHd);
+    return Q35M_OK;
+}
+
 
 namespace q35 {
 
 const char* kernel_name(int id) {
     static const char* names[K_COUNT] = {
         "deltanet_decode_kernel", "deltanet_conv_writeback", "dn_chunk_prep",
-        "dn_chunk_scan",          "dn_chunk_out",            "attn_decode_partial",
+        "dn_chunk_scan",          "dn_chunk_out",            "attn_decode_partial<1>",
+        "attn_decode_partial<2>", "attn_decode_partial<4>",  "attn_decode_partial<8>",
         "attn_decode_merge",      "attn_prefill_prep",       "attn_prefill_flash",
         "q8k_quantize",           "linear_q<4>",             "linear_q<6>",
         "q4k_gemm", "q6k_gemm", "add_rmsnorm"};
@@ -256,6 +274,12 @@ int q35m_create(const q35m_config* cfg, int n_seqs, int kv_capacity, q35m_ctx** 
     c->n_seqs = n_seqs;
     c->cap = kv_capacity;
     (void)hipGetDevice(&c->device);
+    {
+        int ncu = 0;
+        if (hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, c->device) == hipSuccess &&
+            ncu > 0)
+            c->n_cu = ncu;
+    }
     q35::Dims& d = c->d;
     d.nk = cfg->ssm_group_count;
     d.nv = cfg->ssm_time_step_rank;
@@ -469,10 +493,8 @@ int q35m_attn_decode(q35m_ctx* ctx, int layer, int n, const int* seqs, const flo
     q35::SeqBatch sb;
     r = build_seq_batch(ctx, n, seqs, true, &sb);
     if (r) return r;
-    int max_len = 0;
-    for (int i = 0; i < n; i++) max_len = sb.pos[i] + 1 > max_len ? sb.pos[i] + 1 : max_len;
-    HIP_TRY(q35::ensure_work(ctx, q35::attn_decode_work_bytes(ctx->d, n, max_len)), "workspace");
-    HIP_TRY(q35::launch_attn_decode(ctx, layer, sb, q_gate, k, v, out), "attn_decode");
+    HIP_TRY(q35::ensure_work(ctx, q35::attn_decode_work_bytes(ctx, sb)), "workspace");
+    HIP_TRY(q35::launch_attn_decode(ctx, layer, sb, q_gate, k, v, out, ctx->work), "attn_decode");
     return Q35M_OK;
 }
 
@@ -652,14 +674,23 @@ int q35m_snapshot_save(q35m_ctx* ctx, int seq, void* dev, size_t bytes, q35m_sna
 }
 
 int q35m_snapshot_restore(q35m_ctx* ctx, int seq, const void* dev, size_t bytes,
-                          const q35m_snapshot_info* info) {
+                          q35m_snapshot_info* info) {
     int r = snapshot_check(ctx, seq, dev, bytes, info);
     if (r) return r;
     if (info->epoch != ctx->epoch[seq] || info->kv_len > ctx->kv_len[seq])
         return fail(Q35M_ERR_RANGE,
-                    "snapshot at length %d no longer matches sequence %d at length %d (reset, truncate "
-                    "or K/V write since the save)", info->kv_len, seq, ctx->kv_len[seq]);
+                    "snapshot at length %d no longer matches sequence %d at length %d (reset, truncate, "
+                    "restore to a shorter length or K/V write since the save)",
+                    info->kv_len, seq, ctx->kv_len[seq]);
     if ((r = snapshot_copy(ctx, seq, const_cast<char*>((const char*)dev), false))) return r;
+    if (info->kv_len < ctx->kv_len[seq]) {
+        // Rows at and above the restored length will be written again, so
+        // snapshots taken at a longer length (which hold a linear state that
+        // went with the old rows) must be refused from now on: a new epoch.
+        // The snapshot just restored stays usable: it gets the new epoch.
+        ctx->epoch[seq]++;
+        info->epoch = ctx->epoch[seq];
+    }
     ctx->kv_len[seq] = info->kv_len;
     return Q35M_OK;
 }
@@ -787,13 +818,14 @@ int q35m_state_write(q35m_ctx* ctx, int layer, int seq, int kind, const void* ho
     int r = state_locate(ctx, layer, seq, kind, &base, &cap_bytes);
     if (r) return r;
     if (!host) return fail(Q35M_ERR_INVALID, "null host buffer");
-    if (is_kv(kind)) ctx->epoch[seq]++;
     if (bytes > cap_bytes)
         return fail(Q35M_ERR_INVALID, "write of %zu bytes exceeds the %zu-byte state", bytes,
                     cap_bytes);
     if (is_kv(kind)) {
         if (bytes % ((size_t)ctx->d.kv_dim * sizeof(float)))
             return fail(Q35M_ERR_INVALID, "K/V writes move whole rows of %d floats", ctx->d.kv_dim);
+        // Rows are about to change: snapshots of this sequence no longer hold.
+        ctx->epoch[seq]++;
         HIP_TRY(kv_copy(ctx, base, const_cast<void*>(host), bytes, false), "state_write");
     } else {
         HIP_TRY(hipMemcpyAsync(base, host, bytes, hipMemcpyHostToDevice, ctx->stream), "state_write");

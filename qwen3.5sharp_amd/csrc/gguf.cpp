@@ -19,6 +19,8 @@
 #include "../../include/q35mix.h"
 
 int q35_set_error(int code, const char* msg);
+int q35_check_mixer_dims(const q35m_ctx* ctx, int num_layers, const unsigned char* is_recurrent, int conv_dim,
+                         int n_v_heads, int v_head_dim, int head_dim);
 
 namespace {
 
@@ -227,11 +229,20 @@ int q35m_gguf_tensor(const q35m_gguf* g, const char* name, int* type, int64_t di
     auto it = g->tensors.find(name);
     if (it == g->tensors.end()) return fail(Q35M_ERR_RANGE, "no tensor '%s'", name);
     const Tensor& t = it->second;
+    // Element count and byte size with overflow checks: a header can claim
+    // dims whose product wraps a 64-bit count.
     uint64_t n = 1;
-    for (int d = 0; d < t.n_dims; d++) n *= (uint64_t)t.dims[d];
+    for (int d = 0; d < t.n_dims; d++) {
+        const uint64_t dd = (uint64_t)t.dims[d];
+        if (dd != 0 && n > UINT64_MAX / dd)
+            return fail(Q35M_ERR_INVALID, "tensor '%s' has an element count that overflows", name);
+        n *= dd;
+    }
+    if (n > UINT64_MAX / 4) return fail(Q35M_ERR_INVALID, "tensor '%s' is too large", name);
     const uint64_t nb = type_bytes(t.type, n);
     const uint64_t avail = g->size - (uint64_t)(g->data - static_cast<const unsigned char*>(g->map));
-    if (nb && (t.offset > avail || nb > avail - t.offset))
+    // The offset is checked for every type, the extent for the sized ones.
+    if (t.offset > avail || (nb && nb > avail - t.offset))
         return fail(Q35M_ERR_INVALID, "tensor '%s' runs past the end of the file", name);
     if (type) *type = t.type;
     if (n_dims) *n_dims = t.n_dims;
@@ -292,9 +303,12 @@ static int f32_tensor(const q35m_gguf* g, const std::string& name, uint64_t n, c
 int q35m_load_mixer_weights(q35m_ctx* ctx, const q35m_gguf* g, int num_layers, const unsigned char* is_recurrent,
                             int conv_dim, int n_v_heads, int v_head_dim, int head_dim) {
     if (!ctx || !g || !is_recurrent) return fail(Q35M_ERR_INVALID, "null pointer");
+    // The setters copy context-sized byte counts from the mapped tensors, so
+    // the sizes the tensors are checked against must be the context's.
+    int r = q35_check_mixer_dims(ctx, num_layers, is_recurrent, conv_dim, n_v_heads, v_head_dim, head_dim);
+    if (r) return r;
     for (int l = 0; l < num_layers; l++) {
         const std::string b = "blk." + std::to_string(l) + ".";
-        int r;
         if (is_recurrent[l]) {
             const float *cw, *sa, *dt, *sn;
             if ((r = f32_tensor(g, b + "ssm_conv1d.weight", 4ull * conv_dim, &cw))) return r;

@@ -48,8 +48,8 @@ struct DeltaNetLayer {
 struct AttnLayer {
     float* q_norm = nullptr;   // [head_dim]
     float* k_norm = nullptr;   // [head_dim]
-    float* k_cache = nullptr;  // [n_seqs][cap][kv_dim]
-    float* v_cache = nullptr;  // [n_seqs][cap][kv_dim]
+    float* k_cache = nullptr;  // [n_seqs][kv_heads][cap][head_dim], head-major
+    float* v_cache = nullptr;  // [n_seqs][kv_heads][cap][head_dim]
     bool has_weights = false;
 };
 
@@ -62,7 +62,10 @@ enum KernelId {
     K_DN_CHUNK_PREP,
     K_DN_CHUNK_SCAN,
     K_DN_CHUNK_OUT,
-    K_ATTN_DECODE_PARTIAL,
+    K_ATTN_DECODE_PARTIAL1,   // attn_decode_partial<NSUB> by sub-chunks per workgroup
+    K_ATTN_DECODE_PARTIAL2,
+    K_ATTN_DECODE_PARTIAL4,
+    K_ATTN_DECODE_PARTIAL8,
     K_ATTN_DECODE_MERGE,
     K_ATTN_PREFILL_PREP,
     K_ATTN_PREFILL_FLASH,
@@ -89,6 +92,7 @@ struct Dims {
 
 struct q35m_ctx {
     int device = 0;
+    int n_cu = 256;                    // compute units of the device
     hipStream_t stream = nullptr;
     q35m_config cfg{};
     q35::Dims d{};
@@ -122,9 +126,11 @@ hipError_t launch_deltanet_decode(q35m_ctx* c, int layer, const SeqBatch& sb, co
 hipError_t launch_deltanet_prefill(q35m_ctx* c, int layer, int seq, int T, const float* qkv,
                                    const float* z, const float* b, const float* a, float* out);
 size_t deltanet_prefill_work_bytes(const Dims& d, int T);
+// Decode attention: the split-K partials live in `work`, of at least
+// attn_decode_work_bytes(c, sb) bytes.
 hipError_t launch_attn_decode(q35m_ctx* c, int layer, const SeqBatch& sb, const float* q_gate,
-                              const float* k, const float* v, float* out);
-size_t attn_decode_work_bytes(const Dims& d, int n, int max_kv_len);
+                              const float* k, const float* v, float* out, float* work);
+size_t attn_decode_work_bytes(const q35m_ctx* c, const SeqBatch& sb);
 hipError_t launch_attn_prefill(q35m_ctx* c, int layer, int seq, int start, int T,
                                const float* q_gate, const float* k, const float* v, float* out);
 size_t attn_prefill_work_bytes(const Dims& d, int T);

@@ -431,6 +431,31 @@ def hip() -> ctypes.CDLL:
     return _hip
 
 
+HIP_ATTR_MULTIPROCESSOR_COUNT = 63   # hipDeviceAttributeMultiprocessorCount
+
+
+def cu_count(device: int = 0) -> int:
+    """Compute units of a device (the decode-attention split is sized by it)."""
+    n = ctypes.c_int(0)
+    h = hip()
+    h.hipDeviceGetAttribute.argtypes = [ctypes.POINTER(ctypes.c_int), ctypes.c_int, ctypes.c_int]
+    r = h.hipDeviceGetAttribute(ctypes.byref(n), HIP_ATTR_MULTIPROCESSOR_COUNT, device)
+    if r != 0:
+        raise RuntimeError(f"hipDeviceGetAttribute failed: {r}")
+    return n.value
+
+
+def attn_decode_variant(n_seqs: int, n_kv_heads: int, lengths, n_cu: int) -> int:
+    """Sub-chunks per workgroup the decode attention picks for a batch whose
+    sequences hold `lengths` cached rows: the fewest (1, 2, 4) keeping the
+    grid within 2 workgroups per CU, else 8."""
+    max_subs = max((int(x) + 63) // 64 for x in lengths)
+    for ns in (1, 2, 4):
+        if n_seqs * n_kv_heads * max(1, -(-max_subs // ns)) <= 2 * n_cu:
+            return ns
+    return 8
+
+
 class Event:
     def __init__(self):
         self.h = ctypes.c_void_p()

@@ -24,9 +24,11 @@ def _value(t, v) -> bytes:
 
 
 def write(path, kv: list, tensors: list, alignment: int | None = None, version: int = 3,
-          magic: bytes = b"GGUF") -> None:
+          magic: bytes = b"GGUF", offsets: list | None = None) -> None:
     """kv: [(key, type, value)] (ARRAY values as (elem_type, [values]));
-    tensors: [(name, ggml_type, dims innermost first, raw bytes)]."""
+    tensors: [(name, ggml_type, dims innermost first, raw bytes)];
+    offsets: data offsets to write into the tensor infos in place of the
+    computed ones (for files with bad offsets)."""
     if alignment is not None:
         kv = list(kv) + [("general.alignment", U32, alignment)]
     align = alignment or 32
@@ -38,16 +40,16 @@ def write(path, kv: list, tensors: list, alignment: int | None = None, version: 
             out += struct.pack("<IQ", et, len(vals)) + b"".join(_value(et, x) for x in vals)
         else:
             out += _value(t, v)
-    offsets, off = [], 0
+    computed, off = [], 0
     for _, _, _, raw in tensors:
-        offsets.append(off)
+        computed.append(off)
         off += (len(raw) + align - 1) // align * align
-    for (name, gt, dims, _), o in zip(tensors, offsets):
+    for (name, gt, dims, _), o in zip(tensors, computed if offsets is None else list(offsets)):
         out += _str(name) + struct.pack("<I", len(dims)) + b"".join(struct.pack("<q", d) for d in dims)
         out += struct.pack("<iQ", gt, o)
     if tensors:
         out += b"\0" * ((-len(out)) % align)
-    for (_, _, _, raw), o in zip(tensors, offsets):
+    for _, _, _, raw in tensors:
         out += raw + b"\0" * ((-len(raw)) % align)
     open(path, "wb").write(bytes(out))
 

@@ -56,3 +56,23 @@ def test_rejects_bad_files(tmp_path, case, code):
     with pytest.raises(q35mix.Q35Error) as e:
         q35mix.Gguf(p)
     assert e.value.code == getattr(q35mix, "ERR_" + code)
+
+
+def test_tensor_extent_checks(tmp_path):
+    """q35m_gguf_tensor refuses a tensor whose element count overflows 64 bits
+    and a tensor (of a type the reader sizes or not) whose offset lies past
+    the end of the file, rather than returning a pointer outside the mapping."""
+    p = tmp_path / "c.gguf"
+    ok = gw.f32("ok", np.ones(8, np.float32))
+    huge = ("huge", 0, (1 << 40, 1 << 40), b"")            # 2^80 F32 elements
+    far_f32 = ("far_f32", 0, (8,), b"")                     # F32 at a far offset
+    far_q40 = ("far_q40", 2, (32,), b"")                    # Q4_0: not sized by the reader
+    gw.write(p, [], [ok, huge, far_f32, far_q40], offsets=[0, 0, 1 << 30, 1 << 30])
+    g = q35mix.Gguf(p)
+    t, dims, raw = g.tensor("ok")
+    assert t == 0 and np.array_equal(np.frombuffer(raw, np.float32), np.ones(8, np.float32))
+    for name in ("huge", "far_f32", "far_q40"):
+        with pytest.raises(q35mix.Q35Error) as e:
+            g.tensor(name)
+        assert e.value.code == q35mix.ERR_INVALID, name
+    g.close()

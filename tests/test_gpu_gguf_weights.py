@@ -1,13 +1,17 @@
 """q35m_load_mixer_weights: the mixers' F32 tensors read from a GGUF file
 (written to the published layout by tests/gguf_writer.py under the
-reference's tensor names) give a context that decodes bit-identically to one
-whose weights were set directly; a missing or non-F32 tensor is refused."""
+reference's tensor names) give a context that decodes like the oracle given
+the same weights, and bit-identically to one whose weights were set
+directly; a missing or non-F32 tensor is refused, and so are dims that are
+not the context's."""
+import ctypes
 import sys
 
 import numpy as np
 import pytest
 
 import gguf_writer as gw
+import oracle
 import q35mix
 import synth
 
@@ -56,6 +60,25 @@ def test_loaded_weights_decode_identically(tmp_path):
         outs.append((od.download(), oa.download()))
     for u, v in zip(*outs):
         assert np.array_equal(u.view(np.uint32), v.view(np.uint32))
+    # oracle leg: zero state, position 0, the weights the file holds
+    d = oracle.dims()
+    conv_dim = 2 * NK * 128 + NV * 128
+    rd, _, _, _ = oracle.deltanet_decode(d, xd["qkv"][0], xd["z"][0], xd["b"][0], xd["a"][0], wd,
+                                         np.zeros((conv_dim, 3), np.float32), np.zeros((NV, 128, 128), np.float32))
+    z = np.zeros((1, NKV * HD), np.float32)
+    ra, _, _ = oracle.attn_decode(d, 0, xa["q_gate"][0], xa["k"][0], xa["v"][0], wa, z, z)
+    for got, ref in zip(outs[0], (rd, ra)):
+        e = float(np.max(np.abs(got[0].astype(np.float64) - ref)) / np.max(np.abs(ref)))
+        say(f"loaded weights vs oracle: rel err {e:.2e}")
+        assert e <= 1e-4
+    # dims that are not the context's are refused before any copy
+    lib = q35mix.lib()
+    rec = bytes([1, 0])
+    for args in ((2, rec, conv_dim // 2, NV, 128, HD), (2, rec, conv_dim, NV // 2, 128, HD),
+                 (2, rec, conv_dim, NV, 64, HD), (2, rec, conv_dim, NV, 128, 128),
+                 (1, rec, conv_dim, NV, 128, HD), (2, bytes([1, 1]), conv_dim, NV, 128, HD)):
+        r = lib.q35m_load_mixer_weights(ctypes.c_void_p(a.handle), ctypes.c_void_p(g.handle), *args)
+        assert r == q35mix.ERR_INVALID, args
     g.close()
     for name, kw, code in (("m.gguf", {"drop": "blk.0.ssm_a"}, q35mix.ERR_RANGE),
                            ("h.gguf", {"as_f16": "blk.1.attn_k_norm.weight"}, q35mix.ERR_UNSUPPORTED)):
