@@ -95,19 +95,23 @@ def time_calls(ctx, fn, steps, warmup):
     return ms / steps
 
 
-def time_calls_median(ctx, fn, steps, warmup):
-    """Per-call times from one event between consecutive calls (calls stay
-    back to back on the stream): (median ms, mean ms)."""
+def time_calls_median(ctx, fn, steps, warmup, group=10):
+    """Per-call time of back-to-back calls: `steps` calls in groups of
+    `group`, one event pair around each group (an event recorded between
+    single calls would add its own few microseconds to every call), the
+    median over the groups of the per-call mean: (median ms, mean ms)."""
     for i in range(warmup):
         fn(i)
     ctx.sync()
-    ev = [q35mix.Event() for _ in range(steps + 1)]
+    groups = max(1, steps // group)
+    ev = [q35mix.Event() for _ in range(groups + 1)]
     ev[0].record(ctx.stream)
-    for i in range(steps):
-        fn(warmup + i)
-        ev[i + 1].record(ctx.stream)
+    for g in range(groups):
+        for j in range(group):
+            fn(warmup + g * group + j)
+        ev[g + 1].record(ctx.stream)
     ev[-1].synchronize()
-    per = [ev[i].elapsed_ms(ev[i + 1]) for i in range(steps)]
+    per = [ev[g].elapsed_ms(ev[g + 1]) / group for g in range(groups)]
     return float(np.median(per)), float(np.mean(per))
 
 
@@ -573,10 +577,11 @@ def main():
 
     if want("dn_decode"):
         log("[bench] DeltaNet decode batch 1 ...")
-        (ms, mean_ms), kt = bench_dn_decode(max(K, 100), max(W, 20))
+        (ms, mean_ms), kt = bench_dn_decode(max(K, 200), max(W, 20))
         kname, kms = dominant(kt)
         workloads["deltanet_decode_b1"] = {
             "us_per_token": ms * 1e3, "us_per_token_mean": mean_ms * 1e3,
+            "timing": "median over 20 groups of 10 back-to-back calls",
             "hbm_frac_call": DN_DECODE_BYTES / (ms / 1e3) / HBM_PEAK,
             "kernel": kname, "kernel_us": kms * 1e3,
             "hbm_frac_kernel": DN_DECODE_BYTES / (kms / 1e3) / HBM_PEAK}
@@ -590,10 +595,11 @@ def main():
 
     if want("attn_decode"):
         log("[bench] GQA decode at 8193 rows ...")
-        (ms, mean_ms), kt = bench_attn_decode(max(K, 100), max(W, 20))
+        (ms, mean_ms), kt = bench_attn_decode(max(K, 200), max(W, 20))
         by = attn_decode_bytes(8193)
         workloads["attn_decode_8193"] = {
             "us_per_token": ms * 1e3, "us_per_token_mean": mean_ms * 1e3,
+            "timing": "median over 20 groups of 10 back-to-back calls",
             "hbm_frac_call": by / (ms / 1e3) / HBM_PEAK,
             "kernels_us": {k: v[0] * 1e3 for k, v in kt.items()}}
         if not args.no_cpu:
