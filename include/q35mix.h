@@ -172,6 +172,20 @@ int q35m_deltanet_prefill(q35m_ctx* ctx, int layer, int seq, int T, const float*
 int q35m_attn_decode(q35m_ctx* ctx, int layer, int n, const int* seqs, const float* q_gate,
                      const float* k, const float* v, float* out);
 
+/* The same as q35m_attn_decode, for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): it calls no hipMalloc, hipFree or other allocating
+ * routine.  No counterpart in the reference.  The split-K partials go to a
+ * fixed device array of Q35M_NOALLOC_SCRATCH_BYTES that the library holds
+ * on every GPU it runs on until the process ends; a call that would need
+ * more (roughly n * kv_heads * ceil(longest cached length / 512) * 16.5 KiB)
+ * is refused with Q35M_ERR_CAPACITY.  Every call on one GPU shares that
+ * array: calls that overlap on one GPU (other contexts or streams) race.
+ * The per-kernel timers are not used by this entry point. */
+#define Q35M_NOALLOC_SCRATCH_BYTES ((size_t)16 << 20)
+int q35m_attn_decode_noalloc(q35m_ctx* ctx, int layer, int n, const int* seqs, const float* q_gate,
+                             const float* k, const float* v, float* out);
+
 /* PrefillAttention steps after the projections (Qwen35Model.Prefill.cs:
  * 113-149) for T tokens of one sequence starting at row kv_len(seq).
  * q_gate [T][heads*2*head_dim]; k, v [T][kv_heads*head_dim];

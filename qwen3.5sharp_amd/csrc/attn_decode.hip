@@ -388,6 +388,17 @@ int nchunks_for(int max_subs, int nsub) { return max(1, (max_subs + nsub - 1) / 
 
 }  // namespace
 
+// Fixed device scratch of q35m_attn_decode_noalloc: the split-K partials of
+// one call (kNoAllocScratchBytes).  Every GPU the library runs on holds its
+// own copy until the process ends.  Host code never passes this name to a
+// kernel (on the host it is only a stand-in for the symbol): it uses the
+// device address that attn_decode_scratch_address returns.
+static __device__ __align__(256) float scratch[kNoAllocScratchBytes / sizeof(float)];
+
+hipError_t attn_decode_scratch_address(float** ptr) {
+    return hipGetSymbolAddress(reinterpret_cast<void**>(ptr), HIP_SYMBOL(scratch));
+}
+
 size_t attn_decode_work_bytes(const q35m_ctx* c, const SeqBatch& sb) {
     const int max_subs = max_subchunks(sb);
     const int nsub = pick_nsub(sb.n, c->d.nkv, max_subs, c->n_cu);

@@ -8,6 +8,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 
 #include "q35mix_internal.h"
@@ -122,6 +123,25 @@ int build_seq_batch(const q35m_ctx* c, int n, const int* seqs, bool with_pos, q3
             sb->pos[i] = p;
         }
     }
+    return Q35M_OK;
+}
+
+// Device address of the decode attention's fixed scratch, looked up once per
+// device (with that device current) and kept for the process.
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch[kMaxDevices] = {};
+
+int scratch_for_device(int device, float** out) {
+    if (device < 0 || device >= kMaxDevices) return fail(Q35M_ERR_NO_DEVICE, "device %d out of range", device);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch[device]) {
+        float* p = nullptr;
+        hipError_t e = q35::attn_decode_scratch_address(&p);
+        if (e != hipSuccess || !p) return hip_fail(e == hipSuccess ? hipErrorInvalidSymbol : e, "hipGetSymbolAddress(scratch)");
+        g_scratch[device] = p;
+    }
+    *out = g_scratch[device];
     return Q35M_OK;
 }
 
@@ -304,6 +324,14 @@ int q35m_create(const q35m_config* cfg, int n_seqs, int kv_capacity, q35m_ctx** 
     if (e != hipSuccess) {
         r = hip_fail(e, "hipStreamCreate");
         delete c;
+        return r;
+    }
+    // The device is current here: its fixed decode-attention scratch.
+    if ((r = scratch_for_device(c->device, &c->noalloc_scratch))) {
+        std::string msg = g_last_error;
+        release(c);
+        delete c;
+        g_last_error = msg;
         return r;
     }
     c->lin.resize(cfg->num_layers);
@@ -495,6 +523,32 @@ int q35m_attn_decode(q35m_ctx* ctx, int layer, int n, const int* seqs, const flo
     if (r) return r;
     HIP_TRY(q35::ensure_work(ctx, q35::attn_decode_work_bytes(ctx, sb)), "workspace");
     HIP_TRY(q35::launch_attn_decode(ctx, layer, sb, q_gate, k, v, out, ctx->work), "attn_decode");
+    return Q35M_OK;
+}
+
+int q35m_attn_decode_noalloc(q35m_ctx* ctx, int layer, int n, const int* seqs, const float* q_gate,
+                             const float* k, const float* v, float* out) {
+    int r = check_ctx(ctx);
+    if (!r) r = check_layer(ctx, layer, false);
+    if (r) return r;
+    if (!ctx->full[layer].has_weights) return fail(Q35M_ERR_INVALID, "layer %d has no weights", layer);
+    if (!q_gate || !k || !v || !out) return fail(Q35M_ERR_INVALID, "null activation pointer");
+    if (!ctx->noalloc_scratch) return fail(Q35M_ERR_NO_DEVICE, "no device scratch");
+    q35::SeqBatch sb;
+    r = build_seq_batch(ctx, n, seqs, true, &sb);
+    if (r) return r;
+    const size_t need = q35::attn_decode_work_bytes(ctx, sb);
+    if (need > q35::kNoAllocScratchBytes)
+        return fail(Q35M_ERR_CAPACITY,
+                    "attn_decode_noalloc: this batch needs %zu bytes of split-K partials, the fixed scratch "
+                    "holds %zu (use q35m_attn_decode, or fewer sequences per call)",
+                    need, q35::kNoAllocScratchBytes);
+    // No per-kernel timers here: they may create events.
+    const bool prof = ctx->profile;
+    ctx->profile = false;
+    hipError_t e = q35::launch_attn_decode(ctx, layer, sb, q_gate, k, v, out, ctx->noalloc_scratch);
+    ctx->profile = prof;
+    HIP_TRY(e, "attn_decode_noalloc");
     return Q35M_OK;
 }
 

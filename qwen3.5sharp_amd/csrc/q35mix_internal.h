@@ -108,6 +108,7 @@ struct q35m_ctx {
     int rope_cap = 0;
     float* work = nullptr;             // scratch for split-K partials and prefill
     size_t work_bytes = 0;
+    float* noalloc_scratch = nullptr;  // the device's fixed scratch (q35m_attn_decode_noalloc)
     std::vector<void*> allocations;
     // Per-kernel event timers (off unless q35m_profile enables them).
     bool profile = false;
@@ -131,6 +132,11 @@ size_t deltanet_prefill_work_bytes(const Dims& d, int T);
 hipError_t launch_attn_decode(q35m_ctx* c, int layer, const SeqBatch& sb, const float* q_gate,
                               const float* k, const float* v, float* out, float* work);
 size_t attn_decode_work_bytes(const q35m_ctx* c, const SeqBatch& sb);
+// Size of the fixed device scratch of q35m_attn_decode_noalloc.
+constexpr size_t kNoAllocScratchBytes = Q35M_NOALLOC_SCRATCH_BYTES;
+// Device address of that scratch on the current device (call with the device
+// current; each device has its own copy).
+hipError_t attn_decode_scratch_address(float** ptr);
 hipError_t launch_attn_prefill(q35m_ctx* c, int layer, int seq, int start, int T,
                                const float* q_gate, const float* k, const float* v, float* out);
 size_t attn_prefill_work_bytes(const Dims& d, int T);

@@ -310,6 +310,13 @@ class Context:
                                      _seqs(seqs), *[ctypes.c_void_p(x.ptr) for x in
                                                     (q_gate, k, v, out)]))
 
+    def attn_decode_noalloc(self, layer, seqs, q_gate, k, v, out) -> None:
+        """q35m_attn_decode with the split-K partials in the library's fixed
+        device scratch (no allocation)."""
+        check(lib().q35m_attn_decode_noalloc(ctypes.c_void_p(self.handle), layer, len(seqs),
+                                             _seqs(seqs), *[ctypes.c_void_p(x.ptr) for x in
+                                                            (q_gate, k, v, out)]))
+
     def attn_prefill(self, layer, seq, T, q_gate, k, v, out) -> None:
         check(lib().q35m_attn_prefill(ctypes.c_void_p(self.handle), layer, seq, T,
                                       *[ctypes.c_void_p(x.ptr) for x in (q_gate, k, v, out)]))
