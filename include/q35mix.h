@@ -261,6 +261,15 @@ int q35m_linear_q4k(q35m_ctx* ctx, const void* w, const float* x, float* y, int 
                     int tokens);
 int q35m_linear_q6k(q35m_ctx* ctx, const void* w, const float* x, float* y, int n_in, int n_out,
                     int tokens);
+/* The same for Q5_K (176 B a block) and IQ4_XS (136 B) weights: Q5K.Gemv /
+ * Q5K.Gemm (src/Qwen35Sharp.Kernels/Q5K.cs:97-117) and IQ4XS.Gemv /
+ * IQ4XS.Gemm (src/Qwen35Sharp.Kernels/IQ4XS.cs:75-104), whose scalar dot
+ * products (Q5K.Dot, Q5K.cs:45-95; IQ4XS.Dot, IQ4XS.cs:49-73) run per token;
+ * results are bit-identical to them. */
+int q35m_linear_q5k(q35m_ctx* ctx, const void* w, const float* x, float* y, int n_in, int n_out,
+                    int tokens);
+int q35m_linear_iq4xs(q35m_ctx* ctx, const void* w, const float* x, float* y, int n_in, int n_out,
+                      int tokens);
 
 /* The layer boundary around a mixer: hidden[t] += delta[t] (fp32 adds,
  * written back; delta NULL: no add), then y[t] = RmsNormZeroCentered(hidden[t],
@@ -294,6 +303,10 @@ int q35m_linear_q4k_prequant(q35m_ctx* ctx, const void* w, const void* q8, float
                              int n_out, int tokens);
 int q35m_linear_q6k_prequant(q35m_ctx* ctx, const void* w, const void* q8, float* y, int n_in,
                              int n_out, int tokens);
+int q35m_linear_q5k_prequant(q35m_ctx* ctx, const void* w, const void* q8, float* y, int n_in,
+                             int n_out, int tokens);
+int q35m_linear_iq4xs_prequant(q35m_ctx* ctx, const void* w, const void* q8, float* y, int n_in,
+                               int n_out, int tokens);
 
 /* Per-kernel HIP event timers, the device-side counterpart of the
  * reference's Qwen35Model.ProfileEnabled / Ticks* counters

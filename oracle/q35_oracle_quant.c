@@ -14,9 +14,16 @@
  * horizontal-sum order.  Compiled with -ffp-contract=off; fmaf() only where
  * the C# calls Fma.MultiplyAdd.
  *
+ * Q5_K and IQ4_XS have scalar paths only in the reference (Q5K.Dot,
+ * IQ4XS.Dot): exact integer sums per block or 32-value sub-block, then one
+ * short fp32 chain per block in block order with no fused multiply-add, which
+ * is restated as written.
+ *
  * Block formats (src/Qwen35Sharp.Kernels/BlockLayout.cs:32-78), packed:
  *   Q4_K (144 B): u16 d, u16 dmin (fp16), u8 scales[12], u8 qs[128]
+ *   Q5_K (176 B): u16 d, u16 dmin (fp16), u8 scales[12], u8 qh[32], u8 qs[128]
  *   Q6_K (210 B): u8 ql[128], u8 qh[64], i8 scales[16], u16 d (fp16)
+ *   IQ4_XS (136 B): u16 d (fp16), u16 scales_h, u8 scales_l[4], u8 qs[128]
  *   Q8_K (292 B): f32 d, i8 qs[256], i16 bsums[16]
  */
 #include "q35_oracle.h"
@@ -41,6 +48,19 @@ typedef struct __attribute__((packed)) {
 } blk_q6k;
 
 typedef struct __attribute__((packed)) {
+    uint16_t d, dmin;
+    uint8_t scales[12];
+    uint8_t qh[QK / 8];
+    uint8_t qs[QK / 2];
+} blk_q5k;
+
+typedef struct __attribute__((packed)) {
+    uint16_t d, scales_h;
+    uint8_t scales_l[QK / 64];
+    uint8_t qs[QK / 2];
+} blk_iq4xs;
+
+typedef struct __attribute__((packed)) {
     float d;
     int8_t qs[QK];
     int16_t bsums[QK / 16];
@@ -48,6 +68,8 @@ typedef struct __attribute__((packed)) {
 
 _Static_assert(sizeof(blk_q4k) == 144, "Q4_K block");
 _Static_assert(sizeof(blk_q6k) == 210, "Q6_K block");
+_Static_assert(sizeof(blk_q5k) == 176, "Q5_K block");
+_Static_assert(sizeof(blk_iq4xs) == 136, "IQ4_XS block");
 _Static_assert(sizeof(blk_q8k) == 292, "Q8_K block");
 
 /* HalfBits.ToSingle (BlockLayout.cs:155): the exact fp16 -> fp32 conversion
@@ -272,6 +294,124 @@ void q35o_q6k_dequantize_row(const void* wx, float* y, int k) {
     }
 }
 
+/* Q5K.Dot, src/Qwen35Sharp.Kernels/Q5K.cs:45-95: per block, the 5-bit values
+ * a = (nibble) + 16 * (high bit), acc = sum_j scale_j * (q8 . a over
+ * sub-block j), sumi = sum_j bsums[j] * min[j / 2] (exact integers); then
+ * sumf += d * acc - dmin * sumi with d = fp16(D) * dy, dmin = fp16(Dmin) * dy
+ * (int -> float conversions, no fused multiply-add). */
+float q35o_q5k_dot(const void* wx, const void* wy, int n) {
+    const blk_q5k* x = (const blk_q5k*)wx;
+    const blk_q8k* y = (const blk_q8k*)wy;
+    const int nb = n / QK;
+    float sumf = 0.0f;
+    for (int i = 0; i < nb; i++) {
+        int8_t aux[QK];
+        const uint8_t* q4 = x[i].qs;
+        const uint8_t* hm = x[i].qh;
+        int8_t* a = aux;
+        uint8_t m = 1;
+        for (int j = 0; j < QK / 64; j++) {
+            for (int l = 0; l < 32; l++) a[l] = (int8_t)((q4[l] & 0xF) + ((hm[l] & m) != 0 ? 16 : 0));
+            a += 32;
+            m <<= 1;
+            for (int l = 0; l < 32; l++) a[l] = (int8_t)((q4[l] >> 4) + ((hm[l] & m) != 0 ? 16 : 0));
+            a += 32;
+            m <<= 1;
+            q4 += 32;
+        }
+        uint8_t sm[16];
+        q4k_unpack_scales(x[i].scales, sm);
+        int sumi = 0;
+        for (int j = 0; j < QK / 16; j++) sumi += y[i].bsums[j] * sm[8 + j / 2];
+        int acc = 0;
+        for (int j = 0; j < QK / 32; j++) {
+            const int scale = sm[j];
+            for (int l = 0; l < 32; l++) acc += scale * y[i].qs[32 * j + l] * aux[32 * j + l];
+        }
+        const float d = q35o_half_to_float(x[i].d) * y[i].d;
+        const float dmin = q35o_half_to_float(x[i].dmin) * y[i].d;
+        sumf += d * acc - dmin * sumi;
+    }
+    return sumf;
+}
+
+/* Q5K.DequantizeRow, src/Qwen35Sharp.Kernels/Q5K.cs:5-43. */
+void q35o_q5k_dequantize_row(const void* wx, float* y, int k) {
+    const blk_q5k* x = (const blk_q5k*)wx;
+    for (int i = 0; i < k / QK; i++) {
+        const uint8_t* ql = x[i].qs;
+        const uint8_t* qh = x[i].qh;
+        const float d = q35o_half_to_float(x[i].d), mn = q35o_half_to_float(x[i].dmin);
+        uint8_t sm[16];
+        q4k_unpack_scales(x[i].scales, sm);
+        uint8_t u1 = 1, u2 = 2;
+        for (int j = 0, is = 0; j < QK; j += 64, is += 2) {
+            const float d1 = d * sm[is], m1 = mn * sm[8 + is];
+            const float d2 = d * sm[is + 1], m2 = mn * sm[8 + is + 1];
+            for (int l = 0; l < 32; l++) *y++ = d1 * ((ql[l] & 0xF) + ((qh[l] & u1) != 0 ? 16 : 0)) - m1;
+            for (int l = 0; l < 32; l++) *y++ = d2 * ((ql[l] >> 4) + ((qh[l] & u2) != 0 ? 16 : 0)) - m2;
+            ql += 32;
+            u1 <<= 2;
+            u2 <<= 2;
+        }
+    }
+}
+
+/* IQ4XS.KValues, src/Qwen35Sharp.Kernels/IQ4XS.cs:15-18: the non-linear grid. */
+static const int kvalues_iq4[16] = {-127, -104, -83, -65, -49, -35, -22, -10,
+                                    1,    13,   25,  38,  53,  69,  89,  113};
+
+/* IQ4XS.SubBlockScale, IQ4XS.cs:20-26: ls from 4 low bits (scales_l) and 2
+ * high bits (scales_h); dl = fp16(d) * (ls - 32). */
+static float iq4xs_dl(const blk_iq4xs* x, int ib) {
+    const int ls = ((x->scales_l[ib / 2] >> (4 * (ib % 2))) & 0xF) | (((x->scales_h >> (2 * ib)) & 3) << 4);
+    return q35o_half_to_float(x->d) * (ls - 32);
+}
+
+/* IQ4XS.Dot, src/Qwen35Sharp.Kernels/IQ4XS.cs:49-73: per 32-value sub-block
+ * the exact integer q8 . grid[idx] (low nibbles then high nibbles of 16
+ * bytes), then sumf += dl * acc * d8 (left to right, no fused multiply-add),
+ * sub-blocks in order. */
+float q35o_iq4xs_dot(const void* wx, const void* wy, int n) {
+    const blk_iq4xs* x = (const blk_iq4xs*)wx;
+    const blk_q8k* y = (const blk_q8k*)wy;
+    const int nb = n / QK;
+    float sumf = 0.0f;
+    for (int i = 0; i < nb; i++) {
+        const uint8_t* qs = x[i].qs;
+        const float d8 = y[i].d;
+        for (int ib = 0; ib < QK / 32; ib++) {
+            const float dl = iq4xs_dl(&x[i], ib);
+            const int8_t* q8 = y[i].qs + 32 * ib;
+            int acc = 0;
+            for (int j = 0; j < 16; j++) {
+                acc += q8[j] * kvalues_iq4[qs[j] & 0xF];
+                acc += q8[j + 16] * kvalues_iq4[qs[j] >> 4];
+            }
+            sumf += dl * acc * d8;
+            qs += 16;
+        }
+    }
+    return sumf;
+}
+
+/* IQ4XS.DequantizeRow, src/Qwen35Sharp.Kernels/IQ4XS.cs:28-47. */
+void q35o_iq4xs_dequantize_row(const void* wx, float* y, int k) {
+    const blk_iq4xs* x = (const blk_iq4xs*)wx;
+    for (int i = 0; i < k / QK; i++) {
+        const uint8_t* qs = x[i].qs;
+        for (int ib = 0; ib < QK / 32; ib++) {
+            const float dl = iq4xs_dl(&x[i], ib);
+            for (int j = 0; j < 16; j++) {
+                y[j] = dl * kvalues_iq4[qs[j] & 0xF];
+                y[j + 16] = dl * kvalues_iq4[qs[j] >> 4];
+            }
+            qs += 16;
+            y += 32;
+        }
+    }
+}
+
 /* GemmQ4K.GemmAvx2Tile (src/Qwen35Sharp.Kernels/GemmQ4K.Avx2.cs:39-207), the
  * reference's Q4_K path for more than one token (MulMatQ4K.Gemm,
  * MulMatQ4K.cs:45-127, over the x8 panels and the BlockQ4Kx8Meta sidecar of
@@ -307,17 +447,21 @@ static float q4k_panel_dot(const blk_q4k* x, const blk_q8k* y, int n) {
     return acc - mn;
 }
 
-/* Qwen35Model.Linear for Q4_K / Q6_K weights: MulMatQ4K.Gemv / Gemm
- * (src/Qwen35Sharp.Kernels/MulMatQ4K.cs:12-127) and Q6K.Gemv / Gemm
- * (src/Qwen35Sharp.Kernels/Q6K.cs:301-413): each token row is quantized to
+/* Qwen35Model.Linear for Q4_K / Q5_K / Q6_K / IQ4_XS weights: MulMatQ4K.Gemv
+ * / Gemm (src/Qwen35Sharp.Kernels/MulMatQ4K.cs:12-127), Q6K.Gemv / Gemm
+ * (src/Qwen35Sharp.Kernels/Q6K.cs:301-413), Q5K.Gemv / Gemm (Q5K.cs:97-117)
+ * and IQ4XS.Gemv / Gemm (IQ4XS.cs:75-104): each token row is quantized to
  * Q8_K, then every output is one dot product (the panel order above for Q4_K
- * with several tokens).  (Q6K.Gemm's
+ * with several tokens; Q5_K and IQ4_XS run their GEMV per token).  (Q6K.Gemm's
  * four-token DotAvx2x4 gives the same value per token as DotAvx2: the same
- * integer lanes and the same fma per block.)  type 4 = Q4_K, 6 = Q6_K. */
+ * integer lanes and the same fma per block.)  type 4 = Q4_K, 5 = Q5_K,
+ * 6 = Q6_K, 14 = IQ4_XS. */
 void q35o_linear_q(int type, const void* w, const float* x, float* y, int n_in, int n_out,
                    int tokens) {
     const int nb = n_in / QK;
-    const size_t wrow = (size_t)nb * (type == 4 ? sizeof(blk_q4k) : sizeof(blk_q6k));
+    const size_t bsz = type == 4 ? sizeof(blk_q4k) : type == 5 ? sizeof(blk_q5k)
+                     : type == 6 ? sizeof(blk_q6k) : sizeof(blk_iq4xs);
+    const size_t wrow = (size_t)nb * bsz;
     /* Q4_K with more than one token: the panel GEMM for the first n_out & ~7
      * outputs (MulMatQ4K.cs:104-123 sends the rest through VecDotQ4K.Dot). */
     const int panel_rows = (type == 4 && tokens > 1) ? (n_out & ~7) : 0;
@@ -330,8 +474,14 @@ void q35o_linear_q(int type, const void* w, const float* x, float* y, int n_in, 
             float v;
             if (r < panel_rows)
                 v = q4k_panel_dot((const blk_q4k*)wr, q8, n_in);
+            else if (type == 4)
+                v = q35o_q4k_dot(wr, q8, n_in);
+            else if (type == 5)
+                v = q35o_q5k_dot(wr, q8, n_in);
+            else if (type == 6)
+                v = q35o_q6k_dot(wr, q8, n_in);
             else
-                v = type == 4 ? q35o_q4k_dot(wr, q8, n_in) : q35o_q6k_dot(wr, q8, n_in);
+                v = q35o_iq4xs_dot(wr, q8, n_in);
             y[(size_t)t * n_out + r] = v;
         }
     }

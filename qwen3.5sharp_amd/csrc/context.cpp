@@ -177,7 +177,7 @@ const char* kernel_name(int id) {
         "attn_decode_partial<2>", "attn_decode_partial<4>",  "attn_decode_partial<8>",
         "attn_decode_merge",      "attn_prefill_prep",       "attn_prefill_flash",
         "q8k_quantize",           "linear_q<4>",             "linear_q<6>",
-        "q4k_gemm", "q6k_gemm", "add_rmsnorm"};
+        "q4k_gemm", "q6k_gemm", "add_rmsnorm", "linear_qs<5>", "linear_qs<14>"};
     return (id >= 0 && id < K_COUNT) ? names[id] : nullptr;
 }
 
@@ -789,6 +789,26 @@ int q35m_linear_q6k_prequant(q35m_ctx* ctx, const void* w, const void* q8, float
 int q35m_linear_q4k(q35m_ctx* ctx, const void* w, const float* x, float* y, int n_in, int n_out,
                     int tokens) {
     return linear_q(ctx, 4, w, x, y, n_in, n_out, tokens);
+}
+
+int q35m_linear_q5k(q35m_ctx* ctx, const void* w, const float* x, float* y, int n_in, int n_out,
+                    int tokens) {
+    return linear_q(ctx, 5, w, x, y, n_in, n_out, tokens);
+}
+
+int q35m_linear_iq4xs(q35m_ctx* ctx, const void* w, const float* x, float* y, int n_in, int n_out,
+                      int tokens) {
+    return linear_q(ctx, 14, w, x, y, n_in, n_out, tokens);
+}
+
+int q35m_linear_q5k_prequant(q35m_ctx* ctx, const void* w, const void* q8, float* y, int n_in,
+                             int n_out, int tokens) {
+    return linear_q_prequant(ctx, 5, w, q8, y, n_in, n_out, tokens);
+}
+
+int q35m_linear_iq4xs_prequant(q35m_ctx* ctx, const void* w, const void* q8, float* y, int n_in,
+                               int n_out, int tokens) {
+    return linear_q_prequant(ctx, 14, w, q8, y, n_in, n_out, tokens);
 }
 
 int q35m_linear_q6k(q35m_ctx* ctx, const void* w, const float* x, float* y, int n_in, int n_out,

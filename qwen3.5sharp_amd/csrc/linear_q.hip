@@ -374,6 +374,195 @@ __global__ __launch_bounds__(LQ_THREADS) void linear_q(const unsigned char* __re
     }
 }
 
+// ---------------------------------------------------------------- Q5_K, IQ4_XS
+
+// Formats whose reference dot product is scalar (Q5K.Dot, src/Qwen35Sharp.
+// Kernels/Q5K.cs:45-95; IQ4XS.Dot, IQ4XS.cs:49-73): exact integer sums per
+// block (Q5_K) or per 32-value sub-block (IQ4_XS), then one fp32 chain per
+// output in block order with no fused multiply-add.  Their Gemm runs the GEMV
+// per token (Q5K.cs:112-117, IQ4XS.cs:99-104), so every token is a GEMV here
+// too.  Block formats (BlockLayout.cs:49-66):
+//   Q5_K (176 B): f16 d, f16 dmin, u8 scales[12], u8 qh[32], u8 qs[128]
+//   IQ4_XS (136 B): f16 d, u16 scales_h, u8 scales_l[4], u8 qs[128]
+constexpr int Q5K_BYTES = 176, IQ4XS_BYTES = 136;
+constexpr int QS_TLD = 11;           // LDS stride of a block's integer terms
+
+// Q5_K x Q8_K block: acc = sum_j scale_j (q8 . a over sub-block j) with the
+// 5-bit values a = nibble + 16 * (qh bit), sumi = sum_j bsums[j] min[j / 2].
+// Group j (64 values) takes the low nibbles of qs[32 j ..] with qh bit 2j
+// (q8 bytes 64 j ..) and the high nibbles with qh bit 2j + 1 (q8 bytes
+// 64 j + 32 ..).  wb: the block's 44 dwords.
+__device__ __forceinline__ void q5k_block_terms(const uint32_t* __restrict__ wb,
+                                                const uint32_t* __restrict__ q8b, int& acc, int& sumi) {
+    const uint32_t s0 = wb[1], s1 = wb[2], s2 = wb[3];
+    const uint32_t kmask1 = 0x3f3f3f3fu, kmask2 = 0x0f0f0f0fu, kmask3 = 0x03030303u;
+    // Q4K.UnpackScales (Q4K.cs:20-33): bytes 0..7 scales, 8..15 mins.
+    const uint32_t su[2] = {s0 & kmask1, (s2 & kmask2) | (((s0 >> 6) & kmask3) << 4)};
+    const uint32_t mu[2] = {s1 & kmask1, ((s2 >> 4) & kmask2) | (((s1 >> 6) & kmask3) << 4)};
+    uint4 qv[16], bv[2];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) qv[i] = reinterpret_cast<const uint4*>(q8b + Q8K_QS)[i];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) bv[i] = reinterpret_cast<const uint4*>(q8b + Q8K_BS)[i];
+    const uint32_t* bs = reinterpret_cast<const uint32_t*>(bv);
+    sumi = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int m = (mu[j >> 2] >> (8 * (j & 3))) & 0xff;
+        sumi += __mul24((int)(int16_t)(bs[j] & 0xffff), m) + __mul24((int)(int16_t)(bs[j] >> 16), m);
+    }
+    const uint32_t* qh = wb + 4;                                  // 8 dwords
+    const uint32_t* qs = wb + 12;                                 // 32 dwords
+    const uint32_t* q8 = reinterpret_cast<const uint32_t*>(qv);   // 64 dwords
+    acc = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        int dl = 0, dh = 0;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const uint32_t wv = qs[8 * j + k], hv = qh[k];
+            const uint32_t lo = (wv & 0x0f0f0f0fu) | (((hv >> (2 * j)) & 0x01010101u) << 4);
+            const uint32_t hi = ((wv >> 4) & 0x0f0f0f0fu) | (((hv >> (2 * j + 1)) & 0x01010101u) << 4);
+            dl = __builtin_amdgcn_sdot4((int)lo, (int)q8[16 * j + k], dl, false);
+            dh = __builtin_amdgcn_sdot4((int)hi, (int)q8[16 * j + 8 + k], dh, false);
+        }
+        const int sl = (su[j >> 1] >> (16 * (j & 1))) & 0xff;
+        const int sh = (su[j >> 1] >> (16 * (j & 1) + 8)) & 0xff;
+        acc += __mul24(dl, sl) + __mul24(dh, sh);
+    }
+}
+
+// IQ4_XS x Q8_K block: acc[ib] = q8 . grid[idx] over sub-block ib (16 bytes:
+// low nibbles pair with q8 bytes 32 ib .. + 15, high nibbles with 32 ib +
+// 16 ..).  The grid (IQ4XS.cs:15-18) is looked up 4 bytes at a time with two
+// byte permutes (entries 0-7 and 8-7) and a select on the index's bit 3.
+// wb: the block's 34 dwords.
+__device__ __forceinline__ void iq4xs_block_terms(const uint32_t* __restrict__ wb,
+                                                  const uint32_t* __restrict__ q8b, int (&acc)[8]) {
+    // grid bytes: -127 -104 -83 -65 | -49 -35 -22 -10 | 1 13 25 38 | 53 69 89 113
+    const uint32_t g0 = 0xBFAD9881u, g1 = 0xF6EADDCFu, g2 = 0x26190D01u, g3 = 0x71594535u;
+    uint4 qv[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) qv[i] = reinterpret_cast<const uint4*>(q8b + Q8K_QS)[i];
+    const uint32_t* q8 = reinterpret_cast<const uint32_t*>(qv);
+    auto lookup = [&](uint32_t idx) {      // idx: four 4-bit indices, one a byte
+        const uint32_t sel = idx & 0x07070707u;
+        const uint32_t m = ((idx >> 3) & 0x01010101u) * 0xffu;
+        const uint32_t lo = __builtin_amdgcn_perm(g1, g0, sel), hi = __builtin_amdgcn_perm(g3, g2, sel);
+        return (lo & ~m) | (hi & m);
+    };
+#pragma unroll
+    for (int ib = 0; ib < 8; ++ib) {
+        int a = 0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const uint32_t wv = wb[2 + 4 * ib + k];
+            a = __builtin_amdgcn_sdot4((int)lookup(wv & 0x0f0f0f0fu), (int)q8[8 * ib + k], a, false);
+            a = __builtin_amdgcn_sdot4((int)lookup((wv >> 4) & 0x0f0f0f0fu), (int)q8[8 * ib + 4 + k], a, false);
+        }
+        acc[ib] = a;
+    }
+}
+
+// One 64-thread workgroup per group of up to 8 whole rows (at most 64
+// blocks, a block a thread, held in registers) and `tok_per_wg` tokens.  Per
+// token: the token's Q8_K row is staged in LDS, every thread forms its
+// block's integer terms, and one thread per row runs the reference's fp32
+// chain over the row's blocks in order.
+template <int QT>
+__global__ __launch_bounds__(LQ_THREADS) void linear_qs(const unsigned char* __restrict__ w,
+                                                        const uint32_t* __restrict__ q8,
+                                                        float* __restrict__ y, int n_in, int n_out,
+                                                        int tokens, int rows_per_wg, int tok_per_wg) {
+#pragma clang fp contract(off)
+    constexpr int BB = QT == 5 ? Q5K_BYTES : IQ4XS_BYTES;
+    extern __shared__ uint4 smem[];
+    const int nb = n_in / QK, lane = threadIdx.x;
+    const int row0 = blockIdx.x * rows_per_wg;
+    const int nrows = min(rows_per_wg, n_out - row0);
+    const int nblk = nrows * nb;
+    const int t_begin = blockIdx.y * tok_per_wg, t_end = min(tokens, t_begin + tok_per_wg);
+    uint32_t* q8s = reinterpret_cast<uint32_t*>(smem);
+    int* terms = reinterpret_cast<int*>(q8s + nb * Q8K_WORDS);
+
+    // The thread's block straight into registers (Q5_K blocks are 16-byte
+    // multiples, IQ4_XS blocks 8-byte multiples from a 16-byte aligned base).
+    uint32_t wb[BB / 4];
+    {
+        const unsigned char* src = w + ((size_t)row0 * nb + min(lane, nblk - 1)) * BB;
+        if constexpr (QT == 5) {
+#pragma unroll
+            for (int c = 0; c < BB / 16; ++c) reinterpret_cast<uint4*>(wb)[c] = reinterpret_cast<const uint4*>(src)[c];
+        } else {
+#pragma unroll
+            for (int c = 0; c < BB / 8; ++c) reinterpret_cast<uint2*>(wb)[c] = reinterpret_cast<const uint2*>(src)[c];
+        }
+    }
+    for (int t = t_begin; t < t_end; ++t) {
+        {
+            const uint4* src = reinterpret_cast<const uint4*>(q8 + (size_t)t * nb * Q8K_WORDS);
+            uint4* dst = reinterpret_cast<uint4*>(q8s);
+            const int n4 = nb * (Q8K_WORDS / 4);
+            for (int i0 = 0; i0 < n4; i0 += 8 * LQ_THREADS) {
+                uint4 qv[8];
+#pragma unroll
+                for (int c = 0; c < 8; ++c) {
+                    qv[c] = make_uint4(0u, 0u, 0u, 0u);
+                    if (i0 + lane + LQ_THREADS * c < n4) qv[c] = src[i0 + lane + LQ_THREADS * c];
+                }
+#pragma unroll
+                for (int c = 0; c < 8; ++c)
+                    if (i0 + lane + LQ_THREADS * c < n4) dst[i0 + lane + LQ_THREADS * c] = qv[c];
+            }
+        }
+        __syncthreads();
+        if (lane < nblk) {
+            const uint32_t* q8b = q8s + (lane % nb) * Q8K_WORDS;
+            int* out = terms + lane * QS_TLD;
+            if constexpr (QT == 5) {
+                int acc, sumi;
+                q5k_block_terms(wb, q8b, acc, sumi);
+                out[0] = acc;
+                out[1] = sumi;
+                out[2] = (int)wb[0];              // d, dmin
+            } else {
+                int acc[8];
+                iq4xs_block_terms(wb, q8b, acc);
+#pragma unroll
+                for (int ib = 0; ib < 8; ++ib) out[ib] = acc[ib];
+                out[8] = (int)wb[0];              // d, scales_h
+                out[9] = (int)wb[1];              // scales_l
+            }
+        }
+        __syncthreads();
+        if (lane < nrows) {
+            float sumf = 0.0f;
+            for (int b = 0; b < nb; ++b) {
+                const int* T = terms + (lane * nb + b) * QS_TLD;
+                const float yd = __builtin_bit_cast(float, q8s[b * Q8K_WORDS]);
+                if constexpr (QT == 5) {
+                    const uint32_t hdr = (uint32_t)T[2];
+                    const float d = half_bits_to_float(hdr & 0xffff) * yd;
+                    const float dmin = half_bits_to_float(hdr >> 16) * yd;
+                    sumf += d * (float)T[0] - dmin * (float)T[1];
+                } else {
+                    const uint32_t hdr = (uint32_t)T[8], sl = (uint32_t)T[9];
+                    const float d = half_bits_to_float(hdr & 0xffff);
+#pragma unroll
+                    for (int ib = 0; ib < 8; ++ib) {
+                        const int ls = (int)(((sl >> (8 * (ib >> 1) + 4 * (ib & 1))) & 0xf) |
+                                             (((hdr >> (16 + 2 * ib)) & 3) << 4));
+                        const float dl = d * (float)(ls - 32);
+                        sumf += dl * (float)T[ib] * yd;
+                    }
+                }
+            }
+            y[(size_t)t * n_out + row0 + lane] = sumf;
+        }
+        __syncthreads();
+    }
+}
+
 // ---------------------------------------------------------------- Q4_K, several tokens
 
 // The reference's Q4_K path for several tokens (MulMatQ4K.Gemm,
@@ -870,6 +1059,22 @@ hipError_t launch_linear_q_prequant(q35m_ctx* c, int qtype, const void* w, const
     const int nb = n_in / QK;
     const unsigned char* wb = reinterpret_cast<const unsigned char*>(w);
     const uint32_t* qb = reinterpret_cast<const uint32_t*>(q8);
+    if (qtype == 5 || qtype == 14) {
+        // Per-token GEMV; up to 8 tokens a workgroup (the weights stay in
+        // registers across them), more tokens over the grid's second axis.
+        const int rows_per_wg = min(LQ_THREADS / nb, LQ_MAX_ROWS);
+        const int tok_per_wg = 8;
+        const dim3 grid((n_out + rows_per_wg - 1) / rows_per_wg, (tokens + tok_per_wg - 1) / tok_per_wg);
+        const size_t lds = (size_t)nb * Q8K_WORDS * 4 + (size_t)LQ_THREADS * QS_TLD * 4;
+        ProfScope ps_(c, qtype == 5 ? K_Q5K_LINEAR : K_IQ4XS_LINEAR);
+        if (qtype == 5)
+            hipExtLaunchKernelGGL(linear_qs<5>, grid, dim3(LQ_THREADS), lds, c->stream, ps_.a, ps_.b, 0, wb, qb, y,
+                                  n_in, n_out, tokens, rows_per_wg, tok_per_wg);
+        else
+            hipExtLaunchKernelGGL(linear_qs<14>, grid, dim3(LQ_THREADS), lds, c->stream, ps_.a, ps_.b, 0, wb, qb, y,
+                                  n_in, n_out, tokens, rows_per_wg, tok_per_wg);
+        return hipGetLastError();
+    }
     // Q4_K with several tokens: the panel order for the first n_out & ~7 rows
     // (the reference's MulMatQ4K.Gemm), the GEMV for the rest.
     const int row_base = (qtype == 4 && tokens > 1) ? (n_out & ~7) : 0;

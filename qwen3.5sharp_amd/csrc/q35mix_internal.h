@@ -75,6 +75,8 @@ enum KernelId {
     K_Q4K_GEMM,
     K_Q6K_GEMM,
     K_ADD_RMSNORM,
+    K_Q5K_LINEAR,
+    K_IQ4XS_LINEAR,
     K_COUNT
 };
 const char* kernel_name(int id);

@@ -129,22 +129,25 @@ def kv_prefill(n_pos: int, kv_dim: int, salt: int = 0) -> tuple:
     return k, v
 
 
-QBLOCK_BYTES = {4: 144, 6: 210}
+QBLOCK_BYTES = {4: 144, 5: 176, 6: 210, 14: 136}
 
 
 def quant_weights(qtype: int, n_out: int, n_in: int, salt: int = 0) -> np.ndarray:
-    """GGUF Q4_K (qtype 4) or Q6_K (qtype 6) rows [n_out][n_in/256 blocks] as
-    bytes: every quant byte uniform, the fp16 block scales in [0.004, 0.02]
-    (finite, the size trained weights have)."""
+    """GGUF Q4_K (qtype 4), Q5_K (5), Q6_K (6) or IQ4_XS (14) rows
+    [n_out][n_in/256 blocks] as bytes: every quant byte uniform, the fp16
+    block scales in [0.004, 0.02] (finite, the size trained weights have; for
+    IQ4_XS a twentieth of that, its sub-block scales reaching 31)."""
     nblk = n_out * (n_in // 256)
     nb = QBLOCK_BYTES[qtype]
     raw = splitmix64(SEED_BASE + 300 + 10 * qtype + salt, (nblk * nb + 7) // 8)
     b = raw.view(np.uint8)[:nblk * nb].reshape(nblk, nb).copy()
     d = uniform(301 + 10 * qtype + salt, nblk, 0.004, 0.02).astype(np.float16)
-    if qtype == 4:
+    if qtype in (4, 5):
         b[:, 0:2] = d.view(np.uint8).reshape(-1, 2)
         b[:, 2:4] = uniform(302 + 10 * qtype + salt, nblk, 0.004, 0.02).astype(np.float16) \
             .view(np.uint8).reshape(-1, 2)
+    elif qtype == 14:
+        b[:, 0:2] = (d * np.float16(0.05)).view(np.uint8).reshape(-1, 2)
     else:
         b[:, 208:210] = d.view(np.uint8).reshape(-1, 2)
     return b.ravel()

@@ -1,9 +1,12 @@
-"""numpy helpers for the GGUF Q4_K / Q6_K / Q8_K block formats used by the
-quantized-projection tests: random blocks, independent decoders and packers.
+"""numpy helpers for the GGUF Q4_K / Q5_K / Q6_K / IQ4_XS / Q8_K block formats
+used by the quantized-projection tests: random blocks, independent decoders
+and packers.  Type codes: 4 = Q4_K, 5 = Q5_K, 6 = Q6_K, 14 = IQ4_XS.
 
 Layouts (src/Qwen35Sharp.Kernels/BlockLayout.cs:32-78 of the reference):
   Q4_K (144 B): f16 d, f16 dmin, u8 scales[12], u8 qs[128]
+  Q5_K (176 B): f16 d, f16 dmin, u8 scales[12], u8 qh[32], u8 qs[128]
   Q6_K (210 B): u8 ql[128], u8 qh[64], i8 scales[16], f16 d
+  IQ4_XS (136 B): f16 d, u16 scales_h, u8 scales_l[4], u8 qs[128]
   Q8_K (292 B): f32 d, i8 qs[256], i16 bsums[16]
 """
 from __future__ import annotations
@@ -11,7 +14,9 @@ from __future__ import annotations
 import numpy as np
 
 QK = 256
-BYTES = {4: 144, 6: 210}
+BYTES = {4: 144, 5: 176, 6: 210, 14: 136}
+# The IQ4_XS grid (llama.cpp kvalues_iq4nl), as the GGUF format defines it.
+IQ4_GRID = np.array([-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113], dtype=np.int64)
 
 
 def parse_q8k(buf):
@@ -32,10 +37,12 @@ def random_blocks(rng, qtype, nblocks, dscale=0.02):
     n = BYTES[qtype]
     b = rng.integers(0, 256, size=(nblocks, n), dtype=np.uint8)
     d = (rng.uniform(0.2, 1.0, nblocks) * dscale).astype(np.float16)
-    if qtype == 4:
+    if qtype in (4, 5):
         b[:, 0:2] = d.view(np.uint8).reshape(-1, 2)
         dm = (rng.uniform(0.2, 1.0, nblocks) * dscale).astype(np.float16)
         b[:, 2:4] = dm.view(np.uint8).reshape(-1, 2)
+    elif qtype == 14:
+        b[:, 0:2] = (d * np.float16(0.05)).view(np.uint8).reshape(-1, 2)   # dl = d (ls - 32), ls < 64
     else:
         b[:, 208:210] = d.view(np.uint8).reshape(-1, 2)
     return b.ravel()
@@ -82,6 +89,33 @@ def _dequant(qtype, w, dtype):
     b = np.asarray(w, dtype=np.uint8).reshape(-1, BYTES[qtype])
     out = np.empty((b.shape[0], QK), dtype=dtype)
     for i, blk in enumerate(b):
+        if qtype == 5:
+            # llama.cpp dequantize_row_q5_K: 64-value groups j, scale/min pair
+            # 2j (low nibbles, qh bit 2j) and 2j + 1 (high nibbles, qh bit 2j + 1)
+            d = dtype(blk[0:2].copy().view(np.float16)[0])
+            dmin = dtype(blk[2:4].copy().view(np.float16)[0])
+            sc, qh, qs = blk[4:16], blk[16:48].astype(np.int64), blk[48:176].astype(np.int64)
+            for j in range(4):
+                s0, m0 = q4k_scale_min(sc, 2 * j)
+                s1, m1 = q4k_scale_min(sc, 2 * j + 1)
+                q = qs[32 * j:32 * j + 32]
+                lo = (q & 15) + 16 * ((qh >> (2 * j)) & 1)
+                hi = (q >> 4) + 16 * ((qh >> (2 * j + 1)) & 1)
+                out[i, 64 * j:64 * j + 32] = dtype(d * dtype(s0)) * lo.astype(dtype) - dtype(dmin * dtype(m0))
+                out[i, 64 * j + 32:64 * j + 64] = dtype(d * dtype(s1)) * hi.astype(dtype) - dtype(dmin * dtype(m1))
+            continue
+        if qtype == 14:
+            # llama.cpp dequantize_row_iq4_xs
+            d = dtype(blk[0:2].copy().view(np.float16)[0])
+            sh = int(blk[2:4].copy().view(np.uint16)[0])
+            sl, qs = blk[4:8], blk[8:136].astype(np.int64)
+            for ib in range(8):
+                ls = ((int(sl[ib // 2]) >> (4 * (ib % 2))) & 15) | (((sh >> (2 * ib)) & 3) << 4)
+                dl = dtype(d * dtype(ls - 32))
+                q = qs[16 * ib:16 * ib + 16]
+                out[i, 32 * ib:32 * ib + 16] = dl * IQ4_GRID[q & 15].astype(dtype)
+                out[i, 32 * ib + 16:32 * ib + 32] = dl * IQ4_GRID[q >> 4].astype(dtype)
+            continue
         if qtype == 4:
             d = dtype(blk[0:2].copy().view(np.float16)[0])
             dmin = dtype(blk[2:4].copy().view(np.float16)[0])

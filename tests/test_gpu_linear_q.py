@@ -1,8 +1,9 @@
-"""Quantized projections (q35m_linear_q4k / q35m_linear_q6k) through the C ABI
-against the oracle: bit-exact (the kernels keep the reference's integer lanes
-and fp32 accumulation order: the AVX2 GEMV for one token and for Q6_K, the
-panel GEMM for Q4_K with several tokens plus the GEMV for its last
-n_out % 8 outputs), at the projection shapes of the 4B mixers
+"""Quantized projections (q35m_linear_q4k / _q5k / _q6k / _iq4xs) through the C
+ABI against the oracle: bit-exact (the kernels keep the reference's integer
+lanes and fp32 accumulation order: the AVX2 GEMV for one token and for Q6_K,
+the panel GEMM for Q4_K with several tokens plus the GEMV for its last
+n_out % 8 outputs, the scalar per-token dot of Q5_K and IQ4_XS), at the
+projection shapes of the 4B mixers
 (hidden 2560: qkv 8192, gate 4096, beta/alpha 32, ssm_out and attn_output
 4096 -> 2560, attn k/v 1024), ragged small shapes, several tokens, zero and
 extreme activation blocks, and weight buffers whose size is not a multiple of
@@ -49,10 +50,13 @@ SHAPES = [(2560, 8192, 1), (2560, 4096, 1), (2560, 32, 1), (4096, 2560, 1), (256
           (4096, 136, 130), (512, 40, 16), (1024, 72, 15)]
 
 
-@pytest.mark.parametrize("qtype", [4, 6])
+NAMES = {4: "Q4_K", 5: "Q5_K", 6: "Q6_K", 14: "IQ4_XS"}
+
+
+@pytest.mark.parametrize("qtype", [4, 5, 6, 14])
 @pytest.mark.parametrize("n_in,n_out,tokens", SHAPES)
 def test_linear_q_bit_exact(ctx, qtype, n_in, n_out, tokens):
-    say(f"linear_q Q{qtype}_K n_in={n_in} n_out={n_out} tokens={tokens}")
+    say(f"linear_q {NAMES[qtype]} n_in={n_in} n_out={n_out} tokens={tokens}")
     rng = np.random.default_rng(1000 * qtype + n_in + n_out + tokens)
     w = qb.random_blocks(rng, qtype, n_out * n_in // 256)
     x = rng.standard_normal((tokens, n_in)).astype(np.float32)
@@ -63,7 +67,7 @@ def test_linear_q_bit_exact(ctx, qtype, n_in, n_out, tokens):
     assert bad.size == 0
 
 
-@pytest.mark.parametrize("qtype", [4, 6])
+@pytest.mark.parametrize("qtype", [4, 5, 6, 14])
 def test_linear_q_activation_edges(ctx, qtype):
     """Zero blocks (scale 0), a first extremum that is positive (negative
     scale) or repeated with both signs, ties at .5 after scaling, huge and tiny
@@ -71,8 +75,8 @@ def test_linear_q_activation_edges(ctx, qtype):
     n_in, n_out = 2048, 40
     rng = np.random.default_rng(77 + qtype)
     w = qb.random_blocks(rng, qtype, n_out * n_in // 256)
-    w.reshape(-1, qb.BYTES[qtype])[3, (0 if qtype == 4 else 208):(2 if qtype == 4 else 210)] = \
-        np.frombuffer(np.float16(3e-6).tobytes(), np.uint8)
+    d_off = 208 if qtype == 6 else 0
+    w.reshape(-1, qb.BYTES[qtype])[3, d_off:d_off + 2] = np.frombuffer(np.float16(3e-6).tobytes(), np.uint8)
     x = rng.standard_normal((2, n_in)).astype(np.float32)
     x[0, 0:256] = 0.0
     x[0, 256:512] *= 1e-30
@@ -112,7 +116,7 @@ def test_prequant_matches_one_shot(ctx):
     x = rng.standard_normal((2, n_in)).astype(np.float32)
     dx = ctx.array((2, n_in), x)
     q8 = ctx.quantize_q8k(dx, n_in, 2)
-    for qtype, n_out in ((4, 8192), (4, 1024), (6, 1024)):
+    for qtype, n_out in ((4, 8192), (4, 1024), (6, 1024), (5, 1024), (14, 32)):
         w = qb.random_blocks(rng, qtype, n_out * n_in // 256)
         dw = ctx.bytes_array(w)
         dy = ctx.array((2, n_out))

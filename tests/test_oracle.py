@@ -70,6 +70,10 @@ class DotNetRandom:
     def next_double(self) -> float:
         return self._sample() * (1.0 / self.MBIG)
 
+    def next_bytes(self, n: int) -> bytes:
+        """Random.NextBytes: each byte is the low 8 bits of one sample."""
+        return bytes(self._sample() & 0xFF for _ in range(n))
+
 
 def test_dotnet_random_properties():
     r = DotNetRandom(1234)

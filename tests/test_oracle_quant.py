@@ -1,14 +1,15 @@
 """Pins the oracle's quantized-projection restatement (oracle/q35_oracle_quant.c).
 
-The reference has no tests for Q4_K / Q6_K / Q8_K, so the restatement is pinned
-by what the formats and the mathematics fix:
+The reference has no tests for Q4_K / Q5_K / Q6_K / Q8_K, so the restatement is
+pinned by what the formats and the mathematics fix (IQ4_XS also by the
+reference's own IQ4XSTests, ported with the same .NET Random draws):
   - fp16 decoding against numpy's float16 for every bit pattern;
   - Q8_K: the first extremum maps to exactly -127, ties round to even, the
     sign of the scale follows the first extremum, bsums are the sums of 16,
     and every value reconstructs within half a step;
-  - Q4_K / Q6_K dequantization against independent numpy decoders of the bit
-    layouts (Q4_K scales through the per-index GetScaleMin formula, not the
-    word-mask unpacking the dot product uses);
+  - Q4_K / Q5_K / Q6_K / IQ4_XS dequantization against independent numpy
+    decoders of the bit layouts (Q4_K / Q5_K scales through the per-index
+    GetScaleMin formula, not the word-mask unpacking the dot products use);
   - the integer dot products against fp64 dots of the dequantized weights
     with the dequantized activations (equal in exact arithmetic), and exact
     values on hand-built blocks.
@@ -29,6 +30,9 @@ sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
 
 import oracle  # noqa: E402
 import quant_blocks as qb  # noqa: E402
+from test_oracle import DotNetRandom  # noqa: E402
+
+ALL_TYPES = [4, 5, 6, 14]
 
 
 def test_half_to_float_all_patterns():
@@ -75,7 +79,7 @@ def test_q8k_random_against_numpy():
         assert np.all(np.abs(xb[i].astype(np.float64) - d[i] * q[i]) <= 0.5 * abs(d[i]) * (1 + 1e-6))
 
 
-@pytest.mark.parametrize("qtype", [4, 6])
+@pytest.mark.parametrize("qtype", ALL_TYPES)
 def test_dequantize_against_numpy_decoder(qtype):
     rng = np.random.default_rng(3 + qtype)
     w = qb.random_blocks(rng, qtype, 24)
@@ -84,7 +88,7 @@ def test_dequantize_against_numpy_decoder(qtype):
     assert np.array_equal(got, want)
 
 
-@pytest.mark.parametrize("qtype", [4, 6])
+@pytest.mark.parametrize("qtype", ALL_TYPES)
 def test_dot_against_fp64(qtype):
     rng = np.random.default_rng(20 + qtype)
     n = 256 * 16
@@ -97,7 +101,7 @@ def test_dot_against_fp64(qtype):
         wd = qb.dequant_f64(qtype, w)
         exact = float(np.dot(wd, xd))
         scale = float(np.dot(np.abs(wd), np.abs(xd)))
-        got = oracle.q4k_dot(w, q8, n) if qtype == 4 else oracle.q6k_dot(w, q8, n)
+        got = oracle.dot(qtype, w, q8, n)
         assert abs(got - exact) <= 2e-6 * scale + 1e-30, (trial, got, exact)
 
 
@@ -133,7 +137,98 @@ def test_q6k_dot_hand_built():
     assert oracle.q6k_dot(blk, q8, 256) == np.float32(want)
 
 
-@pytest.mark.parametrize("qtype", [4, 6])
+def test_q5k_dot_hand_built():
+    # d = 1, dmin = 0.5, every scale 1, every min 2, every nibble 1 (low) / 3
+    # (high), every qh bit set (+16): values 17 and 19; q8 all -127 with D = 1:
+    # -127 * 128 * (17 + 19) - 0.5 * (16 * 16 * -127 * 2).
+    blk = np.zeros(176, dtype=np.uint8)
+    blk[0:2] = np.frombuffer(np.float16(1.0).tobytes(), np.uint8)
+    blk[2:4] = np.frombuffer(np.float16(0.5).tobytes(), np.uint8)
+    blk[4:16] = qb.pack_q4k_scales([1] * 8, [2] * 8)
+    blk[16:48] = 0xFF
+    blk[48:] = 0x31
+    q8 = oracle.q8k_quantize(np.full(256, -127.0, dtype=np.float32))
+    want = -127 * 128 * 36 - 0.5 * (16 * 16 * -127 * 2)
+    assert oracle.q5k_dot(blk, q8, 256) == np.float32(want)
+    # the high bit matters: clearing qh gives values 1 and 3
+    blk[16:48] = 0
+    assert oracle.q5k_dot(blk, q8, 256) == np.float32(-127 * 128 * 4 - 0.5 * (16 * 16 * -127 * 2))
+
+
+def test_iq4xs_dot_hand_built():
+    # d = 1, every sub-block scale ls = 33 (dl = 1: low nibble 1, high bits 2),
+    # every byte 0x8F (low nibble 15 -> 113, high nibble 8 -> 1); q8 all -127,
+    # D = 1: 8 sub-blocks of -127 * 16 * (113 + 1).
+    blk = np.zeros(136, dtype=np.uint8)
+    blk[0:2] = np.frombuffer(np.float16(1.0).tobytes(), np.uint8)
+    blk[2:4] = np.frombuffer(np.uint16(0xAAAA).tobytes(), np.uint8)
+    blk[4:8] = 0x11
+    blk[8:] = 0x8F
+    q8 = oracle.q8k_quantize(np.full(256, -127.0, dtype=np.float32))
+    assert oracle.iq4xs_dot(blk, q8, 256) == np.float32(8 * -127 * 16 * 114)
+    # sub-block scale ls = 31 on sub-block 0 only (dl = -1): scales_l low nibble 15, high bits 1
+    blk[4] = 0x1F
+    blk[2:4] = np.frombuffer(np.uint16(0xAAA9).tobytes(), np.uint8)
+    assert oracle.iq4xs_dot(blk, q8, 256) == np.float32(6 * -127 * 16 * 114)
+
+
+def _force_valid_scales(raw, nb):
+    """IQ4XSTests.ForceValidScales: every block's fp16 grid scale = 1.0."""
+    for i in range(nb):
+        raw[i * 136] = 0x00
+        raw[i * 136 + 1] = 0x3C
+
+
+def test_iq4xs_reference_dequantize_row():
+    """Port of IQ4XSTests.DequantizeRow_MatchesReference
+    (tests/Qwen35Sharp.Tests/IQ4XSTests.cs:13-53): Random(7) bytes for 3
+    super-blocks, scales forced to 1.0, against the llama.cpp formula, 1e-4."""
+    nb, k = 3, 768
+    rng = DotNetRandom(7)
+    raw = bytearray(rng.next_bytes(nb * 136))
+    _force_valid_scales(raw, nb)
+    raw = np.frombuffer(bytes(raw), np.uint8)
+    expected = np.zeros(k, np.float32)
+    grid = qb.IQ4_GRID
+    for i in range(nb):
+        blk = raw[i * 136:(i + 1) * 136]
+        d = np.float32(blk[0:2].copy().view(np.float16)[0])
+        sh = int(blk[2:4].copy().view(np.uint16)[0])
+        qs = blk[8:]
+        for ib in range(8):
+            ls = ((int(blk[4 + ib // 2]) >> (4 * (ib % 2))) & 0xF) | (((sh >> (2 * ib)) & 3) << 4)
+            dl = np.float32(d * np.float32(ls - 32))
+            for j in range(16):
+                expected[i * 256 + ib * 32 + j] = dl * np.float32(grid[qs[16 * ib + j] & 0xF])
+                expected[i * 256 + ib * 32 + j + 16] = dl * np.float32(grid[qs[16 * ib + j] >> 4])
+    got = oracle.dequantize(14, raw, k)
+    assert np.all(np.abs(expected - got) < 1e-4)
+
+
+def test_iq4xs_reference_dot():
+    """Port of IQ4XSTests.Dot_MatchesScalarDequant (IQ4XSTests.cs:55-101):
+    Random(9) bytes for 2 super-blocks, scales forced to 1.0, activations
+    NextDouble() * 4 - 2 quantized to Q8_K; the dot against the fp32 sum of
+    the dequantized products, within 1e-2 or 1e-4 relative."""
+    nb, k = 2, 512
+    rng = DotNetRandom(9)
+    raw = bytearray(rng.next_bytes(nb * 136))
+    _force_valid_scales(raw, nb)
+    raw = np.frombuffer(bytes(raw), np.uint8)
+    act = np.array([np.float32(rng.next_double() * 4 - 2) for _ in range(k)], np.float32)
+    q8 = oracle.q8k_quantize(act)
+    dot = oracle.iq4xs_dot(raw, q8, k)
+    iq = oracle.dequantize(14, raw, k)
+    d, q, _ = qb.parse_q8k(q8)
+    q8v = (d[:, None] * q.astype(np.float32)).astype(np.float32).ravel()
+    expected = np.float32(0)
+    for i in range(k):
+        expected = np.float32(expected + np.float32(iq[i] * q8v[i]))
+    err = abs(float(expected) - float(dot))
+    assert err < 1e-2 or err < 1e-4 * abs(float(expected)), (expected, dot)
+
+
+@pytest.mark.parametrize("qtype", ALL_TYPES)
 def test_linear_q_against_fp64(qtype):
     rng = np.random.default_rng(40 + qtype)
     n_in, n_out, tokens = 512, 96, 3
