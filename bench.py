@@ -649,14 +649,17 @@ def main():
             "us": ms * 1e3, "bytes": by, "hbm_frac_call": by / (ms / 1e3) / HBM_PEAK,
             "kernels_us": {k: v[0] * 1e3 for k, v in kt.items()}}
         log(f"[bench] boundary_2048x2560: {workloads['boundary_2048x2560']}")
-    for qtype, n_in, n_out, copies in ((4, 2560, 8192, 32), (6, 4096, 2560, 40)):
+    qnames = {4: "q4k", 5: "q5k", 6: "q6k", 14: "iq4xs"}
+    gemv_kernel = {4: "linear_q<4>", 5: "linear_qs<5>", 6: "linear_q<6>", 14: "linear_qs<14>"}
+    for qtype, n_in, n_out, copies in ((4, 2560, 8192, 32), (6, 4096, 2560, 40), (5, 2560, 8192, 28),
+                                       (14, 2560, 8192, 40)):
         if not want("linear_q"):
             break
-        name = f"linear_q{qtype}k_{n_in}x{n_out}"
-        log(f"[bench] Q{qtype}_K projection {n_in} -> {n_out}, one token ...")
+        name = f"linear_{qnames[qtype]}_{n_in}x{n_out}"
+        log(f"[bench] {qnames[qtype]} projection {n_in} -> {n_out}, one token ...")
         ms, kt, by = bench_linear_q(qtype, n_in, n_out, max(K, 200), max(W, 20), copies)
         kus = {k: v[0] * 1e3 for k, v in kt.items()}
-        gemv = f"linear_q<{qtype}>"
+        gemv = gemv_kernel[qtype]
         workloads[name] = {
             "us_per_call": ms * 1e3, "bytes": by, "hbm_frac_call": by / (ms / 1e3) / HBM_PEAK,
             "kernels_us": kus, "hbm_frac_kernel": by / (kus[gemv] / 1e6) / HBM_PEAK}

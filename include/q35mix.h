@@ -268,6 +268,12 @@ int q35m_linear_q6k(q35m_ctx* ctx, const void* w, const float* x, float* y, int 
  * results are bit-identical to them. */
 int q35m_linear_q5k(q35m_ctx* ctx, const void* w, const float* x, float* y, int n_in, int n_out,
                     int tokens);
+/* F32 weights W [n_out][n_in] row-major in device memory (Qwen35Model.F32Gemm,
+ * src/Qwen35Sharp.Model/Qwen35Model.Decode.cs:129-140, the reference's Linear
+ * and DecodeLinear for F32 tensors): y[t][o] = Ops.DotF32(x[t], W[o])
+ * (Ops.cs:418-449), bit-identical to it; any n_in >= 1. */
+int q35m_linear_f32(q35m_ctx* ctx, const float* w, const float* x, float* y, int n_in, int n_out,
+                    int tokens);
 int q35m_linear_iq4xs(q35m_ctx* ctx, const void* w, const float* x, float* y, int n_in, int n_out,
                       int tokens);
 

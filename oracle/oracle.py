@@ -320,6 +320,15 @@ def linear_q(qtype: int, w, x, n_in, n_out) -> np.ndarray:
     return y
 
 
+def linear_f32(w, x, n_in, n_out) -> np.ndarray:
+    """Qwen35Model.F32Gemm: y[t][o] = Ops.DotF32(x[t], w[o]), w [n_out][n_in]."""
+    w = _f32(w).reshape(n_out, n_in)
+    x = _f32(x).reshape(-1, n_in)
+    y = np.empty((x.shape[0], n_out), dtype=np.float32)
+    lib().q35o_linear_f32(_p(w), _p(x), _p(y), ctypes.c_int(n_in), ctypes.c_int(n_out), ctypes.c_int(x.shape[0]))
+    return y
+
+
 def add_rmsnorm(hidden, delta, w, dim, eps=1e-6):
     """Ops.AddInPlace then Qwen35Ops.RmsNormZeroCentered over rows of dim:
     returns (hidden after the add, y).  delta / w may be None."""

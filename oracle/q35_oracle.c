@@ -358,6 +358,15 @@ static float dot_f32(const float* a, const float* b, int n) {
     return sum;
 }
 
+/* Qwen35Model.F32Gemm, src/Qwen35Sharp.Model/Qwen35Model.Decode.cs:129-140:
+ * y[t][o] = DotF32(x[t], W[o]) for W [n_out][n_in] row-major (the reference's
+ * Linear / DecodeLinear for F32 weights, Decode.cs:43-45, 77-79). */
+void q35o_linear_f32(const float* w, const float* x, float* y, int n_in, int n_out, int tokens) {
+    for (int t = 0; t < tokens; t++)
+        for (int o = 0; o < n_out; o++)
+            y[(size_t)t * n_out + o] = dot_f32(x + (size_t)t * n_in, w + (size_t)o * n_in, n_in);
+}
+
 /* Ops.DotF32x4, src/Qwen35Sharp.Model/Ops.cs:535-588 */
 static void dot_f32x4(const float* q, const float* k0, const float* k1, const float* k2,
                       const float* k3, int n, float* dst, float scale) {

@@ -93,6 +93,7 @@ float q35o_q4k_dot(const void* w, const void* q8, int n);
 float q35o_q6k_dot(const void* w, const void* q8, int n);
 void q35o_q4k_dequantize_row(const void* w, float* y, int k);
 void q35o_q6k_dequantize_row(const void* w, float* y, int k);
+void q35o_linear_f32(const float* w, const float* x, float* y, int n_in, int n_out, int tokens);
 float q35o_q5k_dot(const void* w, const void* q8, int n);
 float q35o_iq4xs_dot(const void* w, const void* q8, int n);
 void q35o_q5k_dequantize_row(const void* w, float* y, int k);

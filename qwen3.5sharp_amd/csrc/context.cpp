@@ -177,7 +177,7 @@ const char* kernel_name(int id) {
         "attn_decode_partial<2>", "attn_decode_partial<4>",  "attn_decode_partial<8>",
         "attn_decode_merge",      "attn_prefill_prep",       "attn_prefill_flash",
         "q8k_quantize",           "linear_q<4>",             "linear_q<6>",
-        "q4k_gemm", "q6k_gemm", "add_rmsnorm", "linear_qs<5>", "linear_qs<14>"};
+        "q4k_gemm", "q6k_gemm", "add_rmsnorm", "linear_qs<5>", "linear_qs<14>", "linear_f32"};
     return (id >= 0 && id < K_COUNT) ? names[id] : nullptr;
 }
 
@@ -789,6 +789,18 @@ int q35m_linear_q6k_prequant(q35m_ctx* ctx, const void* w, const void* q8, float
 int q35m_linear_q4k(q35m_ctx* ctx, const void* w, const float* x, float* y, int n_in, int n_out,
                     int tokens) {
     return linear_q(ctx, 4, w, x, y, n_in, n_out, tokens);
+}
+
+int q35m_linear_f32(q35m_ctx* ctx, const float* w, const float* x, float* y, int n_in, int n_out,
+                    int tokens) {
+    int r = check_ctx(ctx);
+    if (r) return r;
+    if (!w || !x || !y) return fail(Q35M_ERR_INVALID, "null pointer");
+    if (n_in < 1 || n_out < 1) return fail(Q35M_ERR_INVALID, "n_in %d, n_out %d", n_in, n_out);
+    if (tokens < 1 || tokens > 65535)
+        return fail(Q35M_ERR_INVALID, "tokens must be in [1, 65535] (got %d)", tokens);
+    HIP_TRY(q35::launch_linear_f32(ctx, w, x, y, n_in, n_out, tokens), "linear_f32");
+    return Q35M_OK;
 }
 
 int q35m_linear_q5k(q35m_ctx* ctx, const void* w, const float* x, float* y, int n_in, int n_out,

@@ -385,7 +385,7 @@ __global__ __launch_bounds__(LQ_THREADS) void linear_q(const unsigned char* __re
 //   Q5_K (176 B): f16 d, f16 dmin, u8 scales[12], u8 qh[32], u8 qs[128]
 //   IQ4_XS (136 B): f16 d, u16 scales_h, u8 scales_l[4], u8 qs[128]
 constexpr int Q5K_BYTES = 176, IQ4XS_BYTES = 136;
-constexpr int QS_TLD = 11;           // LDS stride of a block's integer terms
+constexpr int QS_TLD = 9;            // LDS stride of a block's chain terms
 
 // Q5_K x Q8_K block: acc = sum_j scale_j (q8 . a over sub-block j) with the
 // 5-bit values a = nibble + 16 * (qh bit), sumi = sum_j bsums[j] min[j / 2].
@@ -483,7 +483,7 @@ __global__ __launch_bounds__(LQ_THREADS) void linear_qs(const unsigned char* __r
     const int nblk = nrows * nb;
     const int t_begin = blockIdx.y * tok_per_wg, t_end = min(tokens, t_begin + tok_per_wg);
     uint32_t* q8s = reinterpret_cast<uint32_t*>(smem);
-    int* terms = reinterpret_cast<int*>(q8s + nb * Q8K_WORDS);
+    float* terms = reinterpret_cast<float*>(q8s + nb * Q8K_WORDS);
 
     // The thread's block straight into registers (Q5_K blocks are 16-byte
     // multiples, IQ4_XS blocks 8-byte multiples from a 16-byte aligned base).
@@ -516,50 +516,100 @@ __global__ __launch_bounds__(LQ_THREADS) void linear_qs(const unsigned char* __r
             }
         }
         __syncthreads();
+        // Each thread forms its block's terms of the reference's chain (they do
+        // not depend on the running sum); one thread per row then adds them in
+        // order.
         if (lane < nblk) {
             const uint32_t* q8b = q8s + (lane % nb) * Q8K_WORDS;
-            int* out = terms + lane * QS_TLD;
+            const float yd = __builtin_bit_cast(float, q8b[0]);
+            float* out = terms + lane * QS_TLD;
             if constexpr (QT == 5) {
                 int acc, sumi;
                 q5k_block_terms(wb, q8b, acc, sumi);
-                out[0] = acc;
-                out[1] = sumi;
-                out[2] = (int)wb[0];              // d, dmin
+                const float d = half_bits_to_float(wb[0] & 0xffff) * yd;
+                const float dmin = half_bits_to_float(wb[0] >> 16) * yd;
+                out[0] = d * (float)acc - dmin * (float)sumi;
             } else {
                 int acc[8];
                 iq4xs_block_terms(wb, q8b, acc);
+                const uint32_t hdr = wb[0], sl = wb[1];
+                const float d = half_bits_to_float(hdr & 0xffff);
 #pragma unroll
-                for (int ib = 0; ib < 8; ++ib) out[ib] = acc[ib];
-                out[8] = (int)wb[0];              // d, scales_h
-                out[9] = (int)wb[1];              // scales_l
+                for (int ib = 0; ib < 8; ++ib) {
+                    const int ls = (int)(((sl >> (8 * (ib >> 1) + 4 * (ib & 1))) & 0xf) |
+                                         (((hdr >> (16 + 2 * ib)) & 3) << 4));
+                    const float dl = d * (float)(ls - 32);
+                    out[ib] = dl * (float)acc[ib] * yd;
+                }
             }
         }
         __syncthreads();
         if (lane < nrows) {
+            constexpr int NTERM = QT == 5 ? 1 : 8;
             float sumf = 0.0f;
-            for (int b = 0; b < nb; ++b) {
-                const int* T = terms + (lane * nb + b) * QS_TLD;
-                const float yd = __builtin_bit_cast(float, q8s[b * Q8K_WORDS]);
-                if constexpr (QT == 5) {
-                    const uint32_t hdr = (uint32_t)T[2];
-                    const float d = half_bits_to_float(hdr & 0xffff) * yd;
-                    const float dmin = half_bits_to_float(hdr >> 16) * yd;
-                    sumf += d * (float)T[0] - dmin * (float)T[1];
-                } else {
-                    const uint32_t hdr = (uint32_t)T[8], sl = (uint32_t)T[9];
-                    const float d = half_bits_to_float(hdr & 0xffff);
+            const float* T = terms + lane * nb * QS_TLD;
+            for (int b = 0; b < nb; ++b)
 #pragma unroll
-                    for (int ib = 0; ib < 8; ++ib) {
-                        const int ls = (int)(((sl >> (8 * (ib >> 1) + 4 * (ib & 1))) & 0xf) |
-                                             (((hdr >> (16 + 2 * ib)) & 3) << 4));
-                        const float dl = d * (float)(ls - 32);
-                        sumf += dl * (float)T[ib] * yd;
-                    }
-                }
-            }
+                for (int k = 0; k < NTERM; ++k) sumf += T[b * QS_TLD + k];
             y[(size_t)t * n_out + row0 + lane] = sumf;
         }
         __syncthreads();
+    }
+}
+
+// ---------------------------------------------------------------- F32
+
+// Qwen35Model.F32Gemm (src/Qwen35Sharp.Model/Qwen35Model.Decode.cs:129-140):
+// y[t][o] = Ops.DotF32(x[t], W[o]) (Ops.cs:418-449) in its order: 16 FMA
+// lanes over 16-float strides (lane j takes elements 16 k + j), one 8-float
+// stride into lanes 0-7, then HorizontalSum(acc0 + acc1) and a scalar tail.
+// Four threads per output row, thread q holding reference lanes 4q .. 4q+3
+// (a float4 of each stride when rows are 16-byte aligned); 64 rows a
+// 256-thread workgroup, one token per grid row.
+template <bool VEC>
+__global__ __launch_bounds__(256) void linear_f32(const float* __restrict__ w, const float* __restrict__ x,
+                                                  float* __restrict__ y, int n_in, int n_out) {
+#pragma clang fp contract(off)
+    const int tid = threadIdx.x, q = tid & 3;
+    const int row = blockIdx.x * 64 + (tid >> 2), t = blockIdx.y;
+    const int rr = min(row, n_out - 1);            // rows past n_out compute row n_out - 1, not stored
+    const float* a = x + (size_t)t * n_in;
+    const float* b = w + (size_t)rr * n_in;
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    int i = 0;
+    for (; i + 16 <= n_in; i += 16) {
+        float av[4], bv[4];
+        if constexpr (VEC) {
+            const float4 a4 = *reinterpret_cast<const float4*>(a + i + 4 * q);
+            const float4 b4 = *reinterpret_cast<const float4*>(b + i + 4 * q);
+            av[0] = a4.x; av[1] = a4.y; av[2] = a4.z; av[3] = a4.w;
+            bv[0] = b4.x; bv[1] = b4.y; bv[2] = b4.z; bv[3] = b4.w;
+        } else {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) { av[k] = a[i + 4 * q + k]; bv[k] = b[i + 4 * q + k]; }
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k) acc[k] = fmaf(av[k], bv[k], acc[k]);
+    }
+    if (i + 8 <= n_in) {
+        if (q < 2)
+#pragma unroll
+            for (int k = 0; k < 4; ++k) acc[k] = fmaf(a[i + 4 * q + k], b[i + 4 * q + k], acc[k]);
+        i += 8;
+    }
+    // s_j = acc0_j + acc1_j: threads 0, 1 hold acc0 lanes 0-7, threads 2, 3 acc1.
+    float s[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) s[k] = acc[k] + __shfl_xor(acc[k], 2, kWave);
+    // HorizontalSum: (s_k + s_{k+4}) pairs, then (0 + 2) + (1 + 3).
+    float u[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) u[k] = s[k] + __shfl_xor(s[k], 1, kWave);
+    if (q == 0 && row < n_out) {
+        const float t0 = u[0] + u[2], t1 = u[1] + u[3];
+        float sum = t0 + t1;
+        for (; i < n_in; ++i) sum += a[i] * b[i];
+        y[(size_t)t * n_out + row] = sum;
     }
 }
 
@@ -1129,6 +1179,18 @@ hipError_t launch_add_rmsnorm(q35m_ctx* c, float* hidden, const float* delta, co
     };
     if (delta) q8 ? go(add_rmsnorm<true, true>) : go(add_rmsnorm<true, false>);
     else q8 ? go(add_rmsnorm<false, true>) : go(add_rmsnorm<false, false>);
+    return hipGetLastError();
+}
+
+hipError_t launch_linear_f32(q35m_ctx* c, const float* w, const float* x, float* y, int n_in, int n_out,
+                             int tokens) {
+    const bool vec = n_in % 4 == 0 && ((reinterpret_cast<uintptr_t>(w) | reinterpret_cast<uintptr_t>(x)) & 15) == 0;
+    const dim3 grid((n_out + 63) / 64, tokens);
+    ProfScope ps_(c, K_F32_LINEAR);
+    if (vec)
+        hipExtLaunchKernelGGL(linear_f32<true>, grid, dim3(256), 0, c->stream, ps_.a, ps_.b, 0, w, x, y, n_in, n_out);
+    else
+        hipExtLaunchKernelGGL(linear_f32<false>, grid, dim3(256), 0, c->stream, ps_.a, ps_.b, 0, w, x, y, n_in, n_out);
     return hipGetLastError();
 }
 

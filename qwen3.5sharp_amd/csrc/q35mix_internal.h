@@ -77,6 +77,7 @@ enum KernelId {
     K_ADD_RMSNORM,
     K_Q5K_LINEAR,
     K_IQ4XS_LINEAR,
+    K_F32_LINEAR,
     K_COUNT
 };
 const char* kernel_name(int id);
@@ -147,6 +148,8 @@ hipError_t launch_linear_q(q35m_ctx* c, int qtype, const void* w, const float* x
 hipError_t launch_add_rmsnorm(q35m_ctx* c, float* hidden, const float* delta, const float* w, float* y, void* q8,
                               int dim, int tokens, float eps);
 size_t linear_q_work_bytes(int n_in, int tokens);
+hipError_t launch_linear_f32(q35m_ctx* c, const float* w, const float* x, float* y, int n_in, int n_out,
+                             int tokens);
 hipError_t launch_q8k_quantize(q35m_ctx* c, const float* x, void* q8, int n_in, int tokens);
 hipError_t launch_linear_q_prequant(q35m_ctx* c, int qtype, const void* w, const void* q8, float* y,
                                     int n_in, int n_out, int tokens);

@@ -380,6 +380,11 @@ class Context:
         check(fn(ctypes.c_void_p(self.handle), ctypes.c_void_p(w.ptr), ctypes.c_void_p(x.ptr),
                  ctypes.c_void_p(y.ptr), n_in, n_out, tokens))
 
+    def linear_f32(self, w, x, y, n_in, n_out, tokens) -> None:
+        """y[tokens][n_out] = W x for F32 weights W [n_out][n_in] (Ops.DotF32 order)."""
+        check(lib().q35m_linear_f32(ctypes.c_void_p(self.handle), ctypes.c_void_p(w.ptr), ctypes.c_void_p(x.ptr),
+                                    ctypes.c_void_p(y.ptr), n_in, n_out, tokens))
+
     # ---- per-kernel event timers -----------------------------------------
     def profile(self, enable: bool) -> None:
         check(lib().q35m_profile(self.handle, int(enable)))

@@ -129,3 +129,25 @@ def test_prequant_matches_one_shot(ctx):
         dy.free()
     q8.free()
     dx.free()
+
+
+@pytest.mark.parametrize("n_in,n_out,tokens", [(2560, 32, 1), (2560, 4096, 2), (4096, 129, 3), (17, 70, 5),
+                                               (24, 3, 1), (7, 65, 2), (2561, 40, 70), (1, 1, 1)])
+def test_linear_f32_bit_exact(ctx, n_in, n_out, tokens):
+    """F32 weights: Ops.DotF32's lane order, bit for bit, also at widths that
+    are not multiples of 16, 8 or 4 (the scalar loads and the 8-wide stride)."""
+    say(f"linear_f32 n_in={n_in} n_out={n_out} tokens={tokens}")
+    rng = np.random.default_rng(n_in + 7 * n_out + tokens)
+    w = rng.standard_normal((n_out, n_in)).astype(np.float32)
+    x = rng.standard_normal((tokens, n_in)).astype(np.float32)
+    if n_in >= 17:
+        x[0, 0] = 2.0 ** 24          # order-dependent row
+        w[0, :] = 1.0
+        x[0, 1:] = 1.0
+    dw, dx, dy = ctx.array((n_out, n_in), w), ctx.array((tokens, n_in), x), ctx.array((tokens, n_out))
+    ctx.linear_f32(dw, dx, dy, n_in, n_out, tokens)
+    got = dy.download()
+    want = oracle.linear_f32(w, x, n_in, n_out)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    for a in (dw, dx, dy):
+        a.free()

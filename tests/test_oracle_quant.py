@@ -269,3 +269,30 @@ def test_q4k_several_tokens_panel_rows_and_gemv_tail():
     q8 = oracle.q8k_quantize(x[0])
     gemv = np.array([oracle.q4k_dot(rows[r], q8, n_in) for r in range(n_out)], np.float32)
     assert np.array_equal(y1[0].view(np.uint32), gemv.view(np.uint32))
+
+
+def test_linear_f32_lane_order():
+    """Ops.DotF32's order, pinned on rows whose sum depends on it: 2^24 in
+    lane 0 and ones elsewhere.  With 17 elements the 16 lanes hold 2^24, 1 x 15
+    (2^24 + 1 rounds back to 2^24 in acc0 + acc1), the horizontal sum gives
+    2^24 + 14, and the scalar tail adds 1 more: 2^24 + 15 rounds to 2^24 + 16.
+    A sequential sum would stay at 2^24.  With 24 elements the 8-wide chunk
+    goes into acc0 (lane 0 gets 2^24 + 1 -> 2^24 again)."""
+    big = np.float32(2.0 ** 24)
+    for n, want in ((17, 2.0 ** 24 + 16), (24, 2.0 ** 24 + 22), (7, 2.0 ** 24)):
+        x = np.ones((1, n), np.float32)
+        x[0, 0] = big
+        w = np.ones((1, n), np.float32)
+        got = oracle.linear_f32(w, x, n, 1)[0, 0]
+        assert got == np.float32(want), (n, got)
+
+
+def test_linear_f32_against_fp64():
+    rng = np.random.default_rng(123)
+    for n_in, n_out, tokens in ((2560, 32, 2), (31, 5, 3), (8, 4, 1), (4099, 9, 2)):
+        w = rng.standard_normal((n_out, n_in)).astype(np.float32)
+        x = rng.standard_normal((tokens, n_in)).astype(np.float32)
+        y = oracle.linear_f32(w, x, n_in, n_out)
+        exact = x.astype(np.float64) @ w.astype(np.float64).T
+        scale = np.abs(x.astype(np.float64)) @ np.abs(w.astype(np.float64)).T
+        assert np.all(np.abs(y - exact) <= 2e-6 * scale)
