@@ -53,8 +53,9 @@ extern "C" {
 /* Mixer hyper-parameters: the mixer fields of ModelConfig
  * (src/Qwen35Sharp.Model/ModelConfig.cs:19-54).  The kernels are built for
  * ssm_state_size = 128 (dk = dv), head_dim = 256, rope_dim = 64,
- * ssm_conv_kernel = 4, num_heads = 4 * num_kv_heads; head counts are free
- * (ssm_time_step_rank a multiple of ssm_group_count). */
+ * ssm_conv_kernel = 4; head counts are free within: num_heads = G *
+ * num_kv_heads with G = 1, 2, 4 or a multiple of 8, and ssm_time_step_rank =
+ * R * ssm_group_count with R = 1 .. 4. */
 typedef struct q35m_config {
     int num_layers;
     int num_heads;          /* full-attention q heads            (16)  */

@@ -35,6 +35,8 @@
 // Online softmax is the two-pass softmax regrouped; it omits the reference's
 // -80 floor on shifted logits, which only touches weights below e^-80
 // relative to the row maximum (invisible in fp32 next to the maximum's 1).
+#include <type_traits>
+
 #include "common.h"
 #include "q35mix_internal.h"
 
@@ -44,21 +46,24 @@ namespace {
 constexpr int NT = 256;
 constexpr int SUB = 64;   // positions per sub-chunk
 
-template <int NSUB>
+template <int NSUB, int HPW>
 __global__ __launch_bounds__(NT, 2) void attn_decode_partial(
     const float* __restrict__ q_gate, const float* __restrict__ knew,
     const float* __restrict__ vnew, const float* __restrict__ q_norm,
     const float* __restrict__ k_norm, float* __restrict__ k_cache, float* __restrict__ v_cache,
     const float* __restrict__ rope_cos, const float* __restrict__ rope_sin,
-    float* __restrict__ part_o, float* __restrict__ part_ml, int nkv, int cap, int nchunks,
+    float* __restrict__ part_o, float* __restrict__ part_ml, int nkv, int ng, int cap, int nchunks,
     float eps, SeqBatch sb) {
-    const int c = blockIdx.x, kvh = blockIdx.y, i = blockIdx.z;
+    constexpr int QPW = (HPW + 3) / 4;       // q heads of the group per wave in per-head phases
+    const int c = blockIdx.x, y = blockIdx.y, i = blockIdx.z;
+    const int kvh = y / ng;                  // head group y: q heads HPW y .. HPW y + HPW - 1
     const int pos = sb.pos[i];               // cached rows [0, pos); the new row is pos
     const bool has_rows = c * SUB < pos;     // uniform
     const bool owner = c == 0;               // holds the new row
+    const bool writer = owner && y % ng == 0;   // one group per kv head writes it to the cache
     if (!has_rows && !owner) return;
     const int last = pos - 1;                // last cached row (read only when has_rows)
-    const int nh = nkv * kGqaGroup;
+    const int nh = nkv * ng * HPW;
     const int kv_dim = nkv * kHd;
     // Cache of one (sequence, kv head): [cap][256], head-major.
     const size_t seq_off = ((size_t)sb.seq[i] * nkv + kvh) * cap * kHd;
@@ -66,29 +71,35 @@ __global__ __launch_bounds__(NT, 2) void attn_decode_partial(
     float* V = v_cache + seq_off;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
 
-    __shared__ float4 q_s[kGqaGroup][kHd / 4];
+    __shared__ float4 q_s[HPW][kHd / 4];
     __shared__ float4 knew_s[kHd / 4];
     __shared__ float4 vnew_s[kHd / 4];
     // Scores / weights and the rescale factors, double-buffered by sub-chunk
     // parity so two barriers per sub-chunk suffice.
-    __shared__ float sc[2][kGqaGroup][SUB];
-    __shared__ float al_s[2][kGqaGroup];
-    __shared__ float nr_s[kGqaGroup][2];      // new row: rescale factor, weight
-    __shared__ float ml_s[kGqaGroup][2];
-    __shared__ float4 obuf[4][kGqaGroup][kHd / 4];
+    __shared__ float sc[2][HPW][SUB];
+    __shared__ float al_s[2][HPW];
+    __shared__ float nr_s[HPW][2];           // new row: rescale factor, weight
+    __shared__ float ml_s[HPW][2];
+    __shared__ float4 obuf[4][HPW][kHd / 4];
 
     // Score layout: 16 teams of 16 lanes, team t scores positions t + 16m
     // (m < 4); lane l16 holds dims {4*l16 + 64*j .. +3}, j < 4.
-    // P.V layout: thread holds dims 4*d4..+3 of all 4 heads, positions ps + 4m.
+    // P.V layout: thread holds dims 4*d4..+3 of all HPW heads, positions ps + 4m.
+    // Per-head phases (q preparation, softmax): wave w takes the group's heads
+    // w, w + 4, ... (none when w >= HPW).
     const int team = tid >> 4, l16 = tid & 15;
     const int d4 = tid & 63, ps = tid >> 6;
 
     // Operands of the q / new-row preparation, loaded before the first
-    // sub-chunk's K/V so that their latency hides behind it: wave w prepares
-    // q of head 4 kvh + w; waves 0 and 1 also take the new K and V rows.
-    const int hq = kvh * kGqaGroup + wave;
-    const float4 xq = *reinterpret_cast<const float4*>(
-        q_gate + (size_t)i * 2 * nh * kHd + (size_t)hq * 2 * kHd + 4 * lane);
+    // sub-chunk's K/V so that their latency hides behind it; waves 0 and 1 of
+    // the owner also take the new K and V rows.
+    float4 xq[QPW];
+#pragma unroll
+    for (int k = 0; k < QPW; ++k) {
+        const int hh = min(wave + 4 * k, HPW - 1);
+        xq[k] = *reinterpret_cast<const float4*>(
+            q_gate + (size_t)i * 2 * nh * kHd + (size_t)(HPW * y + hh) * 2 * kHd + 4 * lane);
+    }
     const float4 xn = *reinterpret_cast<const float4*>(
         (wave == 1 ? vnew : knew) + (size_t)i * kv_dim + kvh * kHd + 4 * lane);
     const float4 rc = *reinterpret_cast<const float4*>(rope_cos + (size_t)pos * kRopeHalf + 4 * (lane & 7));
@@ -113,13 +124,13 @@ __global__ __launch_bounds__(NT, 2) void attn_decode_partial(
     }
 
     // One sub-chunk at s0 from kk / vv: scores (q re-read from LDS per head,
-    // so its 64 registers per thread are not held across the K/V loads), the
-    // online softmax (wave h owns head h, lane = position) and P.V.  Score and
-    // weight buffers alternate by sub-chunk parity PAR.
+    // so its registers are not held across the K/V loads), the online
+    // softmax (lane = position) and P.V.  Score and weight buffers alternate
+    // by sub-chunk parity PAR.
 #define Q35_SCORES(PAR)                                                                          \
     {                                                                                            \
-        float a[4][kGqaGroup];                                                                   \
-        _Pragma("unroll") for (int h = 0; h < kGqaGroup; ++h) {                                  \
+        float a[4][HPW];                                                                         \
+        _Pragma("unroll") for (int h = 0; h < HPW; ++h) {                                        \
             float4 qh[4];                                                                        \
             _Pragma("unroll") for (int j = 0; j < 4; ++j) qh[j] = q_s[h][l16 + 16 * j];          \
             _Pragma("unroll") for (int m = 0; m < 4; ++m) {                                      \
@@ -132,32 +143,35 @@ __global__ __launch_bounds__(NT, 2) void attn_decode_partial(
         }                                                                                        \
         if (l16 == 0)                                                                            \
             _Pragma("unroll") for (int m = 0; m < 4; ++m)                                        \
-                _Pragma("unroll") for (int h = 0; h < kGqaGroup; ++h)                            \
+                _Pragma("unroll") for (int h = 0; h < HPW; ++h)                                  \
                     sc[PAR][h][team + 16 * m] = a[m][h];                                         \
     }
 #define Q35_SOFTMAX_PV(PAR)                                                                      \
     {                                                                                            \
         const int np = min(SUB, pos - s0);                                                       \
         lds_barrier();                                                                           \
-        {                                                                                        \
-            const float s = lane < np ? sc[PAR][wave][lane] : -INFINITY;                         \
-            const float mx = fmaxf(m_run, wave_max(s));                                          \
-            const float e = lane < np ? __expf(s - mx) : 0.0f;                                   \
-            const float alpha = __expf(m_run - mx);     /* 0 on the first sub-chunk */           \
-            l_run = l_run * alpha + wave_sum(e);                                                 \
-            m_run = mx;                                                                          \
-            sc[PAR][wave][lane] = e;                                                             \
-            if (lane == 0) al_s[PAR][wave] = alpha;                                              \
+        _Pragma("unroll") for (int k = 0; k < QPW; ++k) {                                        \
+            const int hh = wave + 4 * k;                                                         \
+            if (hh < HPW) {                                                                      \
+                const float s = lane < np ? sc[PAR][hh][lane] : -INFINITY;                       \
+                const float mx = fmaxf(m_run[k], wave_max(s));                                   \
+                const float e = lane < np ? __expf(s - mx) : 0.0f;                               \
+                const float alpha = __expf(m_run[k] - mx);     /* 0 on the first sub-chunk */    \
+                l_run[k] = l_run[k] * alpha + wave_sum(e);                                       \
+                m_run[k] = mx;                                                                   \
+                sc[PAR][hh][lane] = e;                                                           \
+                if (lane == 0) al_s[PAR][hh] = alpha;                                            \
+            }                                                                                    \
         }                                                                                        \
         lds_barrier();                                                                           \
-        _Pragma("unroll") for (int h = 0; h < kGqaGroup; ++h) {                                  \
+        _Pragma("unroll") for (int h = 0; h < HPW; ++h) {                                        \
             const float alpha = al_s[PAR][h];                                                    \
             acc[h].x *= alpha; acc[h].y *= alpha; acc[h].z *= alpha; acc[h].w *= alpha;          \
         }                                                                                        \
         /* masked positions carry weight exactly 0 (their V rows are row last) */               \
         _Pragma("unroll") for (int m = 0; m < 16; ++m) {                                         \
             const int pp = ps + 4 * m;                                                           \
-            _Pragma("unroll") for (int h = 0; h < kGqaGroup; ++h) {                              \
+            _Pragma("unroll") for (int h = 0; h < HPW; ++h) {                                    \
                 const float e = sc[PAR][h][pp];                                                  \
                 acc[h].x += e * vv[m].x;                                                         \
                 acc[h].y += e * vv[m].y;                                                         \
@@ -167,10 +181,15 @@ __global__ __launch_bounds__(NT, 2) void attn_decode_partial(
         }                                                                                        \
     }
 
-    float m_run = -INFINITY, l_run = 0.0f;     // per head (wave = head in the softmax step)
-    float4 acc[kGqaGroup];
+    float m_run[QPW], l_run[QPW];            // the wave's heads
 #pragma unroll
-    for (int h = 0; h < kGqaGroup; ++h) acc[h] = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int k = 0; k < QPW; ++k) {
+        m_run[k] = -INFINITY;
+        l_run[k] = 0.0f;
+    }
+    float4 acc[HPW];
+#pragma unroll
+    for (int h = 0; h < HPW; ++h) acc[h] = make_float4(0.f, 0.f, 0.f, 0.f);
 
     // The first sub-chunk's loads go out before the q preparation.
     int s0 = c * SUB;
@@ -181,17 +200,20 @@ __global__ __launch_bounds__(NT, 2) void attn_decode_partial(
         Q35_LOAD_V(s0)
     }
     // q rows (the attention scale 1/sqrt(256) folded in); the owner also
-    // rotates/norms the new K row and writes K and V into the cache.
-    q_s[wave][lane] = rope_norm_regs(xq, rc, rs, wq, lane, eps, 1.0f / sqrtf((float)kHd));
+    // rotates/norms the new K row, and the writer writes K and V into the cache.
+#pragma unroll
+    for (int k = 0; k < QPW; ++k)
+        if (wave + 4 * k < HPW)
+            q_s[wave + 4 * k][lane] = rope_norm_regs(xq[k], rc, rs, wq, lane, eps, 1.0f / sqrtf((float)kHd));
     if (owner && wave < 2) {
         float4* dst = reinterpret_cast<float4*>((wave == 0 ? K : V) + (size_t)pos * kHd) + lane;
         if (wave == 0) {
             const float4 x = rope_norm_regs(xn, rc, rs, wk, lane, eps, 1.0f);
             knew_s[lane] = x;
-            *dst = x;
+            if (writer) *dst = x;
         } else {
             vnew_s[lane] = xn;
-            *dst = xn;
+            if (writer) *dst = xn;
         }
     }
     lds_barrier();
@@ -221,24 +243,30 @@ __global__ __launch_bounds__(NT, 2) void attn_decode_partial(
 #undef Q35_SOFTMAX_PV
 
     if (owner) {
-        // The new row, from LDS: wave h scores it against q of head h and
-        // folds it into head h's running softmax (m_run = -inf when the
+        // The new row, from LDS: each head's wave scores it against q and
+        // folds it into the head's running softmax (m_run = -inf when the
         // sequence has no cached rows: alpha = 0).
-        const float4 qh = q_s[wave][lane], kn = knew_s[lane];
-        const float s = wave_sum(qh.x * kn.x + qh.y * kn.y + qh.z * kn.z + qh.w * kn.w);
-        const float mx = fmaxf(m_run, s);
-        const float alpha = __expf(m_run - mx);
-        const float e = __expf(s - mx);
-        l_run = l_run * alpha + e;
-        m_run = mx;
-        if (lane == 0) {
-            nr_s[wave][0] = alpha;
-            nr_s[wave][1] = e;
+#pragma unroll
+        for (int k = 0; k < QPW; ++k) {
+            const int hh = wave + 4 * k;
+            if (hh < HPW) {
+                const float4 qh = q_s[hh][lane], kn = knew_s[lane];
+                const float s = wave_sum(qh.x * kn.x + qh.y * kn.y + qh.z * kn.z + qh.w * kn.w);
+                const float mx = fmaxf(m_run[k], s);
+                const float alpha = __expf(m_run[k] - mx);
+                const float e = __expf(s - mx);
+                l_run[k] = l_run[k] * alpha + e;
+                m_run[k] = mx;
+                if (lane == 0) {
+                    nr_s[hh][0] = alpha;
+                    nr_s[hh][1] = e;
+                }
+            }
         }
         lds_barrier();
         const float4 vn = vnew_s[d4];
 #pragma unroll
-        for (int h = 0; h < kGqaGroup; ++h) {
+        for (int h = 0; h < HPW; ++h) {
             const float al = nr_s[h][0];
             const float en = ps == 0 ? nr_s[h][1] : 0.0f;    // added once per dim
             acc[h].x = acc[h].x * al + en * vn.x;
@@ -249,21 +277,22 @@ __global__ __launch_bounds__(NT, 2) void attn_decode_partial(
     }
 
 #pragma unroll
-    for (int h = 0; h < kGqaGroup; ++h) obuf[ps][h][d4] = acc[h];
-    if (lane == 0) {
-        ml_s[wave][0] = m_run;
-        ml_s[wave][1] = l_run;
-    }
+    for (int h = 0; h < HPW; ++h) obuf[ps][h][d4] = acc[h];
+#pragma unroll
+    for (int k = 0; k < QPW; ++k)
+        if (lane == 0 && wave + 4 * k < HPW) {
+            ml_s[wave + 4 * k][0] = m_run[k];
+            ml_s[wave + 4 * k][1] = l_run[k];
+        }
     __syncthreads();
-    {
-        const int h = tid >> 6;
+    for (int h = tid >> 6; h < HPW; h += 4) {
         float4 o = obuf[0][h][d4];
 #pragma unroll
         for (int q = 1; q < 4; ++q) {
             const float4 t = obuf[q][h][d4];
             o.x += t.x; o.y += t.y; o.z += t.z; o.w += t.w;
         }
-        const size_t pidx = (((size_t)i * nkv + kvh) * nchunks + c) * kGqaGroup + h;
+        const size_t pidx = (((size_t)i * nkv * ng + y) * nchunks + c) * HPW + h;
         reinterpret_cast<float4*>(part_o + pidx * kHd)[d4] = o;
         if (d4 == 0) {
             part_ml[2 * pidx] = ml_s[h][0];
@@ -301,14 +330,13 @@ constexpr int MU = 4;                      // chunks per thread per round
 
 __global__ __launch_bounds__(MT) void attn_decode_merge(
     const float* __restrict__ part_o, const float* __restrict__ part_ml,
-    const float* __restrict__ q_gate, float* __restrict__ out, int nkv, int nchunks, SeqBatch sb) {
+    const float* __restrict__ q_gate, float* __restrict__ out, int nh, int hpw, int nchunks, SeqBatch sb) {
     const int h = blockIdx.x / (kHd / MSLICE), slice = blockIdx.x % (kHd / MSLICE);
     const int i = blockIdx.y, t = threadIdx.x, lane = t & 63, wave = t >> 6;
-    const int nh = nkv * kGqaGroup;
-    const int kvh = h / kGqaGroup, hl = h % kGqaGroup;
+    const int y = h / hpw, hl = h % hpw;     // head group of the partials
     const int pos = sb.pos[i];
     const int nc = max(1, min(nchunks, (pos + SUB - 1) / SUB));   // chunks that ran
-    const size_t base = ((size_t)i * nkv + kvh) * nchunks;
+    const size_t base = ((size_t)i * (nh / hpw) + y) * nchunks;
     __shared__ float4 obuf[4][MD4];
     __shared__ float mbuf[4], lbuf[4];
 
@@ -326,7 +354,7 @@ __global__ __launch_bounds__(MT) void attn_decode_merge(
         float4 oc[MU];
 #pragma unroll
         for (int u = 0; u < MU; ++u) {
-            const size_t pidx = (base + min(c0 + u * MG, nc - 1)) * kGqaGroup + hl;
+            const size_t pidx = (base + min(c0 + u * MG, nc - 1)) * hpw + hl;
             mc[u] = part_ml[2 * pidx];
             lc[u] = part_ml[2 * pidx + 1];
             oc[u] = reinterpret_cast<const float4*>(part_o + pidx * kHd)[col];
@@ -377,14 +405,21 @@ int max_subchunks(const SeqBatch& sb) {
 // Sub-chunks per workgroup: the fewest that keep the grid within one round of
 // resident workgroups (2 per CU), at most 8 (beyond, longer workgroups were
 // not faster, and the partials stay small next to the cache they summarise).
-int pick_nsub(int n, int nkv, int max_subs, int n_cu) {
+int pick_nsub(int n, int groups, int max_subs, int n_cu) {
     const long slots = 2L * n_cu;
     for (int ns = 1; ns < 8; ns <<= 1)
-        if ((long)n * nkv * max(1, (max_subs + ns - 1) / ns) <= slots) return ns;
+        if ((long)n * groups * max(1, (max_subs + ns - 1) / ns) <= slots) return ns;
     return 8;
 }
 
 int nchunks_for(int max_subs, int nsub) { return max(1, (max_subs + nsub - 1) / nsub); }
+
+// q heads per workgroup: the whole group of a kv head up to 8 (1, 2, 4 or 8),
+// groups of 8 beyond (each re-reads the kv head's cache).
+int heads_per_wg(const Dims& d) {
+    const int g = d.nh / d.nkv;
+    return g <= 8 ? g : 8;
+}
 
 }  // namespace
 
@@ -401,42 +436,52 @@ hipError_t attn_decode_scratch_address(float** ptr) {
 
 size_t attn_decode_work_bytes(const q35m_ctx* c, const SeqBatch& sb) {
     const int max_subs = max_subchunks(sb);
-    const int nsub = pick_nsub(sb.n, c->d.nkv, max_subs, c->n_cu);
+    const int groups = c->d.nh / heads_per_wg(c->d);
+    const int nsub = pick_nsub(sb.n, groups, max_subs, c->n_cu);
     const size_t nchunks = nchunks_for(max_subs, nsub);
-    return (size_t)sb.n * c->d.nkv * nchunks * kGqaGroup * (kHd + 2) * sizeof(float);
+    return (size_t)sb.n * c->d.nh * nchunks * (kHd + 2) * sizeof(float);
 }
 
 hipError_t launch_attn_decode(q35m_ctx* c, int layer, const SeqBatch& sb, const float* q_gate,
                               const float* k, const float* v, float* out, float* work) {
     const Dims& d = c->d;
     const AttnLayer& L = c->full[layer];
+    const int hpw = heads_per_wg(d);
+    const int groups = d.nh / hpw, ng = groups / d.nkv;
     const int max_subs = max_subchunks(sb);
-    const int nsub = pick_nsub(sb.n, d.nkv, max_subs, c->n_cu);
+    const int nsub = pick_nsub(sb.n, groups, max_subs, c->n_cu);
     const int nchunks = nchunks_for(max_subs, nsub);
     float* part_o = work;
-    float* part_ml = part_o + (size_t)sb.n * d.nkv * nchunks * kGqaGroup * kHd;
-    const dim3 grid(nchunks, d.nkv, sb.n);
+    float* part_ml = part_o + (size_t)sb.n * d.nh * nchunks * kHd;
+    const dim3 grid(nchunks, groups, sb.n);
     {
         const int kid = nsub == 8 ? K_ATTN_DECODE_PARTIAL8
                       : nsub == 4 ? K_ATTN_DECODE_PARTIAL4
                       : nsub == 2 ? K_ATTN_DECODE_PARTIAL2 : K_ATTN_DECODE_PARTIAL1;
         ProfScope ps_(c, kid);
-#define Q35_PARTIAL(NS)                                                                          \
-    hipExtLaunchKernelGGL(attn_decode_partial<NS>, grid, dim3(NT), 0, c->stream, ps_.a, ps_.b, 0, \
-                          q_gate, k, v, L.q_norm, L.k_norm, L.k_cache, L.v_cache, c->rope_cos,   \
-                          c->rope_sin, part_o, part_ml, d.nkv, c->cap, nchunks, d.eps, sb)
-        if (nsub == 8) Q35_PARTIAL(8);
-        else if (nsub == 4) Q35_PARTIAL(4);
-        else if (nsub == 2) Q35_PARTIAL(2);
-        else Q35_PARTIAL(1);
-#undef Q35_PARTIAL
+        auto go = [&](auto kern) {
+            hipExtLaunchKernelGGL(kern, grid, dim3(NT), 0, c->stream, ps_.a, ps_.b, 0, q_gate, k, v, L.q_norm,
+                                  L.k_norm, L.k_cache, L.v_cache, c->rope_cos, c->rope_sin, part_o, part_ml,
+                                  d.nkv, ng, c->cap, nchunks, d.eps, sb);
+        };
+        auto by_nsub = [&](auto h) {
+            constexpr int H = decltype(h)::value;
+            if (nsub == 8) go(attn_decode_partial<8, H>);
+            else if (nsub == 4) go(attn_decode_partial<4, H>);
+            else if (nsub == 2) go(attn_decode_partial<2, H>);
+            else go(attn_decode_partial<1, H>);
+        };
+        if (hpw == 8) by_nsub(std::integral_constant<int, 8>());
+        else if (hpw == 4) by_nsub(std::integral_constant<int, 4>());
+        else if (hpw == 2) by_nsub(std::integral_constant<int, 2>());
+        else by_nsub(std::integral_constant<int, 1>());
     }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     {
         ProfScope ps_(c, K_ATTN_DECODE_MERGE);
         hipExtLaunchKernelGGL(attn_decode_merge, dim3(d.nh * (kHd / MSLICE), sb.n), dim3(MT), 0, c->stream,
-                              ps_.a, ps_.b, 0, part_o, part_ml, q_gate, out, d.nkv, nchunks, sb);
+                              ps_.a, ps_.b, 0, part_o, part_ml, q_gate, out, d.nh, hpw, nchunks, sb);
     }
     return hipGetLastError();
 }

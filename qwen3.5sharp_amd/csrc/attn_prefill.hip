@@ -10,9 +10,9 @@
 //  1. attn_prefill_prep: rotate/norm q (scale folded in) into the workspace,
 //     rotate/norm K into the cache, copy V into the cache.
 //  2. attn_prefill_flash: causal flash attention on fp32 MFMA, one workgroup
-//     per (kv head, 16-row query block) with its 4 q heads, K/V streamed
-//     through LDS in 32-row tiles, online softmax; the [T][kvLen] score matrix
-//     is never materialised.
+//     per (group of up to 4 q heads sharing a kv head, 16-row query block),
+//     K/V streamed through LDS in 32-row tiles, online softmax; the
+//     [T][kvLen] score matrix is never materialised.
 #include "common.h"
 #include "q35mix_internal.h"
 
@@ -58,8 +58,10 @@ constexpr int KT = 32;          // key rows per tile
 constexpr int LDKV = kHd + 4;   // padded LDS row stride of the K/V tiles
 
 // Causal flash attention on fp32 MFMA (v_mfma_f32_16x16x4f32).  Workgroup =
-// (kv head, 16 query rows); wave w is q head 4*kvh + w, so the 4 q heads of a
-// kv head share every K/V tile staged in LDS.  Per 32-row key tile a wave
+// (head group y, 16 query rows): the group is hg = min(4, q heads per kv
+// head) q heads hg y .. hg y + hg - 1 of one kv head, and wave w is q head
+// hg y + w, so the group's q heads share every K/V tile staged in LDS (with
+// fewer than 4 heads the spare waves repeat the last head and store nothing).  Per 32-row key tile a wave
 // computes S^T = K Q^T (positions x queries), so each lane's D column is one
 // query: the online-softmax max/sum and the rescale of O^T = V^T P^T are
 // per lane, and S^T's D tile feeds P^T = B operand register by register.
@@ -70,19 +72,22 @@ constexpr int LDKV = kHd + 4;   // padded LDS row stride of the K/V tiles
 __global__ __launch_bounds__(256, 2) void attn_prefill_flash(
     const float* __restrict__ qbuf, const float* __restrict__ K, const float* __restrict__ V,
     const float* __restrict__ q_gate, float* __restrict__ out, int start, int T, int nh,
-    int nkv, int cap) {
-    // Work items ranked by cost (query block, heaviest first; kv heads
+    int nkv, int hg, int cap) {
+    // Work items ranked by cost (query block, heaviest first; head groups
     // innermost).  Workgroup L < half takes rank L and workgroup half + m
     // takes rank total-1-m, so the two workgroups the dispatcher places on one
     // CU when the whole grid is resident (L and L + half) carry a heavy and a
     // light query block: causal work is balanced per CU, not per workgroup.
+    const int groups = nh / hg;
     const int nqb = (T + QR - 1) / QR;
-    const int total = nqb * nkv, half = (total + 1) / 2, L = blockIdx.x;
+    const int total = nqb * groups, half = (total + 1) / 2, L = blockIdx.x;
     const int rank = L < half ? L : total - 1 - (L - half);
-    const int qb = nqb - 1 - rank / nkv, kvh = rank % nkv;
+    const int qb = nqb - 1 - rank / groups, y = rank % groups;
+    const int kvh = y * hg / (nh / nkv);
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int g = lane >> 4, c16 = lane & 15;
-    const int h = kvh * kGqaGroup + wave;
+    const bool stores = wave < hg;           // uniform per wave
+    const int h = hg * y + min(wave, hg - 1);
     const int r0 = qb * QR;
     const int blk_len = start + min(T - 1, r0 + QR - 1) + 1;
     const int my_t = min(r0 + c16, T - 1);
@@ -193,7 +198,7 @@ __global__ __launch_bounds__(256, 2) void attn_prefill_flash(
         }
     }
     const int t = r0 + c16;
-    if (t >= T) return;
+    if (t >= T || !stores) return;
     const float inv = 1.0f / l_run;
     const float* grow = q_gate + (size_t)t * 2 * nh * kHd + (size_t)h * 2 * kHd + kHd;
     float* orow = out + ((size_t)t * nh + h) * kHd;
@@ -232,9 +237,11 @@ hipError_t launch_attn_prefill(q35m_ctx* c, int layer, int seq, int start, int T
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     {
+        // Head groups of up to 4 q heads of one kv head.
+        const int g = d.nh / d.nkv, hg = g < 4 ? g : 4;
         ProfScope ps_(c, K_ATTN_PREFILL_FLASH);
-        hipExtLaunchKernelGGL(attn_prefill_flash, dim3((T + QR - 1) / QR * d.nkv), dim3(256), 0,
-                           c->stream, ps_.a, ps_.b, 0, qbuf, K, V, q_gate, out, start, T, d.nh, d.nkv,
+        hipExtLaunchKernelGGL(attn_prefill_flash, dim3((T + QR - 1) / QR * (d.nh / hg)), dim3(256), 0,
+                           c->stream, ps_.a, ps_.b, 0, qbuf, K, V, q_gate, out, start, T, d.nh, d.nkv, hg,
                            c->cap);
     }
     return hipGetLastError();

@@ -276,9 +276,14 @@ int q35m_create(const q35m_config* cfg, int n_seqs, int kv_capacity, q35m_ctx** 
     if (cfg->head_dim != q35::kHd || cfg->rope_dim != q35::kRopeDim)
         return fail(Q35M_ERR_UNSUPPORTED, "attention kernels are built for head_dim %d, rope_dim %d",
                     q35::kHd, q35::kRopeDim);
-    if (cfg->num_kv_heads <= 0 || cfg->num_heads != q35::kGqaGroup * cfg->num_kv_heads)
-        return fail(Q35M_ERR_UNSUPPORTED, "attention kernels are built for %d q heads per kv head",
-                    q35::kGqaGroup);
+    if (cfg->num_kv_heads <= 0 || cfg->num_heads <= 0 || cfg->num_heads % cfg->num_kv_heads != 0)
+        return fail(Q35M_ERR_INVALID, "num_heads must be a positive multiple of num_kv_heads");
+    {
+        const int g = cfg->num_heads / cfg->num_kv_heads;
+        if (!(g == 1 || g == 2 || g == 4 || g % 8 == 0))
+            return fail(Q35M_ERR_UNSUPPORTED,
+                        "attention kernels take 1, 2, 4 or a multiple of 8 q heads per kv head (got %d)", g);
+    }
     if (!(cfg->eps > 0.0f) || !(cfg->rope_base > 0.0f))
         return fail(Q35M_ERR_INVALID, "eps and rope_base must be positive");
     if (!cfg->is_recurrent && cfg->full_attention_interval <= 0)

@@ -19,7 +19,6 @@ constexpr int kConvState = 3;   // conv window length (K - 1)
 constexpr int kHd = 256;        // full-attention head dim
 constexpr int kRopeDim = 64;    // rotated dims
 constexpr int kRopeHalf = 32;
-constexpr int kGqaGroup = 4;    // q heads per kv head
 constexpr int kMaxBatch = 64;   // sequences per mixer launch
 constexpr int kMaxVPerK = 4;    // DeltaNet v-heads per k-head (chunk prep stages their gates)
 
