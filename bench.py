@@ -496,6 +496,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default="", help="comma list of: dn_prefill,dn_decode,attn_decode,"
                                                "attn_prefill,linear_q,stack,peaks")
+    ap.add_argument("--stack-steps", type=int, default=128,
+                    help="decode steps of the mixer-stack workload (the context ends at 32768 rows)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="also run one device-to-device copy of MIB MiB (a plain copy kernel "
                          "of known traffic, to scale FETCH_SIZE/WRITE_SIZE counters)")
@@ -666,11 +668,12 @@ def main():
         log(f"[bench] {name}: {workloads[name]}")
 
     if want("stack"):
-        log("[bench] 32-layer mixer stack, 8 seqs x ctx 32768, 128 decode steps ...")
-        ms, kt, by = bench_stack()
+        ns = args.stack_steps
+        log(f"[bench] 32-layer mixer stack, 8 seqs x ctx 32768, {ns} decode steps ...")
+        ms, kt, by = bench_stack(n_steps=ns)
         workloads["stack_decode_8x32k"] = {
-            "us_per_token": ms * 1e3 / (128 * 8), "ms_per_step": ms / 128,
-            "hbm_frac": by / (ms / 1e3) / HBM_PEAK, "gb_per_step": by / 128 / 1e9,
+            "us_per_token": ms * 1e3 / (ns * 8), "ms_per_step": ms / ns, "steps": ns,
+            "hbm_frac": by / (ms / 1e3) / HBM_PEAK, "gb_per_step": by / ns / 1e9,
             "kernels_us": {k: v[0] * 1e3 for k, v in kt.items()}}
         if not args.no_cpu:
             log("[bench] CPU restatement, 4 steps of the stack ...")
