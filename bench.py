@@ -651,10 +651,11 @@ def main():
             "us": ms * 1e3, "bytes": by, "hbm_frac_call": by / (ms / 1e3) / HBM_PEAK,
             "kernels_us": {k: v[0] * 1e3 for k, v in kt.items()}}
         log(f"[bench] boundary_2048x2560: {workloads['boundary_2048x2560']}")
-    qnames = {4: "q4k", 5: "q5k", 6: "q6k", 14: "iq4xs"}
-    gemv_kernel = {4: "linear_q<4>", 5: "linear_qs<5>", 6: "linear_q<6>", 14: "linear_qs<14>"}
+    qnames = {1: "stq1_0", 2: "q2_0c", 4: "q4k", 5: "q5k", 6: "q6k", 14: "iq4xs"}
+    gemv_kernel = {1: "linear_qt<1>", 2: "linear_qt<2>", 4: "linear_q<4>", 5: "linear_qs<5>",
+                   6: "linear_q<6>", 14: "linear_qs<14>"}
     for qtype, n_in, n_out, copies in ((4, 2560, 8192, 32), (6, 4096, 2560, 40), (5, 2560, 8192, 28),
-                                       (14, 2560, 8192, 40)):
+                                       (14, 2560, 8192, 40), (2, 2560, 8192, 60), (1, 2560, 8192, 90)):
         if not want("linear_q"):
             break
         name = f"linear_{qnames[qtype]}_{n_in}x{n_out}"

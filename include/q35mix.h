@@ -269,14 +269,29 @@ int q35m_linear_q6k(q35m_ctx* ctx, const void* w, const float* x, float* y, int 
  * results are bit-identical to them. */
 int q35m_linear_q5k(q35m_ctx* ctx, const void* w, const float* x, float* y, int n_in, int n_out,
                     int tokens);
+int q35m_linear_iq4xs(q35m_ctx* ctx, const void* w, const float* x, float* y, int n_in, int n_out,
+                      int tokens);
+/* The same for Q2_0C (130 B a block of 512 values; n_in a multiple of 512)
+ * and STQ1_0 (42 B a block of 256) weights: MulMatQ2.Gemv / Gemm
+ * (src/Qwen35Sharp.Kernels/MulMatQ2.cs:19-99) and MulMatSTQ.Gemv / Gemm
+ * (src/Qwen35Sharp.Kernels/MulMatSTQ.cs:19-150), as Qwen35Model.Linear /
+ * DecodeLinear dispatch them (Qwen35Model.Decode.cs:31-36, 65-70).  Each
+ * output is bit-identical to the reference's path for it: the eight-row
+ * panel kernels (Q2Panel.cs, STQPanel.cs; the panels exist for the first
+ * n_out & ~7 rows) or the raw-row dot (Q2_0C.DotAvx2, STQ1_0.DotAvx2) for
+ * the rest; STQ1_0 with tokens > 1 takes the panels for all rows when
+ * tokens % 4 == 0 and n_out % 8 == 0 and the raw dot for all rows
+ * otherwise, as MulMatSTQ.Gemm does. */
+int q35m_linear_q2_0c(q35m_ctx* ctx, const void* w, const float* x, float* y, int n_in, int n_out,
+                      int tokens);
+int q35m_linear_stq1_0(q35m_ctx* ctx, const void* w, const float* x, float* y, int n_in, int n_out,
+                       int tokens);
 /* F32 weights W [n_out][n_in] row-major in device memory (Qwen35Model.F32Gemm,
  * src/Qwen35Sharp.Model/Qwen35Model.Decode.cs:129-140, the reference's Linear
  * and DecodeLinear for F32 tensors): y[t][o] = Ops.DotF32(x[t], W[o])
  * (Ops.cs:418-449), bit-identical to it; any n_in >= 1. */
 int q35m_linear_f32(q35m_ctx* ctx, const float* w, const float* x, float* y, int n_in, int n_out,
                     int tokens);
-int q35m_linear_iq4xs(q35m_ctx* ctx, const void* w, const float* x, float* y, int n_in, int n_out,
-                      int tokens);
 
 /* The layer boundary around a mixer: hidden[t] += delta[t] (fp32 adds,
  * written back; delta NULL: no add), then y[t] = RmsNormZeroCentered(hidden[t],
@@ -314,6 +329,10 @@ int q35m_linear_q5k_prequant(q35m_ctx* ctx, const void* w, const void* q8, float
                              int n_out, int tokens);
 int q35m_linear_iq4xs_prequant(q35m_ctx* ctx, const void* w, const void* q8, float* y, int n_in,
                                int n_out, int tokens);
+int q35m_linear_q2_0c_prequant(q35m_ctx* ctx, const void* w, const void* q8, float* y, int n_in,
+                               int n_out, int tokens);
+int q35m_linear_stq1_0_prequant(q35m_ctx* ctx, const void* w, const void* q8, float* y, int n_in,
+                                int n_out, int tokens);
 
 /* Per-kernel HIP event timers, the device-side counterpart of the
  * reference's Qwen35Model.ProfileEnabled / Ticks* counters

@@ -241,9 +241,10 @@ def attn_prefill(d: Dims, start, T, q_gate, k, v, w: dict, cache_k, cache_v, n_t
 QK = 256
 Q4K_BYTES, Q6K_BYTES, Q8K_BYTES = 144, 210, 292
 Q5K_BYTES, IQ4XS_BYTES = 176, 136
+Q2_0C_BYTES, STQ1_0_BYTES = 130, 42     # Q2_0C blocks hold 512 values
 # Projection type codes of q35o_linear_q (and of the library's linear entry
-# points): 4 = Q4_K, 5 = Q5_K, 6 = Q6_K, 14 = IQ4_XS.
-QT_Q4K, QT_Q5K, QT_Q6K, QT_IQ4XS = 4, 5, 6, 14
+# points): 1 = STQ1_0, 2 = Q2_0C, 4 = Q4_K, 5 = Q5_K, 6 = Q6_K, 14 = IQ4_XS.
+QT_STQ1_0, QT_Q2_0C, QT_Q4K, QT_Q5K, QT_Q6K, QT_IQ4XS = 1, 2, 4, 5, 6, 14
 _U8 = ctypes.POINTER(ctypes.c_uint8)
 
 
@@ -296,22 +297,41 @@ def iq4xs_dot(w, q8, n) -> float:
     return f(w.ctypes.data_as(_U8), q8.ctypes.data_as(_U8), ctypes.c_int(n))
 
 
+def q2_0c_dot(w, q8, n) -> float:
+    """Q2_0C.DotAvx2, the raw-row order (rows outside the eight-row panels)."""
+    f = lib().q35o_q2_0c_dot
+    f.restype = ctypes.c_float
+    w, q8 = _bytes(w), _bytes(q8)
+    return f(w.ctypes.data_as(_U8), q8.ctypes.data_as(_U8), ctypes.c_int(n))
+
+
+def stq1_0_dot(w, q8, n) -> float:
+    """STQ1_0.DotAvx2, the raw-row order (rows outside the eight-row panels)."""
+    f = lib().q35o_stq1_0_dot
+    f.restype = ctypes.c_float
+    w, q8 = _bytes(w), _bytes(q8)
+    return f(w.ctypes.data_as(_U8), q8.ctypes.data_as(_U8), ctypes.c_int(n))
+
+
 def dot(qtype: int, w, q8, n) -> float:
-    return {QT_Q4K: q4k_dot, QT_Q5K: q5k_dot, QT_Q6K: q6k_dot, QT_IQ4XS: iq4xs_dot}[qtype](w, q8, n)
+    return {QT_Q4K: q4k_dot, QT_Q5K: q5k_dot, QT_Q6K: q6k_dot, QT_IQ4XS: iq4xs_dot,
+            QT_Q2_0C: q2_0c_dot, QT_STQ1_0: stq1_0_dot}[qtype](w, q8, n)
 
 
 def dequantize(qtype: int, w, k) -> np.ndarray:
     w = _bytes(w)
     y = np.empty(k, dtype=np.float32)
     fn = {QT_Q4K: lib().q35o_q4k_dequantize_row, QT_Q5K: lib().q35o_q5k_dequantize_row,
-          QT_Q6K: lib().q35o_q6k_dequantize_row, QT_IQ4XS: lib().q35o_iq4xs_dequantize_row}[qtype]
+          QT_Q6K: lib().q35o_q6k_dequantize_row, QT_IQ4XS: lib().q35o_iq4xs_dequantize_row,
+          QT_Q2_0C: lib().q35o_q2_0c_dequantize_row, QT_STQ1_0: lib().q35o_stq1_0_dequantize_row}[qtype]
     fn(w.ctypes.data_as(_U8), _p(y), ctypes.c_int(k))
     return y
 
 
 def linear_q(qtype: int, w, x, n_in, n_out) -> np.ndarray:
-    """y[t] = W x[t] with W given as GGUF rows of qtype 4 (Q4_K), 5 (Q5_K),
-    6 (Q6_K) or 14 (IQ4_XS) blocks."""
+    """y[t] = W x[t] with W given as GGUF rows of qtype 1 (STQ1_0), 2 (Q2_0C),
+    4 (Q4_K), 5 (Q5_K), 6 (Q6_K) or 14 (IQ4_XS) blocks; every row of x is one
+    token of the same call (the STQ1_0 order depends on the token count)."""
     w = _bytes(w)
     x = _f32(x).reshape(-1, n_in)
     y = np.empty((x.shape[0], n_out), dtype=np.float32)

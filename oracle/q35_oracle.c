@@ -242,7 +242,8 @@ void q35o_recurrent_gated_delta_rule(const float* q, const float* k, const float
 /* ------------------------------------------------------------------------- */
 
 /* Sum of squares with the AVX 8-lane FMA accumulator and HorizontalSum,
- * then a scalar tail: Qwen35Ops.cs:275-288 and :318-331. */
+ * then a scalar tail: Qwen35Ops.cs:45-58 (RmsNormZeroCentered) and :88-101
+ * (gated RmsNorm). */
 static float sumsq_avx(const float* x, int dim) {
     float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
     int i = 0;

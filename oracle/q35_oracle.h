@@ -98,6 +98,10 @@ float q35o_q5k_dot(const void* w, const void* q8, int n);
 float q35o_iq4xs_dot(const void* w, const void* q8, int n);
 void q35o_q5k_dequantize_row(const void* w, float* y, int k);
 void q35o_iq4xs_dequantize_row(const void* w, float* y, int k);
+float q35o_q2_0c_dot(const void* w, const void* q8, int n);
+float q35o_stq1_0_dot(const void* w, const void* q8, int n);
+void q35o_q2_0c_dequantize_row(const void* w, float* y, int k);
+void q35o_stq1_0_dequantize_row(const void* w, float* y, int k);
 void q35o_linear_q(int type, const void* w, const float* x, float* y, int n_in, int n_out,
                    int tokens);
 

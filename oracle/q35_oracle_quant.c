@@ -19,11 +19,19 @@
  * short fp32 chain per block in block order with no fused multiply-add, which
  * is restated as written.
  *
+ * Q2_0C and STQ1_0 have two fp32 orders in the reference: the eight-row panel
+ * kernels (Q2Panel.cs, STQPanel.cs), one FMA per 256-value Q8_K block of an
+ * exact integer dot, and the raw-row dot of the remaining rows (Q2_0C.DotAvx2,
+ * STQ1_0.DotAvx2), plain multiplies and adds.  Which rows take which order is
+ * MulMatQ2 / MulMatSTQ's dispatch, restated in q35o_linear_q.
+ *
  * Block formats (src/Qwen35Sharp.Kernels/BlockLayout.cs:32-78), packed:
  *   Q4_K (144 B): u16 d, u16 dmin (fp16), u8 scales[12], u8 qs[128]
  *   Q5_K (176 B): u16 d, u16 dmin (fp16), u8 scales[12], u8 qh[32], u8 qs[128]
  *   Q6_K (210 B): u8 ql[128], u8 qh[64], i8 scales[16], u16 d (fp16)
  *   IQ4_XS (136 B): u16 d (fp16), u16 scales_h, u8 scales_l[4], u8 qs[128]
+ *   Q2_0C (130 B, 512 values): u16 d (fp16), u8 qs[128] (4 codes a byte)
+ *   STQ1_0 (42 B): u8 qs[32] (4-bit slots), u8 sign[8], u16 d (fp16)
  *   Q8_K (292 B): f32 d, i8 qs[256], i16 bsums[16]
  */
 #include "q35_oracle.h"
@@ -59,6 +67,17 @@ typedef struct __attribute__((packed)) {
     uint8_t scales_l[QK / 64];
     uint8_t qs[QK / 2];
 } blk_iq4xs;
+
+typedef struct __attribute__((packed)) {
+    uint16_t d;
+    uint8_t qs[128];
+} blk_q2_0c;
+
+typedef struct __attribute__((packed)) {
+    uint8_t qs[32];
+    uint8_t sign[8];
+    uint16_t d;
+} blk_stq1_0;
 
 typedef struct __attribute__((packed)) {
     float d;
@@ -412,6 +431,147 @@ void q35o_iq4xs_dequantize_row(const void* wx, float* y, int k) {
     }
 }
 
+/* ------------------------------------------------------------------------- */
+/* Q2_0C                                                                     */
+/* ------------------------------------------------------------------------- */
+
+/* Q2_0C.Value (src/Qwen35Sharp.Kernels/Q2_0C.cs:12-13): value j of a block is
+ * 2 * code - 3 with code = (qs[j / 4] >> (2 (j % 4))) & 3. */
+static int q2_value(const blk_q2_0c* x, int j) {
+    return ((x->qs[j / 4] >> ((j & 3) * 2)) & 3) * 2 - 3;
+}
+
+/* Exact integer dot of half h (values 256 h .. 256 h + 255) with a Q8_K block. */
+static int q2_half_dot(const blk_q2_0c* x, int h, const blk_q8k* y) {
+    int s = 0;
+    for (int j = 0; j < QK; j++) s += q2_value(x, QK * h + j) * y->qs[j];
+    return s;
+}
+
+/* Q2_0C.DotAvx2 (Q2_0C.cs:67-79), the raw-row dot: per 512-value block,
+ * sum += d * ((float)s0 * y0.d + (float)s1 * y1.d) with s0, s1 the exact
+ * integer dots of the two halves against their Q8_K blocks (Dot256's int16
+ * lanes hold at most 8 * 768 and never saturate). */
+float q35o_q2_0c_dot(const void* wx, const void* wy, int n) {
+    const blk_q2_0c* x = (const blk_q2_0c*)wx;
+    const blk_q8k* y = (const blk_q8k*)wy;
+    float sum = 0.0f;
+    for (int b = 0; b < n / 512; b++) {
+        const int s0 = q2_half_dot(&x[b], 0, &y[2 * b]);
+        const int s1 = q2_half_dot(&x[b], 1, &y[2 * b + 1]);
+        sum += q35o_half_to_float(x[b].d) * ((float)s0 * y[2 * b].d + (float)s1 * y[2 * b + 1].d);
+    }
+    return sum;
+}
+
+/* Q2Panel.Gemv / Gemm (src/Qwen35Sharp.Kernels/Q2Panel.cs:12-46, 48-176) for
+ * one output of an eight-row panel: per 256-value Q8_K block b, acc =
+ * fma((float)(2 I - 3 S), dw * y[b].d, acc) with I = sum code * q8 (the
+ * codes 0..3, exact in the int16 lanes: at most 64 * 3 * 128 each), S = the
+ * block's bsums total and dw the weight block's scale (the panel holds it as
+ * float, RepackQ2.cs:15).  2 I - 3 S equals the half's signed dot exactly. */
+static float q2_panel_dot(const blk_q2_0c* x, const blk_q8k* y, int n) {
+    float acc = 0.0f;
+    for (int b = 0; b < n / QK; b++) {
+        const blk_q2_0c* xb = &x[b / 2];
+        int dot = 0, sum = 0;
+        for (int j = 0; j < QK; j++)
+            dot += ((xb->qs[(QK * (b & 1) + j) / 4] >> ((j & 3) * 2)) & 3) * y[b].qs[j];
+        for (int g = 0; g < QK / 16; g++) sum += y[b].bsums[g];
+        acc = fmaf((float)(2 * dot - 3 * sum), q35o_half_to_float(xb->d) * y[b].d, acc);
+    }
+    return acc;
+}
+
+/* Q2_0C.DequantizeRow (Q2_0C.cs:15-23). */
+void q35o_q2_0c_dequantize_row(const void* wx, float* y, int k) {
+    const blk_q2_0c* x = (const blk_q2_0c*)wx;
+    for (int b = 0; b < k / 512; b++) {
+        const float d = q35o_half_to_float(x[b].d);
+        for (int j = 0; j < 512; j++) y[512 * b + j] = (float)q2_value(&x[b], j) * d;
+    }
+}
+
+/* ------------------------------------------------------------------------- */
+/* STQ1_0                                                                    */
+/* ------------------------------------------------------------------------- */
+
+/* STQ1_0.Codebook (src/Qwen35Sharp.Kernels/STQ1_0.cs:50-56): the four-lane
+ * ternary pattern of slot s with sign bit g is entry 16 g + s, two bits a lane
+ * (0 = -1, 1 = 0, 2 = +1). */
+static const uint8_t stq_codebook[32] = {
+    0xA9, 0x89, 0x29, 0x09, 0xA6, 0x86, 0x26, 0x06, 0x9A, 0x92, 0x1A, 0x12, 0x6A, 0x62, 0x4A, 0x42,
+    0x01, 0x21, 0x81, 0xA1, 0x04, 0x24, 0x84, 0xA4, 0x10, 0x18, 0x90, 0x98, 0x40, 0x48, 0x60, 0x68,
+};
+
+/* STQ1_0.QPack (STQ1_0.cs:58-63): group g's slot is nibble g % 2 of qs[g / 2],
+ * its sign bit g % 8 of sign[g / 8]. */
+static uint8_t stq_qpack(const blk_stq1_0* x, int g) {
+    const int slot = (x->qs[g >> 1] >> ((g & 1) * 4)) & 0x0F;
+    const int sign = (x->sign[g >> 3] >> (g & 7)) & 1;
+    return stq_codebook[(sign << 4) | slot];
+}
+
+/* Exact encoded dot of one block: sum of the 0/1/2 lane codes times q8, value
+ * index chunk * 64 + gloc + 16 * lane for group 16 chunk + gloc
+ * (STQ1_0.DotChunk16, STQ1_0.cs:146-188; STQ1_0.Code, :68-75). */
+static int stq_encoded_dot(const blk_stq1_0* x, const blk_q8k* y) {
+    int e = 0;
+    for (int g = 0; g < 64; g++) {
+        const uint8_t q = stq_qpack(x, g);
+        const int chunk = g >> 4, gloc = g & 15;
+        for (int lane = 0; lane < 4; lane++)
+            e += ((q >> (2 * lane)) & 3) * y->qs[chunk * 64 + gloc + lane * 16];
+    }
+    return e;
+}
+
+static int q8k_total(const blk_q8k* y) {
+    int s = 0;
+    for (int g = 0; g < QK / 16; g++) s += y->bsums[g];
+    return s;
+}
+
+/* STQ1_0.DotAvx2 (STQ1_0.cs:120-138), the raw-row dot: per block, sum +=
+ * d * y.d * (encoded - activationSum), evaluated left to right ((d * y.d)
+ * times the float of the exact ternary dot).  DotScalar (:98-117) gives the
+ * same value. */
+float q35o_stq1_0_dot(const void* wx, const void* wy, int n) {
+    const blk_stq1_0* x = (const blk_stq1_0*)wx;
+    const blk_q8k* y = (const blk_q8k*)wy;
+    float sum = 0.0f;
+    for (int b = 0; b < n / QK; b++) {
+        const int t = stq_encoded_dot(&x[b], &y[b]) - q8k_total(&y[b]);
+        sum += q35o_half_to_float(x[b].d) * y[b].d * (float)t;
+    }
+    return sum;
+}
+
+/* STQPanel.Gemv / Gemm (src/Qwen35Sharp.Kernels/STQPanel.cs:13-48, 50-191) for
+ * one output of an eight-row panel: per block, acc = fma((float)(encoded -
+ * S), dw * y.d, acc). */
+static float stq_panel_dot(const blk_stq1_0* x, const blk_q8k* y, int n) {
+    float acc = 0.0f;
+    for (int b = 0; b < n / QK; b++) {
+        const int t = stq_encoded_dot(&x[b], &y[b]) - q8k_total(&y[b]);
+        acc = fmaf((float)t, q35o_half_to_float(x[b].d) * y[b].d, acc);
+    }
+    return acc;
+}
+
+/* STQ1_0.DequantizeRow (STQ1_0.cs:77-94). */
+void q35o_stq1_0_dequantize_row(const void* wx, float* y, int k) {
+    const blk_stq1_0* x = (const blk_stq1_0*)wx;
+    for (int b = 0; b < k / QK; b++) {
+        const float d = q35o_half_to_float(x[b].d);
+        for (int g = 0; g < 64; g++) {
+            const uint8_t q = stq_qpack(&x[b], g);
+            for (int lane = 0; lane < 4; lane++)
+                y[QK * b + (g >> 4) * 64 + (g & 15) + lane * 16] = (float)(((q >> (2 * lane)) & 3) - 1) * d;
+        }
+    }
+}
+
 /* GemmQ4K.GemmAvx2Tile (src/Qwen35Sharp.Kernels/GemmQ4K.Avx2.cs:39-207), the
  * reference's Q4_K path for more than one token (MulMatQ4K.Gemm,
  * MulMatQ4K.cs:45-127, over the x8 panels and the BlockQ4Kx8Meta sidecar of
@@ -447,24 +607,40 @@ static float q4k_panel_dot(const blk_q4k* x, const blk_q8k* y, int n) {
     return acc - mn;
 }
 
-/* Qwen35Model.Linear for Q4_K / Q5_K / Q6_K / IQ4_XS weights: MulMatQ4K.Gemv
- * / Gemm (src/Qwen35Sharp.Kernels/MulMatQ4K.cs:12-127), Q6K.Gemv / Gemm
- * (src/Qwen35Sharp.Kernels/Q6K.cs:301-413), Q5K.Gemv / Gemm (Q5K.cs:97-117)
- * and IQ4XS.Gemv / Gemm (IQ4XS.cs:75-104): each token row is quantized to
- * Q8_K, then every output is one dot product (the panel order above for Q4_K
- * with several tokens; Q5_K and IQ4_XS run their GEMV per token).  (Q6K.Gemm's
- * four-token DotAvx2x4 gives the same value per token as DotAvx2: the same
- * integer lanes and the same fma per block.)  type 4 = Q4_K, 5 = Q5_K,
- * 6 = Q6_K, 14 = IQ4_XS. */
+/* Qwen35Model.Linear for quantized weights (Qwen35Model.Decode.cs:22-51):
+ * MulMatQ4K.Gemv / Gemm (src/Qwen35Sharp.Kernels/MulMatQ4K.cs:12-127),
+ * Q6K.Gemv / Gemm (src/Qwen35Sharp.Kernels/Q6K.cs:301-413), Q5K.Gemv / Gemm
+ * (Q5K.cs:97-117), IQ4XS.Gemv / Gemm (IQ4XS.cs:75-104), MulMatQ2.Gemv / Gemm
+ * (MulMatQ2.cs:19-99) and MulMatSTQ.Gemv / Gemm (MulMatSTQ.cs:19-150): each
+ * token row is quantized to Q8_K, then every output is one dot product in the
+ * order of the path that computes it (panel orders above for the rows listed
+ * below; Q5_K and IQ4_XS run their GEMV per token).  (Q6K.Gemm's four-token
+ * DotAvx2x4 gives the same value per token as DotAvx2: the same integer lanes
+ * and the same fma per block; Quantize4x8 gives the same values as
+ * Q8K.QuantizeRow.)  type 1 = STQ1_0, 2 = Q2_0C (n_in a multiple of 512),
+ * 4 = Q4_K, 5 = Q5_K, 6 = Q6_K, 14 = IQ4_XS. */
 void q35o_linear_q(int type, const void* w, const float* x, float* y, int n_in, int n_out,
                    int tokens) {
     const int nb = n_in / QK;
     const size_t bsz = type == 4 ? sizeof(blk_q4k) : type == 5 ? sizeof(blk_q5k)
-                     : type == 6 ? sizeof(blk_q6k) : sizeof(blk_iq4xs);
-    const size_t wrow = (size_t)nb * bsz;
-    /* Q4_K with more than one token: the panel GEMM for the first n_out & ~7
-     * outputs (MulMatQ4K.cs:104-123 sends the rest through VecDotQ4K.Dot). */
-    const int panel_rows = (type == 4 && tokens > 1) ? (n_out & ~7) : 0;
+                     : type == 6 ? sizeof(blk_q6k) : type == 14 ? sizeof(blk_iq4xs)
+                     : type == 1 ? sizeof(blk_stq1_0) : sizeof(blk_q2_0c);
+    const size_t wrow = type == 2 ? (size_t)(n_in / 512) * bsz : (size_t)nb * bsz;
+    /* Rows in a panel order:
+     * - Q4_K with more than one token: the panel GEMM for the first n_out & ~7
+     *   outputs (MulMatQ4K.cs:104-123 sends the rest through VecDotQ4K.Dot);
+     * - Q2_0C: the panels (built for the first n_out & ~7 rows when
+     *   n_out >= 8, Qwen35Model.cs:531-539) for any token count, the raw dot
+     *   for the rest (MulMatQ2.cs:25-40, 89-98; padding to four tokens does
+     *   not change a token's values);
+     * - STQ1_0: one token as Q2_0C (MulMatSTQ.cs:25-45); several tokens all
+     *   rows by panel when tokens % 4 == 0 and n_out % 8 == 0, else all rows
+     *   by the raw dot (MulMatSTQ.cs:47-64, 104-150). */
+    int panel_rows = 0;
+    if (type == 4 && tokens > 1) panel_rows = n_out & ~7;
+    if (type == 2) panel_rows = n_out & ~7;
+    if (type == 1)
+        panel_rows = tokens == 1 ? (n_out & ~7) : ((tokens & 3) == 0 && (n_out & 7) == 0) ? n_out : 0;
     blk_q8k q8[64];
     if (nb > 64) return;
     for (int t = 0; t < tokens; t++) {
@@ -472,7 +648,11 @@ void q35o_linear_q(int type, const void* w, const float* x, float* y, int n_in, 
         for (int r = 0; r < n_out; r++) {
             const void* wr = (const uint8_t*)w + (size_t)r * wrow;
             float v;
-            if (r < panel_rows)
+            if (type == 2)
+                v = r < panel_rows ? q2_panel_dot((const blk_q2_0c*)wr, q8, n_in) : q35o_q2_0c_dot(wr, q8, n_in);
+            else if (type == 1)
+                v = r < panel_rows ? stq_panel_dot((const blk_stq1_0*)wr, q8, n_in) : q35o_stq1_0_dot(wr, q8, n_in);
+            else if (r < panel_rows)
                 v = q4k_panel_dot((const blk_q4k*)wr, q8, n_in);
             else if (type == 4)
                 v = q35o_q4k_dot(wr, q8, n_in);

@@ -59,12 +59,6 @@ __device__ __forceinline__ float group_sum(float v) {
     return v;
 }
 
-// Device-scope coherent load of a value another workgroup of the same
-// launch published before a release fence (bypasses the non-coherent L1).
-__device__ __forceinline__ float load_coherent(const float* p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
 // Workgroup index remapped so that consecutive logical indices share an XCD:
 // the hardware deals workgroups round-robin over the 8 XCDs (block b runs on
 // XCD b % 8), each with its own L2.  Requires total % 8 == 0; otherwise the

@@ -177,7 +177,8 @@ const char* kernel_name(int id) {
         "attn_decode_partial<2>", "attn_decode_partial<4>",  "attn_decode_partial<8>",
         "attn_decode_merge",      "attn_prefill_prep",       "attn_prefill_flash",
         "q8k_quantize",           "linear_q<4>",             "linear_q<6>",
-        "q4k_gemm", "q6k_gemm", "add_rmsnorm", "linear_qs<5>", "linear_qs<14>", "linear_f32"};
+        "q4k_gemm", "q6k_gemm", "add_rmsnorm", "linear_qs<5>", "linear_qs<14>", "linear_f32", "linear_qt<2>",
+        "linear_qt<1>"};
     return (id >= 0 && id < K_COUNT) ? names[id] : nullptr;
 }
 
@@ -584,6 +585,12 @@ static int check_linear_dims(int n_in, int n_out, int tokens) {
     return Q35M_OK;
 }
 
+static int check_linear_type(int qtype, int n_in) {
+    if (qtype == 2 && n_in % 512)
+        return fail(Q35M_ERR_UNSUPPORTED, "Q2_0C rows need a multiple of 512 inputs (got %d)", n_in);
+    return Q35M_OK;
+}
+
 static int linear_q(q35m_ctx* ctx, int qtype, const void* w, const float* x, float* y, int n_in,
                     int n_out, int tokens) {
     int r = check_ctx(ctx);
@@ -592,6 +599,7 @@ static int linear_q(q35m_ctx* ctx, int qtype, const void* w, const float* x, flo
     if (((uintptr_t)w & 15) || ((uintptr_t)x & 15))
         return fail(Q35M_ERR_INVALID, "weights and input must be 16-byte aligned");
     if ((r = check_linear_dims(n_in, n_out, tokens))) return r;
+    if ((r = check_linear_type(qtype, n_in))) return r;
     HIP_TRY(q35::ensure_work(ctx, q35::linear_q_work_bytes(n_in, tokens)), "workspace");
     HIP_TRY(q35::launch_linear_q(ctx, qtype, w, x, y, n_in, n_out, tokens), "linear_q");
     return Q35M_OK;
@@ -777,6 +785,7 @@ static int linear_q_prequant(q35m_ctx* ctx, int qtype, const void* w, const void
     if (((uintptr_t)w & 15) || ((uintptr_t)q8 & 15))
         return fail(Q35M_ERR_INVALID, "weights and Q8_K buffer must be 16-byte aligned");
     if ((r = check_linear_dims(n_in, n_out, tokens))) return r;
+    if ((r = check_linear_type(qtype, n_in))) return r;
     HIP_TRY(q35::launch_linear_q_prequant(ctx, qtype, w, q8, y, n_in, n_out, tokens), "linear_q");
     return Q35M_OK;
 }
@@ -831,6 +840,26 @@ int q35m_linear_iq4xs_prequant(q35m_ctx* ctx, const void* w, const void* q8, flo
 int q35m_linear_q6k(q35m_ctx* ctx, const void* w, const float* x, float* y, int n_in, int n_out,
                     int tokens) {
     return linear_q(ctx, 6, w, x, y, n_in, n_out, tokens);
+}
+
+int q35m_linear_q2_0c(q35m_ctx* ctx, const void* w, const float* x, float* y, int n_in, int n_out,
+                      int tokens) {
+    return linear_q(ctx, 2, w, x, y, n_in, n_out, tokens);
+}
+
+int q35m_linear_stq1_0(q35m_ctx* ctx, const void* w, const float* x, float* y, int n_in, int n_out,
+                       int tokens) {
+    return linear_q(ctx, 1, w, x, y, n_in, n_out, tokens);
+}
+
+int q35m_linear_q2_0c_prequant(q35m_ctx* ctx, const void* w, const void* q8, float* y, int n_in,
+                               int n_out, int tokens) {
+    return linear_q_prequant(ctx, 2, w, q8, y, n_in, n_out, tokens);
+}
+
+int q35m_linear_stq1_0_prequant(q35m_ctx* ctx, const void* w, const void* q8, float* y, int n_in,
+                                int n_out, int tokens) {
+    return linear_q_prequant(ctx, 1, w, q8, y, n_in, n_out, tokens);
 }
 
 static int state_locate(q35m_ctx* ctx, int layer, int seq, int kind, char** base, size_t* bytes) {

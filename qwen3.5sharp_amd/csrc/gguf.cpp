@@ -11,6 +11,7 @@
 #include <cstdarg>
 #include <cstdint>
 #include <cstdio>
+#include <cctype>
 #include <cstring>
 #include <map>
 #include <string>
@@ -67,6 +68,8 @@ uint64_t type_bytes(int type, uint64_t n) {
         case 14: return n % 256 ? 0 : n / 256 * 210;  // Q6_K
         case 15: return n % 256 ? 0 : n / 256 * 292;  // Q8_K
         case 23: return n % 256 ? 0 : n / 256 * 136;  // IQ4_XS
+        case 40: return n % 512 ? 0 : n / 512 * 130;  // Q2_0C
+        case 43: return n % 256 ? 0 : n / 256 * 42;   // STQ1_0
         default: return 0;
     }
 }
@@ -129,6 +132,22 @@ struct q35m_gguf {
     std::map<std::string, Tensor> tensors;
 };
 
+// GgufFile.CanonicalTensorType (src/Qwen35Sharp.Gguf/GgufFile.cs:171-181):
+// files written before STQ1_0 got its type number (43) store it as raw type
+// 42, which is now plain Q2_0; only a file with general.file_type 41 whose
+// general.name contains "Stride16" (any case) is read as STQ1_0.
+static int canonical_type(const q35m_gguf* g, int raw) {
+    if (raw != 42) return raw;
+    auto ft = g->kv.find("general.file_type");
+    auto nm = g->kv.find("general.name");
+    if (ft == g->kv.end() || nm == g->kv.end() || nm->second.type != STRING) return raw;
+    const int t = ft->second.type;
+    if (t == F32 || t == F64 || t == STRING || t == ARRAY || ft->second.i != 41) return raw;
+    std::string name = nm->second.s;
+    for (char& ch : name) ch = (char)std::tolower((unsigned char)ch);
+    return name.find("stride16") != std::string::npos ? 43 : raw;
+}
+
 static int parse(q35m_gguf* g) {
     Cursor c{static_cast<const unsigned char*>(g->map), g->size};
     if (c.get<uint32_t>() != kMagic || !c.ok) return fail(Q35M_ERR_INVALID, "not a GGUF file (magic)");
@@ -179,7 +198,7 @@ static int parse(q35m_gguf* g) {
             t.dims[d] = c.get<int64_t>();
             if (t.dims[d] < 0) return fail(Q35M_ERR_INVALID, "tensor '%s' dim %d is negative", name.c_str(), d);
         }
-        t.type = c.get<int32_t>();
+        t.type = canonical_type(g, c.get<int32_t>());
         t.offset = c.get<uint64_t>();
         if (!c.ok) return fail(Q35M_ERR_INVALID, "tensor info %llu unreadable", (unsigned long long)i);
         g->tensors[name] = t;

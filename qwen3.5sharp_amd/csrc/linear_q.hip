@@ -1,6 +1,9 @@
 // Quantized projections on the device: y[t] = W x[t] for a weight W stored
-// as GGUF Q4_K or Q6_K rows, the activation quantized to Q8_K per token,
-// as the reference's decode GEMV does.
+// as GGUF Q4_K, Q5_K, Q6_K, IQ4_XS, Q2_0C or STQ1_0 rows, the activation
+// quantized to Q8_K per token, as the reference's decode GEMV does (and F32
+// weights, unquantized, at the end of the file).  The Q4_K / Q6_K notes
+// below are the model for the other formats, whose sections say where they
+// differ.
 //
 // Reference: Qwen35Model.DecodeLinear (src/Qwen35Sharp.Model/
 // Qwen35Model.Decode.cs:56-88) -> MulMatQ4K.Gemv (src/Qwen35Sharp.Kernels/
@@ -552,6 +555,225 @@ __global__ __launch_bounds__(LQ_THREADS) void linear_qs(const unsigned char* __r
 #pragma unroll
                 for (int k = 0; k < NTERM; ++k) sumf += T[b * QS_TLD + k];
             y[(size_t)t * n_out + row0 + lane] = sumf;
+        }
+        __syncthreads();
+    }
+}
+
+// ---------------------------------------------------------------- Q2_0C, STQ1_0
+
+// Ternary-style formats whose weights sit at 2-byte aligned offsets
+// (BlockLayout.cs:77-96):
+//   Q2_0C (130 B, 512 values): f16 d, u8 qs[128], value 2 code - 3, codes
+//     0..3 four a byte (Q2_0C.cs:12-13)
+//   STQ1_0 (42 B, 256 values): u8 qs[32] (4-bit slots), u8 sign[8], f16 d;
+//     group g = 16 chunk + gloc holds the values at chunk * 64 + gloc + 16
+//     lane through a 32-entry four-lane codebook (STQ1_0.cs:50-75)
+// One integer per 256-value Q8_K block (a "unit"): T = the exact signed dot
+// of the unit's values with the block's int8 activations, formed as the
+// reference does (codes 0..3 or 0..2 times q8, minus 3 or 1 times the bsums
+// total).  The fp32 chain per output then follows the reference's order for
+// that row: the eight-row panels (Q2Panel.cs:12-46, STQPanel.cs:13-48), one
+// FMA per unit, acc = fma((float)T, dw * dx, acc); or the raw-row dot of the
+// other rows, Q2_0C.DotAvx2 (Q2_0C.cs:67-79): acc += dw * ((float)T0 * dx0
+// + (float)T1 * dx1) per 512 values, and STQ1_0.DotAvx2 (STQ1_0.cs:120-138):
+// acc += (dw * dx) * (float)T.  Rows below panel_rows take the panel order.
+constexpr int Q2_BYTES = 130, STQ_BYTES = 42;
+
+// Bytes k of the four dwords q[0..3] gathered into dword k (a 4 x 4 byte
+// transpose): Q2_0C's byte c of a qs dword holds values 4c .. 4c + 3, so its
+// bit pair k of every byte meets the activations 16 i + 4c + k.
+__device__ __forceinline__ uint4 byte_transpose(uint4 q) {
+    const uint32_t a = __builtin_amdgcn_perm(q.y, q.x, 0x05010400u), b = __builtin_amdgcn_perm(q.y, q.x, 0x07030602u);
+    const uint32_t c = __builtin_amdgcn_perm(q.w, q.z, 0x05010400u), d = __builtin_amdgcn_perm(q.w, q.z, 0x07030602u);
+    return make_uint4(__builtin_amdgcn_perm(c, a, 0x05040100u), __builtin_amdgcn_perm(c, a, 0x07060302u),
+                      __builtin_amdgcn_perm(d, b, 0x05040100u), __builtin_amdgcn_perm(d, b, 0x07060302u));
+}
+
+// Sum of a Q8_K block's 16 bsums (the workspace form).
+__device__ __forceinline__ int q8k_bsum_total(const uint32_t* __restrict__ q8b) {
+    int s = 0;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const uint32_t p = q8b[Q8K_BS + k];
+        s += (int16_t)(p & 0xffff) + (int16_t)(p >> 16);
+    }
+    return s;
+}
+
+// Q2_0C half block (64 qs bytes at byte offset o of the staged weights) times
+// a Q8_K block whose qs are staged byte-transposed per 16 bytes: 2 I - 3 S.
+__device__ __forceinline__ int q2_unit_dot(const uint32_t* __restrict__ base, int o,
+                                           const uint32_t* __restrict__ q8b) {
+    int dot = 0;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const uint32_t wv = lds_word(base, o + 4 * i);
+        const uint4 r = reinterpret_cast<const uint4*>(q8b + Q8K_QS)[i];
+        dot = __builtin_amdgcn_sdot4((int)(wv & 0x03030303u), (int)r.x, dot, false);
+        dot = __builtin_amdgcn_sdot4((int)((wv >> 2) & 0x03030303u), (int)r.y, dot, false);
+        dot = __builtin_amdgcn_sdot4((int)((wv >> 4) & 0x03030303u), (int)r.z, dot, false);
+        dot = __builtin_amdgcn_sdot4((int)((wv >> 6) & 0x03030303u), (int)r.w, dot, false);
+    }
+    return 2 * dot - 3 * q8k_bsum_total(q8b);
+}
+
+// STQ1_0 block at byte offset o times a Q8_K block: encoded - S.  Four groups
+// at a time: their slots (nibbles of one 16-bit half of qs) spread to bytes,
+// looked up in the two 16-byte codebook halves with byte permutes, the half
+// chosen per byte by the group's sign bit; lane L of the four patterns then
+// meets activations chunk * 64 + 16 L + 4 i .. + 3.
+__device__ __forceinline__ int stq_unit_dot(const uint32_t* __restrict__ base, int o,
+                                            const uint32_t* __restrict__ q8b) {
+    // STQ1_0.Codebook, entries 0-15 (sign 0) and 16-31 (sign 1), 4 a dword
+    constexpr uint32_t L0 = 0x092989A9u, L1 = 0x062686A6u, L2 = 0x121A929Au, L3 = 0x424A626Au;
+    constexpr uint32_t H0 = 0xA1812101u, H1 = 0xA4842404u, H2 = 0x98901810u, H3 = 0x68604840u;
+    uint32_t qs[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) qs[j] = lds_word(base, o + 4 * j);
+    const uint32_t sg[2] = {lds_word(base, o + 32), lds_word(base, o + 36)};
+    const uint32_t* q8 = q8b + Q8K_QS;
+    int enc = 0;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+        const uint32_t s16 = (sg[c >> 1] >> (16 * (c & 1))) & 0xffffu;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const uint32_t h = (qs[2 * c + (i >> 1)] >> (16 * (i & 1))) & 0xffffu;
+            const uint32_t idx = (h & 0xfu) | ((h & 0xf0u) << 4) | ((h & 0xf00u) << 8) | ((h & 0xf000u) << 12);
+            const uint32_t sel = idx & 0x07070707u;
+            const uint32_t hib = ((idx >> 3) & 0x01010101u) * 0xffu;
+            const uint32_t lo = (__builtin_amdgcn_perm(L1, L0, sel) & ~hib) | (__builtin_amdgcn_perm(L3, L2, sel) & hib);
+            const uint32_t hi = (__builtin_amdgcn_perm(H1, H0, sel) & ~hib) | (__builtin_amdgcn_perm(H3, H2, sel) & hib);
+            const uint32_t neg = ((((s16 >> (4 * i)) & 0xfu) * 0x00204081u) & 0x01010101u) * 0xffu;
+            const uint32_t p = (lo & ~neg) | (hi & neg);
+#pragma unroll
+            for (int L = 0; L < 4; ++L)
+                enc = __builtin_amdgcn_sdot4((int)((p >> (2 * L)) & 0x03030303u), (int)q8[16 * c + 4 * L + i], enc,
+                                             false);
+        }
+    }
+    return enc - q8k_bsum_total(q8b);
+}
+
+// One 64-thread workgroup per group of up to 8 whole rows (at most 64 units,
+// one a thread) and tok_per_wg tokens: the rows' contiguous weight bytes are
+// staged in LDS once (as for Q6_K), then per token the Q8_K row is staged,
+// every thread forms its unit's T, and one thread per row runs the chain.
+template <int QT>
+__global__ __launch_bounds__(LQ_THREADS) void linear_qt(const unsigned char* __restrict__ w,
+                                                        const uint32_t* __restrict__ q8,
+                                                        float* __restrict__ y, int n_in, int n_out,
+                                                        int tokens, int rows_per_wg, int tok_per_wg,
+                                                        int panel_rows) {
+#pragma clang fp contract(off)
+    constexpr int UB = QT == 2 ? Q2_BYTES / 2 : STQ_BYTES;   // weight bytes per unit
+    extern __shared__ uint4 smem[];
+    const int nb = n_in / QK, lane = threadIdx.x;
+    const int row0 = blockIdx.x * rows_per_wg;
+    const int nrows = min(rows_per_wg, n_out - row0);
+    const int nunit = nrows * nb;
+    const int t_begin = blockIdx.y * tok_per_wg, t_end = min(tokens, t_begin + tok_per_wg);
+    const size_t row_bytes = (size_t)nb * UB;
+    const int nchunk_max = (rows_per_wg * nb * UB + 31) / 16 + 1;
+    uint4* wsh = smem;
+    uint32_t* q8s = reinterpret_cast<uint32_t*>(smem + nchunk_max);
+    int* tv = reinterpret_cast<int*>(q8s + nb * Q8K_WORDS);
+    const uint32_t* wbase = reinterpret_cast<const uint32_t*>(wsh);
+
+    // The rows' bytes from the 16-byte boundary below their even start; only
+    // the buffer's last chunk can be partial, read with 2-byte loads.
+    const size_t total = (size_t)n_out * row_bytes;
+    const size_t start = (size_t)row0 * row_bytes;
+    const size_t s16 = start & ~(size_t)15;
+    const int shift = (int)(start - s16);
+    const int nchunks = (int)((start + (size_t)nrows * row_bytes - s16 + 15) >> 4);
+    constexpr int MAXC = (LQ_THREADS * UB + 31 + LQ_THREADS * 16 - 1) / (LQ_THREADS * 16) + 1;
+    {
+        uint4 wv[MAXC];
+#pragma unroll
+        for (int c = 0; c < MAXC; ++c) {
+            const int i = lane + LQ_THREADS * c;
+            const size_t off = s16 + 16 * (size_t)i;
+            wv[c] = make_uint4(0u, 0u, 0u, 0u);
+            if (i < nchunks && off + 16 <= total) wv[c] = *reinterpret_cast<const uint4*>(w + off);
+        }
+#pragma unroll
+        for (int c = 0; c < MAXC; ++c) {
+            const int i = lane + LQ_THREADS * c;
+            const size_t off = s16 + 16 * (size_t)i;
+            if (i < nchunks) {
+                if (off + 16 <= total) {
+                    wsh[i] = wv[c];
+                } else {
+                    uint32_t wd[4] = {0u, 0u, 0u, 0u};
+                    for (int hb = 0; hb < 8 && off + 2 * hb < total; ++hb)
+                        wd[hb >> 1] |= (uint32_t)(*reinterpret_cast<const uint16_t*>(w + off + 2 * hb)) << (16 * (hb & 1));
+                    wsh[i] = make_uint4(wd[0], wd[1], wd[2], wd[3]);
+                }
+            }
+        }
+    }
+
+    for (int t = t_begin; t < t_end; ++t) {
+        {
+            const uint4* src = reinterpret_cast<const uint4*>(q8 + (size_t)t * nb * Q8K_WORDS);
+            uint4* dst = reinterpret_cast<uint4*>(q8s);
+            const int n4 = nb * (Q8K_WORDS / 4);
+            for (int i0 = 0; i0 < n4; i0 += 8 * LQ_THREADS) {
+                uint4 qv[8];
+#pragma unroll
+                for (int c = 0; c < 8; ++c) {
+                    qv[c] = make_uint4(0u, 0u, 0u, 0u);
+                    if (i0 + lane + LQ_THREADS * c < n4) qv[c] = src[i0 + lane + LQ_THREADS * c];
+                }
+#pragma unroll
+                for (int c = 0; c < 8; ++c) {
+                    const int i = i0 + lane + LQ_THREADS * c;
+                    if (i < n4) {
+                        const int part = i % (Q8K_WORDS / 4);     // 1..16: qs, 0 and 17..18: d, bsums
+                        dst[i] = (QT == 2 && part >= 1 && part <= 16) ? byte_transpose(qv[c]) : qv[c];
+                    }
+                }
+            }
+        }
+        __syncthreads();
+        if (lane < nunit) {
+            const int r = lane / nb, b = lane % nb;
+            const uint32_t* q8b = q8s + b * Q8K_WORDS;
+            if constexpr (QT == 2)
+                tv[lane] = q2_unit_dot(wbase, shift + (int)(r * row_bytes) + (b >> 1) * Q2_BYTES + 2 + 64 * (b & 1), q8b);
+            else
+                tv[lane] = stq_unit_dot(wbase, shift + (int)(r * row_bytes) + b * STQ_BYTES, q8b);
+        }
+        __syncthreads();
+        if (lane < nrows) {
+            const int row = row0 + lane;
+            const int* T = tv + lane * nb;
+            const int o = shift + (int)(lane * row_bytes);
+            float acc = 0.0f;
+            if (row < panel_rows) {
+                for (int b = 0; b < nb; ++b) {
+                    const int dof = QT == 2 ? o + (b >> 1) * Q2_BYTES : o + b * STQ_BYTES + 40;
+                    const float dw = half_bits_to_float(lds_word(wbase, dof) & 0xffff);
+                    const float dx = __builtin_bit_cast(float, q8s[b * Q8K_WORDS]);
+                    acc = fmaf((float)T[b], dw * dx, acc);
+                }
+            } else if constexpr (QT == 2) {
+                for (int b = 0; b < nb; b += 2) {
+                    const float dw = half_bits_to_float(lds_word(wbase, o + (b >> 1) * Q2_BYTES) & 0xffff);
+                    const float dx0 = __builtin_bit_cast(float, q8s[b * Q8K_WORDS]);
+                    const float dx1 = __builtin_bit_cast(float, q8s[(b + 1) * Q8K_WORDS]);
+                    acc = acc + dw * ((float)T[b] * dx0 + (float)T[b + 1] * dx1);
+                }
+            } else {
+                for (int b = 0; b < nb; ++b) {
+                    const float dw = half_bits_to_float(lds_word(wbase, o + b * STQ_BYTES + 40) & 0xffff);
+                    const float dx = __builtin_bit_cast(float, q8s[b * Q8K_WORDS]);
+                    acc = acc + (dw * dx) * (float)T[b];
+                }
+            }
+            y[(size_t)t * n_out + row] = acc;
         }
         __syncthreads();
     }
@@ -1109,6 +1331,28 @@ hipError_t launch_linear_q_prequant(q35m_ctx* c, int qtype, const void* w, const
     const int nb = n_in / QK;
     const unsigned char* wb = reinterpret_cast<const unsigned char*>(w);
     const uint32_t* qb = reinterpret_cast<const uint32_t*>(q8);
+    if (qtype == 1 || qtype == 2) {
+        // Which rows take the eight-row panel order (MulMatQ2.cs:25-40,
+        // MulMatSTQ.cs:25-64): the first n_out & ~7, except STQ1_0 with
+        // several tokens: all rows when tokens % 4 == 0 and n_out % 8 == 0,
+        // else none.
+        int panel_rows = n_out & ~7;
+        if (qtype == 1 && tokens > 1) panel_rows = ((tokens & 3) == 0 && (n_out & 7) == 0) ? n_out : 0;
+        const int rows_per_wg = min(LQ_THREADS / nb, LQ_MAX_ROWS);
+        const int tok_per_wg = 8;
+        const int ub = qtype == 2 ? Q2_BYTES / 2 : STQ_BYTES;
+        const int nchunk_max = (rows_per_wg * nb * ub + 31) / 16 + 1;
+        const dim3 grid((n_out + rows_per_wg - 1) / rows_per_wg, (tokens + tok_per_wg - 1) / tok_per_wg);
+        const size_t lds = 16 * (size_t)nchunk_max + (size_t)nb * Q8K_WORDS * 4 + (size_t)LQ_THREADS * 4;
+        ProfScope ps_(c, qtype == 2 ? K_Q2_0C_LINEAR : K_STQ1_0_LINEAR);
+        if (qtype == 2)
+            hipExtLaunchKernelGGL(linear_qt<2>, grid, dim3(LQ_THREADS), lds, c->stream, ps_.a, ps_.b, 0, wb, qb, y,
+                                  n_in, n_out, tokens, rows_per_wg, tok_per_wg, panel_rows);
+        else
+            hipExtLaunchKernelGGL(linear_qt<1>, grid, dim3(LQ_THREADS), lds, c->stream, ps_.a, ps_.b, 0, wb, qb, y,
+                                  n_in, n_out, tokens, rows_per_wg, tok_per_wg, panel_rows);
+        return hipGetLastError();
+    }
     if (qtype == 5 || qtype == 14) {
         // Per-token GEMV; up to 8 tokens a workgroup (the weights stay in
         // registers across them), more tokens over the grid's second axis.

@@ -77,6 +77,8 @@ enum KernelId {
     K_Q5K_LINEAR,
     K_IQ4XS_LINEAR,
     K_F32_LINEAR,
+    K_Q2_0C_LINEAR,
+    K_STQ1_0_LINEAR,
     K_COUNT
 };
 const char* kernel_name(int id);

@@ -64,7 +64,8 @@ def lib() -> ctypes.CDLL:
                                                ctypes.POINTER(ctypes.c_size_t)]
         for name in ("q35m_linear_q4k", "q35m_linear_q6k", "q35m_linear_q4k_prequant",
                      "q35m_linear_q6k_prequant", "q35m_linear_q5k", "q35m_linear_iq4xs",
-                     "q35m_linear_q5k_prequant", "q35m_linear_iq4xs_prequant"):
+                     "q35m_linear_q5k_prequant", "q35m_linear_iq4xs_prequant", "q35m_linear_q2_0c",
+                     "q35m_linear_stq1_0", "q35m_linear_q2_0c_prequant", "q35m_linear_stq1_0_prequant"):
             getattr(_lib, name).argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                                             ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
                                             ctypes.c_int]
@@ -366,7 +367,7 @@ class Context:
         check(lib().q35m_add_rmsnorm(ctypes.c_void_p(self.handle), ctypes.c_void_p(hidden.ptr), ptr(delta),
                                      ptr(w), ptr(y), ptr(q8), dim, tokens, eps))
 
-    _LINEAR = {4: "q4k", 5: "q5k", 6: "q6k", 14: "iq4xs"}
+    _LINEAR = {1: "stq1_0", 2: "q2_0c", 4: "q4k", 5: "q5k", 6: "q6k", 14: "iq4xs"}
 
     def linear_q_prequant(self, qtype: int, w, q8, y, n_in, n_out, tokens) -> None:
         fn = getattr(lib(), f"q35m_linear_{self._LINEAR[qtype]}_prequant")
@@ -374,8 +375,8 @@ class Context:
                  ctypes.c_void_p(y.ptr), n_in, n_out, tokens))
 
     def linear_q(self, qtype: int, w, x, y, n_in, n_out, tokens) -> None:
-        """y[tokens][n_out] = W x for GGUF weight rows of qtype 4 (Q4_K),
-        5 (Q5_K), 6 (Q6_K) or 14 (IQ4_XS)."""
+        """y[tokens][n_out] = W x for GGUF weight rows of qtype 1 (STQ1_0),
+        2 (Q2_0C), 4 (Q4_K), 5 (Q5_K), 6 (Q6_K) or 14 (IQ4_XS)."""
         fn = getattr(lib(), f"q35m_linear_{self._LINEAR[qtype]}")
         check(fn(ctypes.c_void_p(self.handle), ctypes.c_void_p(w.ptr), ctypes.c_void_p(x.ptr),
                  ctypes.c_void_p(y.ptr), n_in, n_out, tokens))

@@ -129,15 +129,17 @@ def kv_prefill(n_pos: int, kv_dim: int, salt: int = 0) -> tuple:
     return k, v
 
 
-QBLOCK_BYTES = {4: 144, 5: 176, 6: 210, 14: 136}
+QBLOCK_BYTES = {1: 42, 2: 130, 4: 144, 5: 176, 6: 210, 14: 136}
+QBLOCK_VALUES = {1: 256, 2: 512, 4: 256, 5: 256, 6: 256, 14: 256}
 
 
 def quant_weights(qtype: int, n_out: int, n_in: int, salt: int = 0) -> np.ndarray:
-    """GGUF Q4_K (qtype 4), Q5_K (5), Q6_K (6) or IQ4_XS (14) rows
-    [n_out][n_in/256 blocks] as bytes: every quant byte uniform, the fp16
-    block scales in [0.004, 0.02] (finite, the size trained weights have; for
-    IQ4_XS a twentieth of that, its sub-block scales reaching 31)."""
-    nblk = n_out * (n_in // 256)
+    """GGUF STQ1_0 (qtype 1), Q2_0C (2), Q4_K (4), Q5_K (5), Q6_K (6) or
+    IQ4_XS (14) rows [n_out][n_in / block values] as bytes: every quant byte
+    uniform, the fp16 block scales in [0.004, 0.02] (finite, the size trained
+    weights have; for IQ4_XS a twentieth of that, its sub-block scales
+    reaching 31)."""
+    nblk = n_out * (n_in // QBLOCK_VALUES[qtype])
     nb = QBLOCK_BYTES[qtype]
     raw = splitmix64(SEED_BASE + 300 + 10 * qtype + salt, (nblk * nb + 7) // 8)
     b = raw.view(np.uint8)[:nblk * nb].reshape(nblk, nb).copy()
@@ -148,6 +150,10 @@ def quant_weights(qtype: int, n_out: int, n_in: int, salt: int = 0) -> np.ndarra
             .view(np.uint8).reshape(-1, 2)
     elif qtype == 14:
         b[:, 0:2] = (d * np.float16(0.05)).view(np.uint8).reshape(-1, 2)
+    elif qtype == 2:
+        b[:, 0:2] = d.view(np.uint8).reshape(-1, 2)
+    elif qtype == 1:
+        b[:, 40:42] = d.view(np.uint8).reshape(-1, 2)
     else:
         b[:, 208:210] = d.view(np.uint8).reshape(-1, 2)
     return b.ravel()

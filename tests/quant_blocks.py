@@ -1,12 +1,15 @@
-"""numpy helpers for the GGUF Q4_K / Q5_K / Q6_K / IQ4_XS / Q8_K block formats
-used by the quantized-projection tests: random blocks, independent decoders
-and packers.  Type codes: 4 = Q4_K, 5 = Q5_K, 6 = Q6_K, 14 = IQ4_XS.
+"""numpy helpers for the GGUF Q4_K / Q5_K / Q6_K / IQ4_XS / Q2_0C / STQ1_0 /
+Q8_K block formats used by the quantized-projection tests: random blocks,
+independent decoders and packers.  Type codes: 1 = STQ1_0, 2 = Q2_0C,
+4 = Q4_K, 5 = Q5_K, 6 = Q6_K, 14 = IQ4_XS.
 
-Layouts (src/Qwen35Sharp.Kernels/BlockLayout.cs:32-78 of the reference):
+Layouts (src/Qwen35Sharp.Kernels/BlockLayout.cs:32-101 of the reference):
   Q4_K (144 B): f16 d, f16 dmin, u8 scales[12], u8 qs[128]
   Q5_K (176 B): f16 d, f16 dmin, u8 scales[12], u8 qh[32], u8 qs[128]
   Q6_K (210 B): u8 ql[128], u8 qh[64], i8 scales[16], f16 d
   IQ4_XS (136 B): f16 d, u16 scales_h, u8 scales_l[4], u8 qs[128]
+  Q2_0C (130 B, 512 values): f16 d, u8 qs[128] (value 2 code - 3, 4 a byte)
+  STQ1_0 (42 B): u8 qs[32] (4-bit codebook slots), u8 sign[8], f16 d
   Q8_K (292 B): f32 d, i8 qs[256], i16 bsums[16]
 """
 from __future__ import annotations
@@ -14,7 +17,17 @@ from __future__ import annotations
 import numpy as np
 
 QK = 256
-BYTES = {4: 144, 5: 176, 6: 210, 14: 136}
+BYTES = {1: 42, 2: 130, 4: 144, 5: 176, 6: 210, 14: 136}
+VALUES = {1: 256, 2: 512, 4: 256, 5: 256, 6: 256, 14: 256}     # values per block
+# STQ1_0's four-lane patterns, entry 16 sign + slot, two bits a lane
+# (0 = -1, 1 = 0, 2 = +1): the format's table (STQ1_0.cs:50-56).
+STQ_CODEBOOK = np.array([0xA9, 0x89, 0x29, 0x09, 0xA6, 0x86, 0x26, 0x06, 0x9A, 0x92, 0x1A, 0x12,
+                         0x6A, 0x62, 0x4A, 0x42, 0x01, 0x21, 0x81, 0xA1, 0x04, 0x24, 0x84, 0xA4,
+                         0x10, 0x18, 0x90, 0x98, 0x40, 0x48, 0x60, 0x68], dtype=np.uint8)
+
+
+def nblocks(qtype, n_values):
+    return n_values // VALUES[qtype]
 # The IQ4_XS grid (llama.cpp kvalues_iq4nl), as the GGUF format defines it.
 IQ4_GRID = np.array([-127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113], dtype=np.int64)
 
@@ -43,6 +56,10 @@ def random_blocks(rng, qtype, nblocks, dscale=0.02):
         b[:, 2:4] = dm.view(np.uint8).reshape(-1, 2)
     elif qtype == 14:
         b[:, 0:2] = (d * np.float16(0.05)).view(np.uint8).reshape(-1, 2)   # dl = d (ls - 32), ls < 64
+    elif qtype == 2:
+        b[:, 0:2] = d.view(np.uint8).reshape(-1, 2)
+    elif qtype == 1:
+        b[:, 40:42] = d.view(np.uint8).reshape(-1, 2)
     else:
         b[:, 208:210] = d.view(np.uint8).reshape(-1, 2)
     return b.ravel()
@@ -85,10 +102,34 @@ def pack_q6k_values(vals):
     return np.concatenate([ql, qh])
 
 
+def stq_values(blk):
+    """The 256 ternary values of one STQ1_0 block: group g = 16 chunk + gloc
+    (slot: nibble g % 2 of qs[g / 2]; sign: bit g % 8 of sign[g / 8]) holds
+    the values at chunk * 64 + gloc + 16 lane, lane = 0..3."""
+    qs, sg = blk[0:32], blk[32:40]
+    slots = np.stack([qs & 15, qs >> 4], axis=1).ravel().astype(np.int64)          # [64]
+    signs = np.unpackbits(sg, bitorder="little").astype(np.int64)                   # [64]
+    pat = STQ_CODEBOOK[16 * signs + slots].astype(np.int64)
+    lanes = np.stack([(pat >> (2 * l)) & 3 for l in range(4)], axis=1) - 1          # [64 groups][4 lanes]
+    return lanes.reshape(4, 16, 4).transpose(0, 2, 1).reshape(256)                  # [chunk][lane][gloc]
+
+
+def q2_values(blk):
+    """The 512 values 2 code - 3 of one Q2_0C block (4 codes a byte, low first)."""
+    qs = blk[2:130].astype(np.int64)
+    codes = np.stack([(qs >> (2 * k)) & 3 for k in range(4)], axis=1).ravel()
+    return 2 * codes - 3
+
+
 def _dequant(qtype, w, dtype):
     b = np.asarray(w, dtype=np.uint8).reshape(-1, BYTES[qtype])
-    out = np.empty((b.shape[0], QK), dtype=dtype)
+    out = np.empty((b.shape[0], VALUES[qtype]), dtype=dtype)
     for i, blk in enumerate(b):
+        if qtype in (1, 2):
+            d = dtype(blk[40:42].copy().view(np.float16)[0] if qtype == 1 else blk[0:2].copy().view(np.float16)[0])
+            vals = stq_values(blk) if qtype == 1 else q2_values(blk)
+            out[i] = vals.astype(dtype) * d
+            continue
         if qtype == 5:
             # llama.cpp dequantize_row_q5_K: 64-value groups j, scale/min pair
             # 2j (low nibbles, qh bit 2j) and 2j + 1 (high nibbles, qh bit 2j + 1)

@@ -76,3 +76,25 @@ def test_tensor_extent_checks(tmp_path):
             g.tensor(name)
         assert e.value.code == q35mix.ERR_INVALID, name
     g.close()
+
+
+def test_legacy_stride16_type42_is_stq1_0(tmp_path):
+    """GgufTypeTests.LegacyStride16Type42IsNormalizedWithoutBreakingQ2
+    (tests/Qwen35Sharp.Tests/GgufTypeTests.cs:8-29): raw type 42 in a file
+    with general.file_type 41 named "... Stride16" reads as STQ1_0 (43, sized
+    at 42 bytes a 256-value block); in a plain file it stays 42 (Q2_0)."""
+    for name, want in (("Hy-MT2 1.25Bit Stride16", 43), ("plain Q2 model", 42), ("x stride16 y", 43)):
+        p = tmp_path / "t.gguf"
+        gw.write(p, [("general.name", gw.STRING, name), ("general.file_type", gw.I32, 41)],
+                 [("x", 42, (256,), bytes(range(64)))])
+        g = q35mix.Gguf(p)
+        t, dims, raw = g.tensor("x")
+        assert t == want and dims == (256,), name
+        if want == 43:
+            assert raw == bytes(range(42))
+        g.close()
+    gw.write(p, [("general.name", gw.STRING, "Stride16"), ("general.file_type", gw.I32, 40)],
+             [("x", 42, (256,), bytes(64))])
+    g = q35mix.Gguf(p)
+    assert g.tensor("x")[0] == 42
+    g.close()

@@ -1,8 +1,10 @@
-"""Quantized projections (q35m_linear_q4k / _q5k / _q6k / _iq4xs) through the C
-ABI against the oracle: bit-exact (the kernels keep the reference's integer
-lanes and fp32 accumulation order: the AVX2 GEMV for one token and for Q6_K,
-the panel GEMM for Q4_K with several tokens plus the GEMV for its last
-n_out % 8 outputs, the scalar per-token dot of Q5_K and IQ4_XS), at the
+"""Quantized projections (q35m_linear_q4k / _q5k / _q6k / _iq4xs / _q2_0c /
+_stq1_0) through the C ABI against the oracle: bit-exact (the kernels keep the
+reference's integer lanes and fp32 accumulation order: the AVX2 GEMV for one
+token and for Q6_K, the panel GEMM for Q4_K with several tokens plus the GEMV
+for its last n_out % 8 outputs, the scalar per-token dot of Q5_K and IQ4_XS,
+the eight-row panel and raw-row orders of Q2_0C and STQ1_0 split as the
+reference splits them, by row and, for STQ1_0, by token count), at the
 projection shapes of the 4B mixers
 (hidden 2560: qkv 8192, gate 4096, beta/alpha 32, ssm_out and attn_output
 4096 -> 2560, attn k/v 1024), ragged small shapes, several tokens, zero and
@@ -47,18 +49,21 @@ def run(ctx, qtype, w, x, n_in, n_out):
 
 SHAPES = [(2560, 8192, 1), (2560, 4096, 1), (2560, 32, 1), (4096, 2560, 1), (2560, 1024, 1),
           (256, 7, 1), (512, 33, 5), (2560, 1024, 3), (16384, 19, 2), (2560, 520, 70),
-          (4096, 136, 130), (512, 40, 16), (1024, 72, 15)]
+          (4096, 136, 130), (512, 40, 16), (1024, 72, 15), (2560, 64, 4), (1024, 13, 4), (1536, 24, 8)]
 
 
-NAMES = {4: "Q4_K", 5: "Q5_K", 6: "Q6_K", 14: "IQ4_XS"}
+NAMES = {1: "STQ1_0", 2: "Q2_0C", 4: "Q4_K", 5: "Q5_K", 6: "Q6_K", 14: "IQ4_XS"}
+TYPES = [1, 2, 4, 5, 6, 14]
 
 
-@pytest.mark.parametrize("qtype", [4, 5, 6, 14])
+@pytest.mark.parametrize("qtype", TYPES)
 @pytest.mark.parametrize("n_in,n_out,tokens", SHAPES)
 def test_linear_q_bit_exact(ctx, qtype, n_in, n_out, tokens):
+    if n_in % qb.VALUES[qtype]:
+        n_in += qb.VALUES[qtype] - n_in % qb.VALUES[qtype]
     say(f"linear_q {NAMES[qtype]} n_in={n_in} n_out={n_out} tokens={tokens}")
     rng = np.random.default_rng(1000 * qtype + n_in + n_out + tokens)
-    w = qb.random_blocks(rng, qtype, n_out * n_in // 256)
+    w = qb.random_blocks(rng, qtype, qb.nblocks(qtype, n_out * n_in))
     x = rng.standard_normal((tokens, n_in)).astype(np.float32)
     got = run(ctx, qtype, w, x, n_in, n_out)
     want = oracle.linear_q(qtype, w, x, n_in, n_out)
@@ -67,15 +72,15 @@ def test_linear_q_bit_exact(ctx, qtype, n_in, n_out, tokens):
     assert bad.size == 0
 
 
-@pytest.mark.parametrize("qtype", [4, 5, 6, 14])
+@pytest.mark.parametrize("qtype", TYPES)
 def test_linear_q_activation_edges(ctx, qtype):
     """Zero blocks (scale 0), a first extremum that is positive (negative
     scale) or repeated with both signs, ties at .5 after scaling, huge and tiny
     magnitudes, and an fp16 subnormal weight scale."""
     n_in, n_out = 2048, 40
     rng = np.random.default_rng(77 + qtype)
-    w = qb.random_blocks(rng, qtype, n_out * n_in // 256)
-    d_off = 208 if qtype == 6 else 0
+    w = qb.random_blocks(rng, qtype, qb.nblocks(qtype, n_out * n_in))
+    d_off = {6: 208, 1: 40}.get(qtype, 0)
     w.reshape(-1, qb.BYTES[qtype])[3, d_off:d_off + 2] = np.frombuffer(np.float16(3e-6).tobytes(), np.uint8)
     x = rng.standard_normal((2, n_in)).astype(np.float32)
     x[0, 0:256] = 0.0
@@ -103,6 +108,9 @@ def test_linear_q_rejects_bad_arguments(ctx):
     assert L.q35m_linear_q6k(h, dw.ptr, dx.ptr, dy.ptr, 512, 0, 1) == q35mix.ERR_INVALID
     assert L.q35m_linear_q6k(h, dw.ptr, dx.ptr, dy.ptr, 512, 2, 0) == q35mix.ERR_INVALID
     assert L.q35m_linear_q6k(h, None, dx.ptr, dy.ptr, 512, 2, 1) == q35mix.ERR_INVALID
+    assert L.q35m_linear_q2_0c(h, dw.ptr, dx.ptr, dy.ptr, 256, 2, 1) == q35mix.ERR_UNSUPPORTED
+    assert L.q35m_linear_q2_0c_prequant(h, dw.ptr, dx.ptr, dy.ptr, 768, 2, 1) == q35mix.ERR_UNSUPPORTED
+    assert L.q35m_linear_stq1_0(h, dw.ptr + 2, dx.ptr, dy.ptr, 512, 2, 1) == q35mix.ERR_INVALID
     for a in (dw, dx, dy):
         a.free()
 
@@ -116,8 +124,8 @@ def test_prequant_matches_one_shot(ctx):
     x = rng.standard_normal((2, n_in)).astype(np.float32)
     dx = ctx.array((2, n_in), x)
     q8 = ctx.quantize_q8k(dx, n_in, 2)
-    for qtype, n_out in ((4, 8192), (4, 1024), (6, 1024), (5, 1024), (14, 32)):
-        w = qb.random_blocks(rng, qtype, n_out * n_in // 256)
+    for qtype, n_out in ((4, 8192), (4, 1024), (6, 1024), (5, 1024), (14, 32), (2, 1024), (1, 8192), (1, 13)):
+        w = qb.random_blocks(rng, qtype, qb.nblocks(qtype, n_out * n_in))
         dw = ctx.bytes_array(w)
         dy = ctx.array((2, n_out))
         ctx.linear_q_prequant(qtype, dw, q8, dy, n_in, n_out, 2)

@@ -1,15 +1,21 @@
 """Pins the oracle's quantized-projection restatement (oracle/q35_oracle_quant.c).
 
-The reference has no tests for Q4_K / Q5_K / Q6_K / Q8_K, so the restatement is
-pinned by what the formats and the mathematics fix (IQ4_XS also by the
-reference's own IQ4XSTests, ported with the same .NET Random draws):
+The reference has no tests for Q4_K / Q5_K / Q6_K / Q2_0C / STQ1_0 / Q8_K, so
+the restatement is pinned by what the formats and the mathematics fix (IQ4_XS
+also by the reference's own IQ4XSTests, ported with the same .NET Random
+draws):
   - fp16 decoding against numpy's float16 for every bit pattern;
   - Q8_K: the first extremum maps to exactly -127, ties round to even, the
     sign of the scale follows the first extremum, bsums are the sums of 16,
     and every value reconstructs within half a step;
-  - Q4_K / Q5_K / Q6_K / IQ4_XS dequantization against independent numpy
-    decoders of the bit layouts (Q4_K / Q5_K scales through the per-index
-    GetScaleMin formula, not the word-mask unpacking the dot products use);
+  - dequantization of every format against independent numpy decoders of
+    the bit layouts (Q4_K / Q5_K scales through the per-index GetScaleMin
+    formula, not the word-mask unpacking the dot products use; STQ1_0 through
+    a reshape of its group / lane order); the STQ1_0 codebook by its
+    invariants (one zero lane per pattern, the sign bit negates, all 32
+    one-zero ternary patterns present);
+  - Q2_0C / STQ1_0 dots exactly equal to the integer dot of the decoded
+    values when every scale is 1, and which rows take the panel order;
   - the integer dot products against fp64 dots of the dequantized weights
     with the dequantized activations (equal in exact arithmetic), and exact
     values on hand-built blocks.
@@ -32,7 +38,7 @@ import oracle  # noqa: E402
 import quant_blocks as qb  # noqa: E402
 from test_oracle import DotNetRandom  # noqa: E402
 
-ALL_TYPES = [4, 5, 6, 14]
+ALL_TYPES = [1, 2, 4, 5, 6, 14]
 
 
 def test_half_to_float_all_patterns():
@@ -83,7 +89,7 @@ def test_q8k_random_against_numpy():
 def test_dequantize_against_numpy_decoder(qtype):
     rng = np.random.default_rng(3 + qtype)
     w = qb.random_blocks(rng, qtype, 24)
-    got = oracle.dequantize(qtype, w, 24 * 256)
+    got = oracle.dequantize(qtype, w, 24 * qb.VALUES[qtype])
     want = qb.dequant(qtype, w)
     assert np.array_equal(got, want)
 
@@ -93,7 +99,7 @@ def test_dot_against_fp64(qtype):
     rng = np.random.default_rng(20 + qtype)
     n = 256 * 16
     for trial in range(8):
-        w = qb.random_blocks(rng, qtype, 16)
+        w = qb.random_blocks(rng, qtype, qb.nblocks(qtype, n))
         x = (rng.standard_normal(n) * (1 + 3 * trial)).astype(np.float32)
         q8 = oracle.q8k_quantize(x)
         d, q, _ = qb.parse_q8k(q8)
@@ -232,7 +238,7 @@ def test_iq4xs_reference_dot():
 def test_linear_q_against_fp64(qtype):
     rng = np.random.default_rng(40 + qtype)
     n_in, n_out, tokens = 512, 96, 3
-    w = qb.random_blocks(rng, qtype, n_out * n_in // 256)
+    w = qb.random_blocks(rng, qtype, qb.nblocks(qtype, n_out * n_in))
     x = rng.standard_normal((tokens, n_in)).astype(np.float32)
     y = oracle.linear_q(qtype, w, x, n_in, n_out)
     wd = qb.dequant_f64(qtype, w).reshape(n_out, n_in)
@@ -269,6 +275,125 @@ def test_q4k_several_tokens_panel_rows_and_gemv_tail():
     q8 = oracle.q8k_quantize(x[0])
     gemv = np.array([oracle.q4k_dot(rows[r], q8, n_in) for r in range(n_out)], np.float32)
     assert np.array_equal(y1[0].view(np.uint32), gemv.view(np.uint32))
+
+
+def test_stq_codebook_invariants():
+    cb = qb.STQ_CODEBOOK.astype(np.int64)
+    lanes = np.stack([(cb >> (2 * l)) & 3 for l in range(4)], axis=1) - 1      # [32][4]
+    assert np.all(np.sum(lanes == 0, axis=1) == 1)                              # one zero lane
+    assert np.all(np.isin(lanes, [-1, 0, 1]))
+    assert np.array_equal(lanes[16:], -lanes[:16])                              # sign bit negates
+    pats = {tuple(r) for r in lanes}
+    want = {tuple(np.insert(np.array(sg), z, 0)) for z in range(4)
+            for sg in np.array(np.meshgrid([-1, 1], [-1, 1], [-1, 1])).T.reshape(-1, 3)}
+    assert pats == want and len(pats) == 32
+    # the oracle's table is the same one: slot s with sign 0 / 1 decodes to lanes[s] / lanes[16 + s]
+    for sign in (0, 1):
+        blk = np.zeros(42, np.uint8)
+        blk[0:32] = np.arange(64, dtype=np.uint8)[0::2] % 16 | ((np.arange(64, dtype=np.uint8)[1::2] % 16) << 4)
+        blk[32:40] = 0xFF * sign
+        blk[40:42] = np.frombuffer(np.float16(1.0).tobytes(), np.uint8)
+        vals = oracle.dequantize(1, blk, 256).astype(np.int64)
+        for g in range(64):
+            chunk, gloc = g >> 4, g & 15
+            got = [vals[chunk * 64 + gloc + 16 * l] for l in range(4)]
+            assert got == list(lanes[16 * sign + g % 16]), (sign, g)
+
+
+def _unit_scale_blocks(rng, qtype, nb):
+    w = qb.random_blocks(rng, qtype, nb).reshape(nb, qb.BYTES[qtype])
+    d_off = 40 if qtype == 1 else 0
+    w[:, d_off:d_off + 2] = np.frombuffer(np.float16(1.0).tobytes(), np.uint8)
+    return w.ravel()
+
+
+@pytest.mark.parametrize("qtype", [1, 2])
+def test_ternary_dots_exact_with_unit_scales(qtype):
+    """Unit weight scales and a Q8_K scale of 1 (every block's first extremum
+    -127): the dot is the exact integer dot of the decoded values with the
+    int8 activations, in both orders (raw dot, and the panel rows of a call)."""
+    rng = np.random.default_rng(70 + qtype)
+    n = 2048
+    for trial in range(6):
+        w = _unit_scale_blocks(rng, qtype, qb.nblocks(qtype, n))
+        x = rng.integers(-127, 128, n).astype(np.float32)
+        x[::256] = -127.0
+        q8 = oracle.q8k_quantize(x)
+        d, q, _ = qb.parse_q8k(q8)
+        assert np.all(d == 1.0) and np.array_equal(q.ravel(), x.astype(np.int8))
+        vals = np.concatenate([qb.stq_values(b) if qtype == 1 else qb.q2_values(b)
+                               for b in w.reshape(-1, qb.BYTES[qtype])])
+        exact = int(np.dot(vals, x.astype(np.int64)))
+        assert oracle.dot(qtype, w, q8, n) == np.float32(exact)
+        y = oracle.linear_q(qtype, np.tile(w, 8), x[None, :], n, 8)       # eight panel rows
+        assert np.all(y == np.float32(exact))
+
+
+def _raw_rows(qtype, w, x, n_in, n_out):
+    rows = w.reshape(n_out, -1)
+    out = np.empty((x.shape[0], n_out), np.float32)
+    for t in range(x.shape[0]):
+        q8 = oracle.q8k_quantize(x[t])
+        out[t] = [oracle.dot(qtype, rows[r], q8, n_in) for r in range(n_out)]
+    return out
+
+
+@pytest.mark.parametrize("qtype,tokens,n_out,panel_rows", [
+    (2, 1, 13, 8), (2, 3, 13, 8), (2, 5, 16, 16), (2, 2, 5, 0),
+    (1, 1, 13, 8), (1, 3, 16, 0), (1, 4, 16, 16), (1, 4, 13, 0), (1, 8, 24, 24), (1, 2, 7, 0)])
+def test_ternary_panel_rows(qtype, tokens, n_out, panel_rows):
+    """Which rows take the eight-row panel order: Q2_0C the first n_out & ~7
+    for any token count; STQ1_0 the same for one token, and for several all
+    rows when tokens % 4 == 0 and n_out % 8 == 0, else none.  The other rows
+    equal the raw-row dot; panel rows differ from it somewhere; all are within
+    fp32 rounding of the exact value."""
+    rng = np.random.default_rng(100 * qtype + 10 * tokens + n_out)
+    n_in = 4096
+    w = qb.random_blocks(rng, qtype, qb.nblocks(qtype, n_out * n_in))
+    x = rng.standard_normal((tokens, n_in)).astype(np.float32)
+    y = oracle.linear_q(qtype, w, x, n_in, n_out)
+    raw = _raw_rows(qtype, w, x, n_in, n_out)
+    assert np.array_equal(y[:, panel_rows:].view(np.uint32), raw[:, panel_rows:].view(np.uint32))
+    if panel_rows:
+        assert np.any(y[:, :panel_rows].view(np.uint32) != raw[:, :panel_rows].view(np.uint32))
+    wd = qb.dequant_f64(qtype, w).reshape(n_out, n_in)
+    for t in range(tokens):
+        d, q, _ = qb.parse_q8k(oracle.q8k_quantize(x[t]))
+        xd = (d[:, None].astype(np.float64) * q).ravel()
+        assert np.all(np.abs(y[t] - wd @ xd) <= 2e-6 * (np.abs(wd) @ np.abs(xd)))
+
+
+def test_q2_dot_hand_built():
+    # d = 0.5; half 0 codes 3 (+3), half 1 codes 1 (-1); activations -127 with
+    # Q8_K scale 1 in block 0 and -63.5 (scale 0.5) in block 1:
+    # 0.5 * (3 * -127 * 256 * 1 + -1 * -127 * 256 * 0.5)
+    blk = np.zeros(130, np.uint8)
+    blk[0:2] = np.frombuffer(np.float16(0.5).tobytes(), np.uint8)
+    blk[2:66] = 0xFF
+    blk[66:130] = 0x55
+    x = np.concatenate([np.full(256, -127.0), np.full(256, -63.5)]).astype(np.float32)
+    q8 = oracle.q8k_quantize(x)
+    want = 0.5 * (3 * -127 * 256 + -1 * -127 * 256 * 0.5)
+    assert oracle.q2_0c_dot(blk, q8, 512) == np.float32(want)
+    assert oracle.linear_q(2, np.tile(blk, 8), x[None, :], 512, 8)[0, 3] == np.float32(want)
+
+
+def test_stq_dot_hand_built():
+    # slot 0, sign 0: lanes (0, +1, +1, +1) -> the first 16 values of every
+    # 64-value chunk are 0, the other 48 are +1; sign 1 negates.  d = 0.25,
+    # activations -127 (Q8_K scale 1): 0.25 * 4 * 48 * -127 per block.
+    blk = np.zeros(42, np.uint8)
+    blk[40:42] = np.frombuffer(np.float16(0.25).tobytes(), np.uint8)
+    q8 = oracle.q8k_quantize(np.full(256, -127.0, np.float32))
+    assert oracle.stq1_0_dot(blk, q8, 256) == np.float32(0.25 * 4 * 48 * -127)
+    blk[32:40] = 0xFF
+    assert oracle.stq1_0_dot(blk, q8, 256) == np.float32(-0.25 * 4 * 48 * -127)
+    # activations nonzero only on the first 16 of each chunk: the zero lane
+    x = np.zeros(256, np.float32)
+    x[0] = -127.0
+    for c in range(4):
+        x[64 * c + 1:64 * c + 16] = 5.0
+    assert oracle.stq1_0_dot(blk, oracle.q8k_quantize(x), 256) == 0.0
 
 
 def test_linear_f32_lane_order():
