@@ -997,6 +997,10 @@ void q4k_gemm(const unsigned char* __restrict__ w, const uint32_t* __restrict__ 
                         const float t = fmaf(__int_as_float(d[r]), scf[rt], negc[rt]);
                         acc[tt][rt][r] = fmaf(t, cs[tt][rt][r], acc[tt][rt][r]);
                     }
+                    // The sub-block's sums are folded here, not all after the
+                    // last sub-block (which would hold 8 tiles of results live).
+                    asm volatile("" : "+v"(acc[tt][rt][0]), "+v"(acc[tt][rt][1]), "+v"(acc[tt][rt][2]),
+                                 "+v"(acc[tt][rt][3]));
                 }
             }
             if (sb == 3 && more) {
@@ -1200,6 +1204,10 @@ __global__ __launch_bounds__(256) void q6k_gemm(const unsigned char* __restrict_
                     const int sumi = (int)((unsigned)hr << 7) + lr;
                     acc[tt][k][r] = fmaf(d[tt][r], (float)sumi, acc[tt][k][r]);
                 }
+                // folded here rather than after the last lane (keeps the
+                // MFMA results of one lane live, not of all eight)
+                asm volatile("" : "+v"(acc[tt][k][0]), "+v"(acc[tt][k][1]), "+v"(acc[tt][k][2]),
+                             "+v"(acc[tt][k][3]));
             }
         }
         if (b + 1 < nb) commit(buf ^ 1);
