@@ -157,17 +157,18 @@ __device__ __forceinline__ void conv_load(const QkvRows& q, const float* __restr
     }
 }
 
+// The window write-back reloads the three raw inputs rather than selecting
+// them from x: a select by the uniform T - ts becomes one scalar mask per
+// element, which the compiler keeps live across the caller's loops.
 template <int N>
-__device__ __forceinline__ void conv_finish(float4 wt, float* __restrict__ cs, int c, int conv_dim,
-                                            int T, int ts, float (&x)[N + 3], float (&y)[N]) {
+__device__ __forceinline__ void conv_finish(const QkvRows& q, float4 wt, float* __restrict__ cs, int c,
+                                            int conv_dim, int T, int ts, float (&x)[N + 3], float (&y)[N]) {
     if (T >= kConvState && ts <= T - 1 && T - 1 < ts + N) {
 #pragma unroll
         for (int j = 0; j < kConvState; ++j) {
-            float v = 0.0f;
-#pragma unroll
-            for (int jj = 0; jj < N + 3; ++jj)
-                if (jj == T - ts + j) v = x[jj];
-            cs[(size_t)c * kConvState + j] = v;
+            const int row = T - kConvState + j - q.r0;
+            cs[(size_t)c * kConvState + j] = __builtin_bit_cast(
+                float, __builtin_amdgcn_raw_buffer_load_b32(q.rsrc, (row * conv_dim + c) * 4, 0, 0));
         }
     }
 #pragma unroll
@@ -276,7 +277,7 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep(
     conv_load<32>(rows, conv_w, cq_q, conv_dim, t0 + 32 * hq, xq, wq);
     conv_load<32>(rows, conv_w, cq_k, conv_dim, t0 + 32 * hq, xk, wk);
     auto conv_qk = [&](int ch, float4 wt, float (&x)[35], float (&y)[32]) {
-        conv_finish<32>(wt, cs, ch, conv_dim, T, t0 + 32 * hq, x, y);
+        conv_finish<32>(rows, wt, cs, ch, conv_dim, T, t0 + 32 * hq, x, y);
 #pragma unroll
         for (int j = 0; j < 32; ++j) Ks[32 * hq + j][cq] = y[j];
         lds_barrier();
@@ -458,7 +459,7 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep(
             {
                 float y[16];
                 const int ch = 2 * key_dim + vh * kDk + 64 * h + cl;
-                conv_finish<16>(wv[h], cs, ch, conv_dim, T, t0 + 16 * qt, xv[h], y);
+                conv_finish<16>(rows, wv[h], cs, ch, conv_dim, T, t0 + 16 * qt, xv[h], y);
                 if (h == 1) lds_barrier();   // every wave is past the first half
 #pragma unroll
                 for (int j = 0; j < 16; ++j) Vs[16 * qt + j][cl] = y[j];
