@@ -457,15 +457,18 @@ def cpu_baseline_prefill(x, T=2048):
 
 
 def measured_peaks():
-    """Ceilings measured on this GPU by libq35probe.so (plain streaming-read and
-    copy kernels, an fp32 MFMA loop), reported beside the datasheet peaks."""
+    """Ceilings measured on this GPU by libq35probe.so (grid-stride streaming
+    read and copy kernels, with plain and with non-temporal accesses, and an
+    fp32 MFMA loop), reported beside the datasheet peaks."""
     path = os.path.join(ROOT, "qwen3.5sharp_amd", "libq35probe.so")
     if not os.path.exists(path):
         raise FileNotFoundError(f"{path} is not built (run __graft_entry__.build())")
     lib = ctypes.CDLL(path)
     out = {}
-    for name, fn, args in (("hbm_read_GBps", lib.q35p_hbm_read_gbs, (ctypes.c_size_t(1 << 31), 10)),
-                           ("hbm_copy_rw_GBps", lib.q35p_hbm_copy_gbs, (ctypes.c_size_t(1 << 30), 10)),
+    for name, fn, args in (("hbm_read_GBps", lib.q35p_hbm_read_gbs, (ctypes.c_size_t(1 << 31), 10, 0)),
+                           ("hbm_read_nt_GBps", lib.q35p_hbm_read_gbs, (ctypes.c_size_t(1 << 31), 10, 1)),
+                           ("hbm_copy_rw_GBps", lib.q35p_hbm_copy_gbs, (ctypes.c_size_t(1 << 30), 10, 0)),
+                           ("hbm_copy_rw_nt_GBps", lib.q35p_hbm_copy_gbs, (ctypes.c_size_t(1 << 30), 10, 1)),
                            ("mfma_f32_TFLOPs", lib.q35p_mfma_f32_tflops, (20000,))):
         v = ctypes.c_double(0.0)
         r = fn(*args, ctypes.byref(v))

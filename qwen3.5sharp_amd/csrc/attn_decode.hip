@@ -20,7 +20,9 @@
 // single row.  The 4 q heads of the kv head share every K/V row it reads, so
 // each cache byte is read once per token.  A sub-chunk is processed with
 // every K and V load issued before any arithmetic (64 KiB of K and 64 KiB of
-// V in flight per workgroup), which is what keeps HBM busy; the first
+// V in flight per workgroup), which is what keeps HBM busy; the cache rows are
+// loaded non-temporally (each is read once per token, and the caches of a
+// long context do not fit the 256 MB MALL); the first
 // sub-chunk's loads go out before the q preparation, so that preparation
 // (each workgroup rotates and norms the 4 q rows, 4 KiB of input) costs no
 // memory round trip of its own.  Chunk 0 also rotates/norms the new K row,
@@ -114,13 +116,13 @@ __global__ __launch_bounds__(NT, 2) void attn_decode_partial(
     _Pragma("unroll") for (int m = 0; m < 4; ++m) {                                              \
         const float4* krow = reinterpret_cast<const float4*>(                                    \
             K + (size_t)min((S0) + team + 16 * m, last) * kHd);                                  \
-        _Pragma("unroll") for (int j = 0; j < 4; ++j) kk[m][j] = krow[l16 + 16 * j];             \
+        _Pragma("unroll") for (int j = 0; j < 4; ++j) kk[m][j] = load_nt(&krow[l16 + 16 * j].x); \
     }
 #define Q35_LOAD_V(S0)                                                                           \
     _Pragma("unroll") for (int m = 0; m < 16; ++m) {                                             \
         const float4* vrow = reinterpret_cast<const float4*>(                                    \
             V + (size_t)min((S0) + ps + 4 * m, last) * kHd);                                     \
-        vv[m] = vrow[d4];                                                                        \
+        vv[m] = load_nt(&vrow[d4].x);                                                            \
     }
 
     // One sub-chunk at s0 from kk / vv: scores (q re-read from LDS per head,

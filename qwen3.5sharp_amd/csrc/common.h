@@ -59,6 +59,19 @@ __device__ __forceinline__ float group_sum(float v) {
     return v;
 }
 
+// Non-temporal 16-byte load and store (global_load / global_store_dwordx4 with
+// the nt bit): for data streamed through once per call, such as decode states
+// and KV rows, so that it does not evict from L2 and MALL what the following
+// kernels read.
+typedef float nt_f32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ float4 load_nt(const float* p) {
+    const nt_f32x4 v = __builtin_nontemporal_load(reinterpret_cast<const nt_f32x4*>(p));
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ void store_nt(float* p, float4 v) {
+    __builtin_nontemporal_store(nt_f32x4{v.x, v.y, v.z, v.w}, reinterpret_cast<nt_f32x4*>(p));
+}
+
 // Workgroup index remapped so that consecutive logical indices share an XCD:
 // the hardware deals workgroups round-robin over the 8 XCDs (block b runs on
 // XCD b % 8), each with its own L2.  Requires total % 8 == 0; otherwise the

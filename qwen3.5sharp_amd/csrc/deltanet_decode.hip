@@ -9,8 +9,10 @@
 // Qwen35Ops.GatedRmsNorm (Qwen35Ops.cs:74-111).
 //
 // Work split.  One workgroup of 256 threads per (sequence, v-head) streams the
-// head's [128][128] fp32 state through HBM exactly once (read, then write)
-// from registers: a thread holds 4 columns x 16 rows.  Each workgroup
+// head's [128][128] fp32 state through HBM exactly once (read, then write,
+// both non-temporal: the states of a stack of layers and sequences do not fit
+// the MALL, and kept out of it they leave it to the KV rows of the attention
+// layers) from registers: a thread holds 4 columns x 16 rows.  Each workgroup
 // recomputes the conv + L2 norms of the 256 q/k channels of its k-head (a few
 // KiB, cache resident, shared by the H_v/H_k v-heads of the k-head) and owns
 // the 128 value channels of its head; the gated norm needs only the head.
@@ -117,7 +119,7 @@ __global__ __launch_bounds__(NT) void deltanet_decode_kernel(
     float4 s[RPT];
 #pragma unroll
     for (int j = 0; j < RPT; ++j)
-        s[j] = *reinterpret_cast<const float4*>(S + (size_t)(rg + RG * j) * kDk + 4 * c4);
+        s[j] = load_nt(S + (size_t)(rg + RG * j) * kDk + 4 * c4);
 
     qk_s[t] = conv_out(oq);
     // Threads t >= 128 recompute the head's last value channel and store the
@@ -199,7 +201,7 @@ __global__ __launch_bounds__(NT) void deltanet_decode_kernel(
         n.y = decay * s[j].y + ka * delta[1];
         n.z = decay * s[j].z + ka * delta[2];
         n.w = decay * s[j].w + ka * delta[3];
-        *reinterpret_cast<float4*>(S + (size_t)(rg + RG * j) * kDk + 4 * c4) = n;
+        store_nt(S + (size_t)(rg + RG * j) * kDk + 4 * c4, n);
     }
 
     if (rg == 0)

@@ -11,21 +11,30 @@ namespace {
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 // Grid-stride float4 read; one partial sum per thread keeps the loads alive.
-__global__ __launch_bounds__(256) void read_kernel(const float4* __restrict__ p, size_t n4,
+typedef float v4 __attribute__((ext_vector_type(4)));
+
+// NT: non-temporal loads (and stores), as the decode kernels stream state.
+template <bool NT>
+__global__ __launch_bounds__(256) void read_kernel(const v4* __restrict__ p, size_t n4,
                                                    float* __restrict__ out) {
     float acc = 0.0f;
     const size_t stride = (size_t)gridDim.x * 256;
     for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += stride) {
-        const float4 v = p[i];
+        const v4 v = NT ? __builtin_nontemporal_load(p + i) : p[i];
         acc += v.x + v.y + v.z + v.w;
     }
     out[(size_t)blockIdx.x * 256 + threadIdx.x] = acc;
 }
 
-__global__ __launch_bounds__(256) void copy_kernel(const float4* __restrict__ p,
-                                                   float4* __restrict__ q, size_t n4) {
+template <bool NT>
+__global__ __launch_bounds__(256) void copy_kernel(const v4* __restrict__ p, v4* __restrict__ q, size_t n4) {
     const size_t stride = (size_t)gridDim.x * 256;
-    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += stride) q[i] = p[i];
+    for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n4; i += stride) {
+        if (NT)
+            __builtin_nontemporal_store(__builtin_nontemporal_load(p + i), q + i);
+        else
+            q[i] = p[i];
+    }
 }
 
 // 8 independent v_mfma_f32_16x16x4f32 chains per wave, `iters` rounds.
@@ -67,20 +76,23 @@ hipError_t time_ms(F f, int reps, float* ms) {
 
 extern "C" {
 
-// Streaming read of `bytes` (multiple of 16), `reps` times: GB/s (1e9 B/s).
-int q35p_hbm_read_gbs(size_t bytes, int reps, double* gbs) {
+// Streaming read of `bytes` (multiple of 16), `reps` times: GB/s (1e9 B/s);
+// nt != 0: non-temporal loads.
+int q35p_hbm_read_gbs(size_t bytes, int reps, int nt, double* gbs) {
     if (!gbs || bytes < 16 || reps < 1) return -1;
     const size_t n4 = bytes / 16;
     const int grid = 2048;
-    float4* p = nullptr;
+    v4* p = nullptr;
     float* out = nullptr;
     hipError_t e = hipMalloc(&p, n4 * 16);
     if (e == hipSuccess) e = hipMalloc(&out, (size_t)grid * 256 * sizeof(float));
     if (e == hipSuccess) e = hipMemset(p, 0, n4 * 16);
     float ms = 0.0f;
     if (e == hipSuccess)
-        e = time_ms([&] { hipLaunchKernelGGL(read_kernel, dim3(grid), dim3(256), 0, nullptr, p, n4, out); },
-                    reps, &ms);
+        e = time_ms([&] {
+                if (nt) hipLaunchKernelGGL(read_kernel<true>, dim3(grid), dim3(256), 0, nullptr, p, n4, out);
+                else hipLaunchKernelGGL(read_kernel<false>, dim3(grid), dim3(256), 0, nullptr, p, n4, out);
+            }, reps, &ms);
     if (e == hipSuccess) *gbs = (double)n4 * 16 * reps / (ms * 1e-3) / 1e9;
     if (p) (void)hipFree(p);
     if (out) (void)hipFree(out);
@@ -88,19 +100,21 @@ int q35p_hbm_read_gbs(size_t bytes, int reps, double* gbs) {
 }
 
 // Copy of `bytes` into a second buffer, `reps` times: GB/s counting the bytes
-// read plus the bytes written.
-int q35p_hbm_copy_gbs(size_t bytes, int reps, double* gbs) {
+// read plus the bytes written; nt != 0: non-temporal loads and stores.
+int q35p_hbm_copy_gbs(size_t bytes, int reps, int nt, double* gbs) {
     if (!gbs || bytes < 16 || reps < 1) return -1;
     const size_t n4 = bytes / 16;
     const int grid = 2048;
-    float4 *p = nullptr, *q = nullptr;
+    v4 *p = nullptr, *q = nullptr;
     hipError_t e = hipMalloc(&p, n4 * 16);
     if (e == hipSuccess) e = hipMalloc(&q, n4 * 16);
     if (e == hipSuccess) e = hipMemset(p, 0, n4 * 16);
     float ms = 0.0f;
     if (e == hipSuccess)
-        e = time_ms([&] { hipLaunchKernelGGL(copy_kernel, dim3(grid), dim3(256), 0, nullptr, p, q, n4); },
-                    reps, &ms);
+        e = time_ms([&] {
+                if (nt) hipLaunchKernelGGL(copy_kernel<true>, dim3(grid), dim3(256), 0, nullptr, p, q, n4);
+                else hipLaunchKernelGGL(copy_kernel<false>, dim3(grid), dim3(256), 0, nullptr, p, q, n4);
+            }, reps, &ms);
     if (e == hipSuccess) *gbs = 2.0 * n4 * 16 * reps / (ms * 1e-3) / 1e9;
     if (p) (void)hipFree(p);
     if (q) (void)hipFree(q);
