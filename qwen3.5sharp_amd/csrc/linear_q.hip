@@ -1060,169 +1060,228 @@ void q4k_gemm(const unsigned char* __restrict__ w, const uint32_t* __restrict__ 
 // b = 4k + i of part j, m), minus 32 (bsums[2k] scales[2k] + bsums[2k+1]
 // scales[2k+1]); acc[k] = fma(dx * dw, (float)sumi[k], acc[k]); out =
 // hsum8(acc).  Each sumi[k] is exact in int32, so it is formed on
-// v_mfma_i32_16x16x32_i8: K runs over lane k's 32 bytes (j, m, i), with the
-// weights scales * v (|.| <= 8064) split into two int8 planes, 128 hi + lo;
-// a second K-chunk of 32 adds the bsums term as q8[32k .. 32k + 31] times
-// -32 * scales[2k + (value / 16 odd)], split the same way.  sumi = (D_hi << 7)
-// + D_lo.  A workgroup takes 64 tokens x 32 rows; a wave 32 tokens x 16 rows
-// (8 fp32 lane accumulators an output, as the reference keeps them).  Q6_K
-// blocks are 2-byte aligned: each is staged into LDS realigned to 4 bytes.
+// v_mfma_i32_16x16x64_i8: for lane k, lane group g of the MFMA (j = g / 2,
+// m0 = 2 (g % 2)) brings the 8 values of parts (j, m0) and (j, m0 + 1) at
+// bytes 4k .. 4k + 3 and, as the other half of K, q8 bytes 32k + 8g .. + 7
+// (sub-block 2k + j) against -32 scales[2k + j]: the bsums term without the
+// bsums.  The weights scales * v (|.| <= 8064) and -32 scales are split into
+// two int8 planes, 128 hi + lo, one MFMA each: sumi = (D_hi << 7) + D_lo.
+//
+// A workgroup takes 64 tokens x 32 rows; wave w takes rows 16 (w % 2) ..
+// + 15 of all 64 tokens for lanes k in {0, 1, 4, 5} (w < 2) or {2, 3, 6, 7},
+// so each value split serves four token tiles; at the end the upper waves
+// pass a_2 + a_6 and a_3 + a_7 to the lower ones, which finish hsum8 in its
+// order.  Blocks go to LDS by buffer loads straight into LDS (no registers,
+// double-buffered, one block ahead): per token its 64 qs dwords (dwords
+// 16-31 and 48-63 swapped in pairs so the value reads of lane groups 2g and
+// 2g + 1 fall on opposite bank parities; with a 66-dword token stride every
+// read is conflict-free) and its scale; per row the 53 dwords from the
+// 4-byte boundary below its 2-byte-aligned block, realigned on read.  Needs
+// n_out * n_in / 256 even (the last row block then ends on a 4-byte
+// boundary) and both operands below 2 GiB; otherwise the per-token GEMV runs.
 constexpr int SGT = 64, SGR = 32;
-constexpr int S_WD = 53;                                // dwords of a realigned block (212 B)
-constexpr int SX_CHUNKS = SGT * Q8K_WORDS / 4;          // 1216
-constexpr int SNX = (SX_CHUNKS + 255) / 256;
+constexpr int SX_STRIDE = 66;      // LDS dwords a token: 64 qs dwords, 2 of padding
+constexpr int SW_STRIDE = 53;      // LDS dwords a row: the raw dwords covering its block
+
+struct Q6Stage {
+    uint32_t x[SGT * SX_STRIDE];
+    float dx[SGT];
+    uint32_t w[SGR * SW_STRIDE];
+};
+
+typedef __attribute__((address_space(3))) void lds_void;
+typedef const volatile __attribute__((address_space(3))) uint32_t lds_cvu32;
+
+__device__ __forceinline__ void dma_b32(__amdgpu_buffer_rsrc_t rs, void* lds, uint32_t voff, uint32_t soff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)lds, 4, voff, soff, 0, 0);
+}
 
 typedef short s16x2 __attribute__((ext_vector_type(2)));
 
-// Four unsigned 6-bit values (bytes of v) times sc, as the low (& 127) and
-// high (>> 7) int8 planes of the products.
-__device__ __forceinline__ void q6k_split(uint32_t v, int sc, uint32_t& lo, uint32_t& hi) {
+// Four unsigned 6-bit values given doubled (bytes of v2 = 2 v) times sc, as
+// the low (& 127) and high (>> 7, two's complement) int8 planes of the
+// products sc v.  The doubled 16-bit products 2 sc v are formed in pairs:
+// the high plane is their high bytes, the low plane bits 1-7 of their low
+// bytes.
+__device__ __forceinline__ void q6k_split(uint32_t v2, int sc, uint32_t& lo, uint32_t& hi) {
     const s16x2 s2 = {(short)sc, (short)sc};
-    const s16x2 a = __builtin_bit_cast(s16x2, __builtin_amdgcn_perm(0u, v, 0x0c010c00u)) * s2;
-    const s16x2 b = __builtin_bit_cast(s16x2, __builtin_amdgcn_perm(0u, v, 0x0c030c02u)) * s2;
-    const uint32_t al = __builtin_bit_cast(uint32_t, a) & 0x007f007fu, bl = __builtin_bit_cast(uint32_t, b) & 0x007f007fu;
-    const uint32_t ah = __builtin_bit_cast(uint32_t, a >> (short)7), bh = __builtin_bit_cast(uint32_t, b >> (short)7);
-    lo = __builtin_amdgcn_perm(bl, al, 0x06040200u);
-    hi = __builtin_amdgcn_perm(bh, ah, 0x06040200u);
+    const uint32_t a = __builtin_bit_cast(uint32_t, __builtin_bit_cast(s16x2, __builtin_amdgcn_perm(0u, v2, 0x0c010c00u)) * s2);
+    const uint32_t b = __builtin_bit_cast(uint32_t, __builtin_bit_cast(s16x2, __builtin_amdgcn_perm(0u, v2, 0x0c030c02u)) * s2);
+    lo = (__builtin_amdgcn_perm(b, a, 0x06040200u) >> 1) & 0x7f7f7f7fu;
+    hi = __builtin_amdgcn_perm(b, a, 0x07050301u);
 }
 
-__global__ __launch_bounds__(256) void q6k_gemm(const unsigned char* __restrict__ w,
-                                                const uint32_t* __restrict__ q8,
-                                                float* __restrict__ y, int n_in, int n_out, int tokens) {
+// A operand of lane k = 2 KH + (kk & 1) + 4 (kk >> 1) for token tile tt:
+// qs dwords 32j + 8 m0 + k and + 8 (the values' q8), then 8k + 4j + (g & 1)
+// and + 2 (sub-block 2k + j: lane groups 2j and 2j + 1 read opposite bank
+// parities).  LDS slot s holds qs dword s ^ ((s >> 4) & 1).  Volatile LDS
+// reads keep each operand's four dwords in their own registers (merged reads
+// would mix operands of different lanes in one register quad).
+template <int KH>
+__device__ __forceinline__ i32x4 q6k_load_a(lds_cvu32* xv, int kk, int tt, int j, int odd) {
+    const int k = 2 * KH + (kk & 1) + 4 * (kk >> 1);
+    const int qa_s = 32 * j + 16 * odd + (k ^ odd);
+    const int qe_s = (8 * k + 4 * j + odd) ^ ((k >> 1) & 1);
+    lds_cvu32* xt = xv + SX_STRIDE * 16 * tt;
+    return i32x4{(int)xt[qa_s], (int)xt[qa_s + 8], (int)xt[qe_s], (int)xt[qe_s + 2]};
+}
+
+// One staged block: lanes k of half KH for the wave's 16 rows x 64 tokens.
+template <int KH>
+__device__ __forceinline__ void q6k_gemm_block(const Q6Stage& s, int shift, int rl, int l16, int lg,
+                                               float (&acc)[4][4][4]) {
 #pragma clang fp contract(off)
-    const int nb = n_in / QK;
-    const int row0 = blockIdx.x * SGR, tok0 = blockIdx.y * SGT;
-    const int tid = threadIdx.x, lane = tid & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int l16 = lane & 15, lg = lane >> 4;
-    const int rt = wave & 1, tp = wave >> 1;                // row tile; token tiles 2 tp, 2 tp + 1
-
-    __shared__ uint4 xsh[2][SX_CHUNKS];
-    __shared__ uint32_t wsh[2][SGR * S_WD];
-
-    const size_t total = (size_t)n_out * nb * Q6K_BYTES;
-    const int wrow = tid >> 3, wpart = tid & 7;             // staging: row, dwords 7 wpart .. +6
-    uint4 px[SNX];
-    uint32_t pw[8];
-    int wshift = 0;
-    auto issue = [&](int b) {
-#pragma unroll
-        for (int c = 0; c < SNX; ++c) {
-            const int i = tid + 256 * c;
-            px[c] = make_uint4(0u, 0u, 0u, 0u);
-            if (i < SX_CHUNKS) {
-                const int t = i / 19, k = i % 19;
-                px[c] = reinterpret_cast<const uint4*>(
-                    q8 + ((size_t)min(tok0 + t, tokens - 1) * nb + b) * Q8K_WORDS)[k];
-            }
-        }
-        const size_t s = ((size_t)min(row0 + wrow, n_out - 1) * nb + b) * Q6K_BYTES;
-        const size_t s4 = s & ~(size_t)3;
-        wshift = (int)(s - s4);
-#pragma unroll
-        for (int c = 0; c < 8; ++c) {
-            const int d = 7 * wpart + c;
-            const size_t off = s4 + 4 * (size_t)d;
-            pw[c] = 0u;
-            if (d <= S_WD) {
-                if (off + 4 <= total) pw[c] = *reinterpret_cast<const uint32_t*>(w + off);
-                else if (off < total) pw[c] = *reinterpret_cast<const uint16_t*>(w + off);
-            }
-        }
-    };
-    auto commit = [&](int buf) {
-#pragma unroll
-        for (int c = 0; c < SNX; ++c)
-            if (tid + 256 * c < SX_CHUNKS) xsh[buf][tid + 256 * c] = px[c];
-#pragma unroll
-        for (int c = 0; c < 7; ++c) {
-            const int a = 7 * wpart + c;
-            if (a < S_WD) wsh[buf][wrow * S_WD + a] = __builtin_amdgcn_alignbyte(pw[c + 1], pw[c], wshift);
-        }
-    };
-
-    float acc[2][8][4];
-#pragma unroll
-    for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-        for (int k = 0; k < 8; ++k)
-#pragma unroll
-            for (int r = 0; r < 4; ++r) acc[tt][k][r] = 0.0f;
-    const i32x4 zero = {0, 0, 0, 0};
     const int j = lg >> 1, odd = lg & 1;
-
-    issue(0);
-    commit(0);
-    __syncthreads();
-    for (int b = 0; b < nb; ++b) {
-        const int buf = b & 1;
-        if (b + 1 < nb) issue(b + 1);
-        const uint32_t* X = reinterpret_cast<const uint32_t*>(xsh[buf]);
-        const uint32_t* WB = wsh[buf] + (16 * rt + l16) * S_WD;
-        const float dw = half_bits_to_float(WB[52] & 0xffff);
-        float d[2][4];
+    const i32x4 zero = {0, 0, 0, 0};
+    const uint32_t* wr = s.w + SW_STRIDE * rl;
+    // dword f of the row's block
+    auto wd = [&](int f) { return __builtin_amdgcn_alignbyte(wr[f + 1], wr[f], shift); };
+    const float dw = half_bits_to_float(reinterpret_cast<const uint16_t*>(wr)[(shift + 208) >> 1]);
+    const uint32_t scw = wd(48 + lg);                        // scales 4 lg .. 4 lg + 3
+    float d[4][4];
 #pragma unroll
-        for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-            for (int r = 0; r < 4; ++r)
-                d[tt][r] = __builtin_bit_cast(float, X[(16 * (2 * tp + tt) + 4 * lg + r) * Q8K_WORDS]) * dw;
-        uint32_t scw[4];
-#pragma unroll
-        for (int q = 0; q < 4; ++q) scw[q] = WB[48 + q];
-        auto scale = [&](int idx) { return (int)(int8_t)((scw[idx >> 2] >> (8 * (idx & 3))) & 0xff); };
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            const int half = k >> 2;
-            // this lane's K values: (j, m0, 4k..4k+3) and (j, m0 + 1, 4k..4k+3), m0 = 2 odd
-            const uint32_t qa = WB[16 * j + k], qb = WB[16 * j + 8 + k], qh = WB[32 + 8 * j + k];
-            const uint32_t v0 = odd ? ((qa >> 4) & 0x0f0f0f0fu) | (qh & 0x30303030u)
-                                    : (qa & 0x0f0f0f0fu) | ((qh & 0x03030303u) << 4);
-            const uint32_t v1 = odd ? ((qb >> 4) & 0x0f0f0f0fu) | ((qh & 0xc0c0c0c0u) >> 2)
-                                    : (qb & 0x0f0f0f0fu) | ((qh & 0x0c0c0c0cu) << 2);
-            const int m0 = 2 * odd;
-            uint32_t l0, h0, l1, h1;
-            q6k_split(v0, scale(8 * j + 2 * m0 + half), l0, h0);
-            q6k_split(v1, scale(8 * j + 2 * m0 + 2 + half), l1, h1);
-            const long blo = (long)(((unsigned long)l1 << 32) | l0), bhi = (long)(((unsigned long)h1 << 32) | h0);
-            // bsums term: values 32k + 8 lg .. +7 lie in sub-block 2k + j
-            const int c = -32 * scale(2 * k + j);
-            const uint32_t elo = (uint32_t)(c & 127) * 0x01010101u, ehi = (uint32_t)((c >> 7) & 0xff) * 0x01010101u;
-            const long eblo = (long)(((unsigned long)elo << 32) | elo), ebhi = (long)(((unsigned long)ehi << 32) | ehi);
-#pragma unroll
-            for (int tt = 0; tt < 2; ++tt) {
-                const uint32_t* xt = X + (16 * (2 * tp + tt) + l16) * Q8K_WORDS + Q8K_QS;
-                const long am = (long)(((unsigned long)xt[32 * j + 8 * (m0 + 1) + k] << 32) | xt[32 * j + 8 * m0 + k]);
-                const uint2 e = *reinterpret_cast<const uint2*>(xt + 8 * k + 2 * lg);
-                const long ae = (long)(((unsigned long)e.y << 32) | e.x);
-                i32x4 dh = __builtin_amdgcn_mfma_i32_16x16x32_i8(am, bhi, zero, 0, 0, 0);
-                dh = __builtin_amdgcn_mfma_i32_16x16x32_i8(ae, ebhi, dh, 0, 0, 0);
-                i32x4 dl = __builtin_amdgcn_mfma_i32_16x16x32_i8(am, blo, zero, 0, 0, 0);
-                dl = __builtin_amdgcn_mfma_i32_16x16x32_i8(ae, eblo, dl, 0, 0, 0);
-#pragma unroll
-                for (int r = 0; r < 4; ++r) {
-                    const int hr = dh[r], lr = dl[r];
-                    const int sumi = (int)((unsigned)hr << 7) + lr;
-                    acc[tt][k][r] = fmaf(d[tt][r], (float)sumi, acc[tt][k][r]);
-                }
-                // folded here rather than after the last lane (keeps the
-                // MFMA results of one lane live, not of all eight)
-                asm volatile("" : "+v"(acc[tt][k][0]), "+v"(acc[tt][k][1]), "+v"(acc[tt][k][2]),
-                             "+v"(acc[tt][k][3]));
-            }
-        }
-        if (b + 1 < nb) commit(buf ^ 1);
-        __syncthreads();
+    for (int tt = 0; tt < 4; ++tt) {
+        const float4 x4 = *reinterpret_cast<const float4*>(&s.dx[16 * tt + 4 * lg]);
+        d[tt][0] = x4.x * dw; d[tt][1] = x4.y * dw; d[tt][2] = x4.z * dw; d[tt][3] = x4.w * dw;
     }
-    const int row = row0 + 16 * rt + l16;
+    // right rotations: low (g even) or high nibbles to bits 1-4; qh bits
+    // 0-1 / 4-5 (v0) and 2-3 / 6-7 (v1) to bits 5-6
+    const uint32_t rq = odd ? 3 : 31, rh0 = odd ? 31 : 27, rh1 = odd ? 1 : 29;
+    lds_cvu32* xv = (lds_cvu32*)(s.x + SX_STRIDE * l16);
+    // B operands (both planes) of lane k for this lane's row
+    auto planes = [&](int kk, i32x4& bh, i32x4& bl) {
+        const int k = 2 * KH + (kk & 1) + 4 * (kk >> 1), half = kk >> 1;
+        // Doubled 6-bit values of parts (j, m0) and (j, m0 + 1): nibble bits
+        // to 1-4 and qh bits to 5-6 of each byte, by rotations.
+        const uint32_t qa = wd(16 * j + k), qb = wd(16 * j + 8 + k), qh = wd(32 + 8 * j + k);
+        const uint32_t v0 = (__builtin_amdgcn_alignbit(qa, qa, rq) & 0x1e1e1e1eu) |
+                            (__builtin_amdgcn_alignbit(qh, qh, rh0) & 0x60606060u);
+        const uint32_t v1 = (__builtin_amdgcn_alignbit(qb, qb, rq) & 0x1e1e1e1eu) |
+                            (__builtin_amdgcn_alignbit(qh, qh, rh1) & 0x60606060u);
+        const int sc0 = (int)(int8_t)(scw >> (8 * half)), sc1 = (int)(int8_t)(scw >> (8 * (2 + half)));
+        uint32_t l0, h0, l1, h1;
+        q6k_split(v0, sc0, l0, h0);
+        q6k_split(v1, sc1, l1, h1);
+        // -32 scales[2k + j] = 128 ((-s) >> 2) + 32 ((-s) & 3), bytes replicated
+        const int neg = -(int)reinterpret_cast<const int8_t*>(wr)[shift + 192 + 2 * k + j];
+        const uint32_t elo = __builtin_amdgcn_perm(0u, (uint32_t)((neg & 3) << 5), 0u);
+        const uint32_t ehi = __builtin_amdgcn_perm(0u, (uint32_t)(neg >> 2), 0u);
+        bh = i32x4{(int)h0, (int)h1, (int)ehi, (int)ehi};
+        bl = i32x4{(int)l0, (int)l1, (int)elo, (int)elo};
+    };
+    // Each operand's reads go out one step (token tile) ahead of its
+    // products; the next lane's B planes are formed after the current
+    // lane's last step.
+    i32x4 a = q6k_load_a<KH>(xv, 0, 0, j, odd);
+    i32x4 bh, bl;
+    planes(0, bh, bl);
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt)
+    for (int step = 0; step < 16; ++step) {
+        const int kk = step >> 2, tt = step & 3;
+        i32x4 an = a;
+        if (step < 15) an = q6k_load_a<KH>(xv, (step + 1) >> 2, (step + 1) & 3, j, odd);
+        const i32x4 dh = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, bh, zero, 0, 0, 0);
+        const i32x4 dl = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, bl, zero, 0, 0, 0);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-            const int t = tok0 + 16 * (2 * tp + tt) + 4 * lg + r;
-            const float h[8] = {acc[tt][0][r], acc[tt][1][r], acc[tt][2][r], acc[tt][3][r],
-                                acc[tt][4][r], acc[tt][5][r], acc[tt][6][r], acc[tt][7][r]};
-            if (row < n_out && t < tokens) y[(size_t)t * n_out + row] = hsum8(h);
+            const int sumi = (int)((unsigned)dh[r] << 7) + dl[r];
+            acc[tt][kk][r] = fmaf(d[tt][r], (float)sumi, acc[tt][kk][r]);
         }
+        if (tt == 3 && kk < 3) planes(kk + 1, bh, bl);
+        a = an;
+    }
+}
+
+template <int KH>
+__device__ __forceinline__ void q6k_gemm_run(Q6Stage (&st)[2], const unsigned char* __restrict__ w,
+                                             const uint32_t* __restrict__ q8, float* __restrict__ y, int nb,
+                                             int n_out, int tokens, int row0, int tok0, int wave, int lane) {
+#pragma clang fp contract(off)
+    const int l16 = lane & 15, lg = lane >> 4, rt = wave & 1;
+    const int rl = 16 * rt + l16;                            // this lane's row in the tile
+    const uint32_t wbytes = (uint32_t)n_out * nb * Q6K_BYTES;
+    const __amdgpu_buffer_rsrc_t wrs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned char*>(w), 0, (int)wbytes, 0x00020000);
+    const uint32_t blk_x = Q8K_WORDS * 4;
+    const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint32_t*>(q8), 0, (int)((uint32_t)tokens * nb * blk_x), 0x00020000);
+    // Per-lane offsets, the same for every block: the qs dword of LDS slot
+    // `lane` (pairs swapped in dwords 16-31 and 48-63), a token's scale.
+    const uint32_t vx = 4u * (Q8K_QS + (lane ^ ((lane >> 4) & 1)));
+    const uint32_t vdx = (uint32_t)min(tok0 + lane, tokens - 1) * nb * blk_x;
+
+    auto stage = [&](int b, Q6Stage& s) {
+#pragma unroll
+        for (int i = 0; i < SGT / 4; ++i) {
+            const int t = wave + 4 * i;
+            dma_b32(xrs, &s.x[SX_STRIDE * t], vx, ((uint32_t)min(tok0 + t, tokens - 1) * nb + b) * blk_x);
+        }
+#pragma unroll
+        for (int i = 0; i < SGR / 4; ++i) {
+            const int r = wave + 4 * i;
+            const uint32_t so = (((uint32_t)min(row0 + r, n_out - 1) * nb + b) * Q6K_BYTES) & ~3u;
+            if (lane < SW_STRIDE) dma_b32(wrs, &s.w[SW_STRIDE * r], 4u * lane, so);
+        }
+        if (wave == 0) dma_b32(xrs, s.dx, vdx, b * blk_x);
+    };
+
+    // Byte offset of the row's block in its raw dwords, for even and odd b
+    // (blocks are 210 bytes: the offset alternates between 0 and 2).
+    const int rpar = (min(row0 + rl, n_out - 1) * nb) & 1;
+    const int shift_e = 2 * rpar, shift_o = 2 * (rpar ^ 1);
+
+    float acc[4][4][4];
+#pragma unroll
+    for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) acc[tt][kk][r] = 0.0f;
+
+    stage(0, st[0]);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    for (int b = 0; b < nb; ++b) {
+        const int p = b & 1;
+        if (b + 1 < nb) stage(b + 1, st[p ^ 1]);
+        q6k_gemm_block<KH>(st[p], p ? shift_o : shift_e, rl, l16, lg, acc);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+    }
+    // hsum8 (s_k = a_k + a_{k+4}; (s0 + s2) + (s1 + s3)) across the two halves.
+    float2* ex = reinterpret_cast<float2*>(st[0].x);
+    if (KH == 1)
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+                ex[(rt * 16 + 4 * tt + r) * 64 + lane] =
+                    make_float2(acc[tt][0][r] + acc[tt][2][r], acc[tt][1][r] + acc[tt][3][r]);
+    __syncthreads();
+    if (KH == 0) {
+        const int row = row0 + rl;
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float2 o = ex[(rt * 16 + 4 * tt + r) * 64 + lane];
+                const float s0 = acc[tt][0][r] + acc[tt][2][r], s1 = acc[tt][1][r] + acc[tt][3][r];
+                const float t0 = s0 + o.x, t1 = s1 + o.y;
+                const int t = tok0 + 16 * tt + 4 * lg + r;
+                if (row < n_out && t < tokens) y[(size_t)t * n_out + row] = t0 + t1;
+            }
+    }
+}
+
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
+void q6k_gemm(const unsigned char* __restrict__ w, const uint32_t* __restrict__ q8, float* __restrict__ y,
+              int n_in, int n_out, int tokens) {
+    __shared__ Q6Stage st[2];
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (wave >> 1)
+        q6k_gemm_run<1>(st, w, q8, y, n_in / QK, n_out, tokens, blockIdx.x * SGR, blockIdx.y * SGT, wave, lane);
+    else
+        q6k_gemm_run<0>(st, w, q8, y, n_in / QK, n_out, tokens, blockIdx.x * SGR, blockIdx.y * SGT, wave, lane);
 }
 
 
@@ -1387,10 +1446,11 @@ hipError_t launch_linear_q_prequant(q35m_ctx* c, int qtype, const void* w, const
         hipError_t e = hipGetLastError();
         if (e != hipSuccess || row_base == n_out) return e;
     }
-    // Q6_K: the tiled kernel from 16 tokens (one workgroup row of 64 tokens
-    // costs about 44 us at 4096 -> 2560, what 16 per-token GEMV passes take);
-    // both keep the same per-token arithmetic, so the results are identical.
-    if (qtype == 6 && tokens >= 16) {
+    // Q6_K: the tiled kernel from 16 tokens where its staging applies (see
+    // q6k_gemm), the per-token GEMV otherwise; both keep the same per-token
+    // arithmetic, so the results are identical.
+    if (qtype == 6 && tokens >= 16 && (((size_t)n_out * nb) & 1) == 0 &&
+        (size_t)n_out * nb * Q6K_BYTES < (1u << 31) && (size_t)tokens * nb * Q8K_WORDS * 4 < (1u << 31)) {
         ProfScope ps_(c, K_Q6K_GEMM);
         hipExtLaunchKernelGGL(q6k_gemm, dim3((n_out + SGR - 1) / SGR, (tokens + SGT - 1) / SGT), dim3(256), 0,
                               c->stream, ps_.a, ps_.b, 0, wb, qb, y, n_in, n_out, tokens);
