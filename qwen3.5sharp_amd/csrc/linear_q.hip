@@ -835,6 +835,18 @@ __global__ __launch_bounds__(256) void linear_f32(const float* __restrict__ w, c
     }
 }
 
+// Buffer loads straight into LDS (no registers): lane l's 4 or 16 bytes at
+// voff + soff go to lds + size * l; offsets past the descriptor's range read
+// as zero.  Completion is waited for with vmcnt.
+typedef __attribute__((address_space(3))) void lds_void;
+
+__device__ __forceinline__ void dma_b32(__amdgpu_buffer_rsrc_t rs, void* lds, uint32_t voff, uint32_t soff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)lds, 4, voff, soff, 0, 0);
+}
+__device__ __forceinline__ void dma_b128(__amdgpu_buffer_rsrc_t rs, void* lds, uint32_t voff, uint32_t soff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)lds, 16, voff, soff, 0, 0);
+}
+
 // ---------------------------------------------------------------- Q4_K, several tokens
 
 // The reference's Q4_K path for several tokens (MulMatQ4K.Gemm,
@@ -852,13 +864,16 @@ __global__ __launch_bounds__(256) void linear_f32(const float* __restrict__ w, c
 // per sub-block, the floor the reference's order sets.  The min term's
 // integer (at most 8 x 63 x 4064, exact in fp32) is two
 // v_mfma_f32_16x16x4f32 on small integers.  Blocks are double-buffered in
-// LDS; the next block's activations are loaded during sub-blocks 0-3 and its
-// weights during 4-7, so at most three 16-byte chunks a thread are staged.
+// LDS, the next one loaded by buffer loads straight into LDS (16-byte chunks,
+// 64 a wave-wide load) while the current one is processed.  The rows and
+// tokens of one launch stay below 2 GiB of weights and of activations (the
+// host splits larger calls).
 constexpr int GT = 64, GR = 128;
 constexpr int GW_CHUNKS = GR * Q4K_BYTES / 16;          // 1152
 constexpr int GX_CHUNKS = GT * Q8K_WORDS / 4;           // 1216
 constexpr int GTHREADS = 512, GRT = GR / 16 / (GTHREADS / 64);   // row tiles a wave: 1
-constexpr int GNW = (GW_CHUNKS + GTHREADS - 1) / GTHREADS, GNX = (GX_CHUNKS + GTHREADS - 1) / GTHREADS;
+constexpr int GWAVES = GTHREADS / 64;
+constexpr int GRUNS = (GX_CHUNKS + 64 * GWAVES - 1) / (64 * GWAVES);   // wave-wide loads a wave: 3
 constexpr int kMagic = 0x4B400000;                      // bits of 1.5 * 2^23
 constexpr float kMagicF = 12582912.0f;
 
@@ -878,40 +893,27 @@ void q4k_gemm(const unsigned char* __restrict__ w, const uint32_t* __restrict__ 
     __shared__ uint4 wsh[2][GW_CHUNKS];
     __shared__ uint4 xsh[2][GX_CHUNKS];
 
-    uint4 px[GNX], pw[GNW];
-    auto issue_x = [&](int b) {
+    const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<unsigned char*>(w), 0, (int)((uint32_t)n_rows * nb * Q4K_BYTES), 0x00020000);
+    const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint32_t*>(q8), 0, (int)((uint32_t)tokens * nb * Q8K_WORDS * 4), 0x00020000);
+    // Wave-wide load q covers chunks 64 q .. 64 q + 63; wave w issues q = w,
+    // w + 8, w + 16.  Per-lane offsets of block 0 (rows and tokens clamped);
+    // block b adds b times the block size as the scalar offset.
+    uint32_t wvo[GRUNS], xvo[GRUNS];
 #pragma unroll
-        for (int c = 0; c < GNX; ++c) {
-            const int i = tid + GTHREADS * c;
-            px[c] = make_uint4(0u, 0u, 0u, 0u);
-            if (i < GX_CHUNKS) {
-                const int t = i / 19, k = i % 19;
-                px[c] = reinterpret_cast<const uint4*>(
-                    q8 + ((size_t)min(tok0 + t, tokens - 1) * nb + b) * Q8K_WORDS)[k];
-            }
+    for (int m = 0; m < GRUNS; ++m) {
+        const int i = 64 * (wave + GWAVES * m) + lane;
+        wvo[m] = (uint32_t)min(row0 + i / 9, n_rows - 1) * nb * Q4K_BYTES + 16 * (i % 9);
+        xvo[m] = (uint32_t)min(tok0 + i / 19, tokens - 1) * nb * Q8K_WORDS * 4 + 16 * (i % 19);
+    }
+    auto stage = [&](int b, int buf) {
+#pragma unroll
+        for (int m = 0; m < GRUNS; ++m) {
+            const int q = wave + GWAVES * m;
+            if (64 * q < GW_CHUNKS) dma_b128(wrs, &wsh[buf][64 * q], wvo[m], (uint32_t)b * Q4K_BYTES);
+            if (64 * q < GX_CHUNKS) dma_b128(xrs, &xsh[buf][64 * q], xvo[m], (uint32_t)b * Q8K_WORDS * 4);
         }
-    };
-    auto issue_w = [&](int b) {
-#pragma unroll
-        for (int c = 0; c < GNW; ++c) {
-            const int i = tid + GTHREADS * c;
-            pw[c] = make_uint4(0u, 0u, 0u, 0u);
-            if (i < GW_CHUNKS) {
-                const int r = i / 9, k = i % 9;
-                pw[c] = reinterpret_cast<const uint4*>(
-                    w + ((size_t)min(row0 + r, n_rows - 1) * nb + b) * Q4K_BYTES)[k];
-            }
-        }
-    };
-    auto commit_x = [&](int buf) {
-#pragma unroll
-        for (int c = 0; c < GNX; ++c)
-            if (tid + GTHREADS * c < GX_CHUNKS) xsh[buf][tid + GTHREADS * c] = px[c];
-    };
-    auto commit_w = [&](int buf) {
-#pragma unroll
-        for (int c = 0; c < GNW; ++c)
-            if (tid + GTHREADS * c < GW_CHUNKS) wsh[buf][tid + GTHREADS * c] = pw[c];
     };
 
     float acc[4][GRT][4], mn[4][GRT][4];
@@ -923,15 +925,12 @@ void q4k_gemm(const unsigned char* __restrict__ w, const uint32_t* __restrict__ 
             for (int r = 0; r < 4; ++r) acc[tt][rt][r] = mn[tt][rt][r] = 0.0f;
     const i32x4 magic = {kMagic, kMagic, kMagic, kMagic};
 
-    issue_x(0);
-    issue_w(0);
-    commit_x(0);
-    commit_w(0);
+    stage(0, 0);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     for (int b = 0; b < nb; ++b) {
         const int buf = b & 1;
-        const bool more = b + 1 < nb;
-        if (more) issue_x(b + 1);
+        if (b + 1 < nb) stage(b + 1, buf ^ 1);
         const uint32_t* W = reinterpret_cast<const uint32_t*>(wsh[buf]);
         const uint32_t* X = reinterpret_cast<const uint32_t*>(xsh[buf]);
         // D rows of tile tt: tokens 16 tt + 4 lg + r; A rows: token 16 tt + l16.
@@ -1003,10 +1002,6 @@ void q4k_gemm(const unsigned char* __restrict__ w, const uint32_t* __restrict__ 
                                  "+v"(acc[tt][rt][3]));
                 }
             }
-            if (sb == 3 && more) {
-                commit_x(buf ^ 1);
-                issue_w(b + 1);
-            }
             // keep each sub-block's MFMA results to its own four quads
             __builtin_amdgcn_sched_barrier(0);
         }
@@ -1034,7 +1029,7 @@ void q4k_gemm(const unsigned char* __restrict__ w, const uint32_t* __restrict__ 
                 }
             }
         }
-        if (more) commit_w(buf ^ 1);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
     }
 #pragma unroll
@@ -1078,7 +1073,9 @@ void q4k_gemm(const unsigned char* __restrict__ w, const uint32_t* __restrict__ 
 // read is conflict-free) and its scale; per row the 53 dwords from the
 // 4-byte boundary below its 2-byte-aligned block, realigned on read.  Needs
 // n_out * n_in / 256 even (the last row block then ends on a 4-byte
-// boundary) and both operands below 2 GiB; otherwise the per-token GEMV runs.
+// boundary; otherwise the per-token GEMV runs).  The rows and tokens of one
+// launch stay below 2 GiB of weights and of activations (the host splits
+// larger calls at even rows).
 constexpr int SGT = 64, SGR = 32;
 constexpr int SX_STRIDE = 66;      // LDS dwords a token: 64 qs dwords, 2 of padding
 constexpr int SW_STRIDE = 53;      // LDS dwords a row: the raw dwords covering its block
@@ -1089,12 +1086,7 @@ struct Q6Stage {
     uint32_t w[SGR * SW_STRIDE];
 };
 
-typedef __attribute__((address_space(3))) void lds_void;
 typedef const volatile __attribute__((address_space(3))) uint32_t lds_cvu32;
-
-__device__ __forceinline__ void dma_b32(__amdgpu_buffer_rsrc_t rs, void* lds, uint32_t voff, uint32_t soff) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)lds, 4, voff, soff, 0, 0);
-}
 
 typedef short s16x2 __attribute__((ext_vector_type(2)));
 
@@ -1195,11 +1187,12 @@ __device__ __forceinline__ void q6k_gemm_block(const Q6Stage& s, int shift, int 
 template <int KH>
 __device__ __forceinline__ void q6k_gemm_run(Q6Stage (&st)[2], const unsigned char* __restrict__ w,
                                              const uint32_t* __restrict__ q8, float* __restrict__ y, int nb,
-                                             int n_out, int tokens, int row0, int tok0, int wave, int lane) {
+                                             int n_rows, int n_out, int tokens, int row0, int tok0, int wave,
+                                             int lane) {
 #pragma clang fp contract(off)
     const int l16 = lane & 15, lg = lane >> 4, rt = wave & 1;
     const int rl = 16 * rt + l16;                            // this lane's row in the tile
-    const uint32_t wbytes = (uint32_t)n_out * nb * Q6K_BYTES;
+    const uint32_t wbytes = (uint32_t)n_rows * nb * Q6K_BYTES;
     const __amdgpu_buffer_rsrc_t wrs =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned char*>(w), 0, (int)wbytes, 0x00020000);
     const uint32_t blk_x = Q8K_WORDS * 4;
@@ -1219,7 +1212,7 @@ __device__ __forceinline__ void q6k_gemm_run(Q6Stage (&st)[2], const unsigned ch
 #pragma unroll
         for (int i = 0; i < SGR / 4; ++i) {
             const int r = wave + 4 * i;
-            const uint32_t so = (((uint32_t)min(row0 + r, n_out - 1) * nb + b) * Q6K_BYTES) & ~3u;
+            const uint32_t so = (((uint32_t)min(row0 + r, n_rows - 1) * nb + b) * Q6K_BYTES) & ~3u;
             if (lane < SW_STRIDE) dma_b32(wrs, &s.w[SW_STRIDE * r], 4u * lane, so);
         }
         if (wave == 0) dma_b32(xrs, s.dx, vdx, b * blk_x);
@@ -1227,7 +1220,7 @@ __device__ __forceinline__ void q6k_gemm_run(Q6Stage (&st)[2], const unsigned ch
 
     // Byte offset of the row's block in its raw dwords, for even and odd b
     // (blocks are 210 bytes: the offset alternates between 0 and 2).
-    const int rpar = (min(row0 + rl, n_out - 1) * nb) & 1;
+    const int rpar = (min(row0 + rl, n_rows - 1) * nb) & 1;
     const int shift_e = 2 * rpar, shift_o = 2 * (rpar ^ 1);
 
     float acc[4][4][4];
@@ -1268,20 +1261,21 @@ __device__ __forceinline__ void q6k_gemm_run(Q6Stage (&st)[2], const unsigned ch
                 const float s0 = acc[tt][0][r] + acc[tt][2][r], s1 = acc[tt][1][r] + acc[tt][3][r];
                 const float t0 = s0 + o.x, t1 = s1 + o.y;
                 const int t = tok0 + 16 * tt + 4 * lg + r;
-                if (row < n_out && t < tokens) y[(size_t)t * n_out + row] = t0 + t1;
+                if (row < n_rows && t < tokens) y[(size_t)t * n_out + row] = t0 + t1;
             }
     }
 }
 
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
 void q6k_gemm(const unsigned char* __restrict__ w, const uint32_t* __restrict__ q8, float* __restrict__ y,
-              int n_in, int n_out, int tokens) {
+              int n_in, int n_rows, int n_out, int tokens) {
     __shared__ Q6Stage st[2];
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int nb = n_in / QK, row0 = blockIdx.x * SGR, tok0 = blockIdx.y * SGT;
     if (wave >> 1)
-        q6k_gemm_run<1>(st, w, q8, y, n_in / QK, n_out, tokens, blockIdx.x * SGR, blockIdx.y * SGT, wave, lane);
+        q6k_gemm_run<1>(st, w, q8, y, nb, n_rows, n_out, tokens, row0, tok0, wave, lane);
     else
-        q6k_gemm_run<0>(st, w, q8, y, n_in / QK, n_out, tokens, blockIdx.x * SGR, blockIdx.y * SGT, wave, lane);
+        q6k_gemm_run<0>(st, w, q8, y, nb, n_rows, n_out, tokens, row0, tok0, wave, lane);
 }
 
 
@@ -1436,26 +1430,39 @@ hipError_t launch_linear_q_prequant(q35m_ctx* c, int qtype, const void* w, const
                                   n_in, n_out, tokens, rows_per_wg, tok_per_wg);
         return hipGetLastError();
     }
+    // The tiled kernels address their operands through buffer descriptors
+    // (32-bit offsets): calls with more than 2 GiB of weight rows or of
+    // activations go in pieces of whole row and token tiles (even rows), each
+    // piece's per-row, per-token arithmetic unchanged.
+    auto tiled = [&](auto kern, int kid, int bb, int gr, int gt, int threads, int n_rows) {
+        const size_t lim = (size_t)1 << 31;
+        const int rmax = (int)std::min<size_t>(n_rows, (lim - 1) / ((size_t)nb * bb) / gr * gr);
+        const int tmax = (int)std::min<size_t>(tokens, (lim - 1) / ((size_t)nb * Q8K_WORDS * 4) / gt * gt);
+        for (int r0 = 0; r0 < n_rows; r0 += rmax)
+            for (int t0 = 0; t0 < tokens; t0 += tmax) {
+                const int nr = std::min(rmax, n_rows - r0), nt = std::min(tmax, tokens - t0);
+                ProfScope ps_(c, kid);
+                hipExtLaunchKernelGGL(kern, dim3((nr + gr - 1) / gr, (nt + gt - 1) / gt), dim3(threads), 0, c->stream,
+                                      ps_.a, ps_.b, 0, wb + (size_t)r0 * nb * bb,
+                                      qb + (size_t)t0 * nb * Q8K_WORDS, y + (size_t)t0 * n_out + r0, n_in, nr,
+                                      n_out, nt);
+                const hipError_t e = hipGetLastError();
+                if (e != hipSuccess) return e;
+            }
+        return hipSuccess;
+    };
     // Q4_K with several tokens: the panel order for the first n_out & ~7 rows
     // (the reference's MulMatQ4K.Gemm), the GEMV for the rest.
     const int row_base = (qtype == 4 && tokens > 1) ? (n_out & ~7) : 0;
     if (row_base > 0) {
-        ProfScope ps_(c, K_Q4K_GEMM);
-        hipExtLaunchKernelGGL(q4k_gemm, dim3((row_base + GR - 1) / GR, (tokens + GT - 1) / GT), dim3(GTHREADS), 0,
-                              c->stream, ps_.a, ps_.b, 0, wb, qb, y, n_in, row_base, n_out, tokens);
-        hipError_t e = hipGetLastError();
+        const hipError_t e = tiled(q4k_gemm, K_Q4K_GEMM, Q4K_BYTES, GR, GT, GTHREADS, row_base);
         if (e != hipSuccess || row_base == n_out) return e;
     }
-    // Q6_K: the tiled kernel from 16 tokens where its staging applies (see
-    // q6k_gemm), the per-token GEMV otherwise; both keep the same per-token
-    // arithmetic, so the results are identical.
-    if (qtype == 6 && tokens >= 16 && (((size_t)n_out * nb) & 1) == 0 &&
-        (size_t)n_out * nb * Q6K_BYTES < (1u << 31) && (size_t)tokens * nb * Q8K_WORDS * 4 < (1u << 31)) {
-        ProfScope ps_(c, K_Q6K_GEMM);
-        hipExtLaunchKernelGGL(q6k_gemm, dim3((n_out + SGR - 1) / SGR, (tokens + SGT - 1) / SGT), dim3(256), 0,
-                              c->stream, ps_.a, ps_.b, 0, wb, qb, y, n_in, n_out, tokens);
-        return hipGetLastError();
-    }
+    // Q6_K: the tiled kernel from 16 tokens when n_out * n_in / 256 is even
+    // (see q6k_gemm), the per-token GEMV otherwise; both keep the same
+    // per-token arithmetic, so the results are identical.
+    if (qtype == 6 && tokens >= 16 && (((size_t)n_out * nb) & 1) == 0)
+        return tiled(q6k_gemm, K_Q6K_GEMM, Q6K_BYTES, SGR, SGT, 256, n_out);
     const int rows_per_wg = min(LQ_THREADS / nb, LQ_MAX_ROWS);
     const int grid = (n_out - row_base + rows_per_wg - 1) / rows_per_wg;
     const int bb = qtype == 4 ? Q4K_BYTES : Q6K_BYTES;
