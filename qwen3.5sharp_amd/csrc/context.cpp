@@ -7,6 +7,7 @@
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <mutex>
 #include <string>
@@ -298,6 +299,10 @@ int q35m_create(const q35m_config* cfg, int n_seqs, int kv_capacity, q35m_ctx** 
     c->cfg = *cfg;
     c->cfg.is_recurrent = nullptr;
     c->n_seqs = n_seqs;
+    if (const char* e = std::getenv("Q35M_TILE_LIMIT_BYTES")) {
+        const unsigned long long v = std::strtoull(e, nullptr, 10);
+        if (v > 0 && v < c->tile_limit) c->tile_limit = (size_t)v;
+    }
     c->cap = kv_capacity;
     (void)hipGetDevice(&c->device);
     {

@@ -1435,10 +1435,10 @@ hipError_t launch_linear_q_prequant(q35m_ctx* c, int qtype, const void* w, const
     // activations go in pieces of whole row and token tiles (even rows), each
     // piece's per-row, per-token arithmetic unchanged.
     auto tiled = [&](auto kern, int kid, int bb, int gr, int gt, int threads, int n_rows) {
-        const size_t lim = (size_t)1 << 31;
+        const size_t lim = c->tile_limit;
         const int rmax = (int)std::min<size_t>(n_rows, (lim - 1) / ((size_t)nb * bb) / gr * gr);
         const int tmax = (int)std::min<size_t>(tokens, (lim - 1) / ((size_t)nb * Q8K_WORDS * 4) / gt * gt);
-        if (rmax <= 0 || tmax <= 0) return hipErrorInvalidValue;   // one tile over 2 GiB (n_in > 28M)
+        if (rmax <= 0 || tmax <= 0) return hipErrorInvalidValue;   // one tile over the limit (n_in > 28M)
         for (int r0 = 0; r0 < n_rows; r0 += rmax)
             for (int t0 = 0; t0 < tokens; t0 += tmax) {
                 const int nr = std::min(rmax, n_rows - r0), nt = std::min(tmax, tokens - t0);

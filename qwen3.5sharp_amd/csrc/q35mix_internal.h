@@ -113,6 +113,11 @@ struct q35m_ctx {
     float* work = nullptr;             // scratch for split-K partials and prefill
     size_t work_bytes = 0;
     float* noalloc_scratch = nullptr;  // the device's fixed scratch (q35m_attn_decode_noalloc)
+    // Largest weight or activation piece (bytes) one tiled-projection launch
+    // addresses: 2 GiB (32-bit buffer offsets); the environment variable
+    // Q35M_TILE_LIMIT_BYTES, read at create, lowers it (tests use it to make
+    // ordinary shapes go in pieces).
+    size_t tile_limit = (size_t)1 << 31;
     std::vector<void*> allocations;
     // Per-kernel event timers (off unless q35m_profile enables them).
     bool profile = false;

@@ -160,3 +160,25 @@ def test_linear_f32_bit_exact(ctx, n_in, n_out, tokens):
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
     for a in (dw, dx, dy):
         a.free()
+
+
+@pytest.mark.parametrize("qtype", [4, 6])
+def test_tiled_pieces_match_whole_launch(monkeypatch, qtype):
+    """The tiled Q4_K / Q6_K kernels go in pieces of whole row and token tiles
+    when a call holds more than 2 GiB of weight rows or activations; a context
+    created with a 256 KiB piece limit splits ordinary shapes the same way
+    (several row and token pieces here), and the results stay bit-identical to
+    the oracle."""
+    monkeypatch.setenv("Q35M_TILE_LIMIT_BYTES", str(256 * 1024))
+    c = q35mix.Context(q35mix.qwen35_config(num_layers=1, is_recurrent=[1]), n_seqs=1, kv_capacity=16)
+    try:
+        n_in, n_out, tokens = (2560, 520, 200) if qtype == 4 else (2560, 424, 200)
+        say(f"pieces {NAMES[qtype]} n_in={n_in} n_out={n_out} tokens={tokens}")
+        rng = np.random.default_rng(4242 + qtype)
+        w = qb.random_blocks(rng, qtype, qb.nblocks(qtype, n_out * n_in))
+        x = rng.standard_normal((tokens, n_in)).astype(np.float32)
+        got = run(c, qtype, w, x, n_in, n_out)
+        want = oracle.linear_q(qtype, w, x, n_in, n_out)
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    finally:
+        c.close()
