@@ -63,6 +63,18 @@ __device__ __forceinline__ float group_sum(float v) {
 // the nt bit): for data streamed through once per call, such as decode states
 // and KV rows, so that it does not evict from L2 and MALL what the following
 // kernels read.
+// Buffer loads straight into LDS (no registers): lane l's 4 or 16 bytes at
+// voff + soff of the descriptor's range go to lds + size * l; offsets past
+// the range read as zero.  Completion is waited for with vmcnt.
+typedef __attribute__((address_space(3))) void lds_void;
+
+__device__ __forceinline__ void dma_b32(__amdgpu_buffer_rsrc_t rs, void* lds, uint32_t voff, uint32_t soff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)lds, 4, voff, soff, 0, 0);
+}
+__device__ __forceinline__ void dma_b128(__amdgpu_buffer_rsrc_t rs, void* lds, uint32_t voff, uint32_t soff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)lds, 16, voff, soff, 0, 0);
+}
+
 typedef float nt_f32x4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ float4 load_nt(const float* p) {
     const nt_f32x4 v = __builtin_nontemporal_load(reinterpret_cast<const nt_f32x4*>(p));

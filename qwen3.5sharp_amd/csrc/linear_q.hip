@@ -835,18 +835,6 @@ __global__ __launch_bounds__(256) void linear_f32(const float* __restrict__ w, c
     }
 }
 
-// Buffer loads straight into LDS (no registers): lane l's 4 or 16 bytes at
-// voff + soff go to lds + size * l; offsets past the descriptor's range read
-// as zero.  Completion is waited for with vmcnt.
-typedef __attribute__((address_space(3))) void lds_void;
-
-__device__ __forceinline__ void dma_b32(__amdgpu_buffer_rsrc_t rs, void* lds, uint32_t voff, uint32_t soff) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)lds, 4, voff, soff, 0, 0);
-}
-__device__ __forceinline__ void dma_b128(__amdgpu_buffer_rsrc_t rs, void* lds, uint32_t voff, uint32_t soff) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)lds, 16, voff, soff, 0, 0);
-}
-
 // ---------------------------------------------------------------- Q4_K, several tokens
 
 // The reference's Q4_K path for several tokens (MulMatQ4K.Gemm,
