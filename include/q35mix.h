@@ -190,7 +190,8 @@ int q35m_attn_decode_noalloc(q35m_ctx* ctx, int layer, int n, const int* seqs, c
 /* PrefillAttention steps after the projections (Qwen35Model.Prefill.cs:
  * 113-149) for T tokens of one sequence starting at row kv_len(seq).
  * q_gate [T][heads*2*head_dim]; k, v [T][kv_heads*head_dim];
- * out [T][heads*head_dim].  Does not advance the length. */
+ * out [T][heads*head_dim].  Does not advance the length.  kv_len(seq) + T
+ * may reach 2097152 rows at most (Q35M_ERR_UNSUPPORTED beyond). */
 int q35m_attn_prefill(q35m_ctx* ctx, int layer, int seq, int T, const float* q_gate,
                       const float* k, const float* v, float* out);
 

@@ -142,6 +142,7 @@ __global__ __launch_bounds__(512, 1) void attn_prefill_flash(
     // Rows past blk_len read row 0 instead (finite data; their scores are
     // masked), so no select waits on the loads, and the refill is
     // unconditional.
+    // (The host keeps start + T <= kPrefillMaxRows, so row offsets fit 31 bits.)
     const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<float*>(Kh), 0, (int)std::min<size_t>((size_t)cap * kHd * sizeof(float), 0x7fffffff), 0x00020000);
     auto load_k = [&](int p0) {

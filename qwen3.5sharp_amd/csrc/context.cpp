@@ -576,6 +576,9 @@ int q35m_attn_prefill(q35m_ctx* ctx, int layer, int seq, int T, const float* q_g
     if ((long)start + T > ctx->cap)
         return fail(Q35M_ERR_CAPACITY, "sequence %d: %d + %d rows exceed KV capacity %d", seq, start,
                     T, ctx->cap);
+    if ((long)start + T > q35::kPrefillMaxRows)
+        return fail(Q35M_ERR_UNSUPPORTED, "attention prefill reads at most %d cached rows (sequence %d "
+                    "would reach %d)", q35::kPrefillMaxRows, seq, start + T);
     HIP_TRY(q35::ensure_work(ctx, q35::attn_prefill_work_bytes(ctx->d, T)), "workspace");
     HIP_TRY(q35::launch_attn_prefill(ctx, layer, seq, start, T, q_gate, k, v, out), "attn_prefill");
     return Q35M_OK;

@@ -21,6 +21,9 @@ constexpr int kRopeDim = 64;    // rotated dims
 constexpr int kRopeHalf = 32;
 constexpr int kMaxBatch = 64;   // sequences per mixer launch
 constexpr int kMaxVPerK = 4;    // DeltaNet v-heads per k-head (chunk prep stages their gates)
+// Rows of one (sequence, kv head) the prefill flash kernel can address: its
+// K tiles come through a buffer descriptor (32-bit byte offsets, 1 KiB a row).
+constexpr int kPrefillMaxRows = 1 << 21;
 
 // Per-launch sequence batch, passed by value in the kernel arguments.
 struct SeqBatch {

@@ -189,3 +189,20 @@ def test_abi_limits(ctx):
     with pytest.raises(q35mix.Q35Error) as ei:
         ctx.state_read(1, 0, 9)
     assert ei.value.code == q35mix.ERR_INVALID
+
+
+def test_attn_prefill_row_limit():
+    """The prefill flash kernel addresses a kv head's rows through a buffer
+    descriptor (32-bit offsets): a prefill that would reach past 2^21 cached
+    rows is refused with ERR_UNSUPPORTED before any work (the capacity check
+    comes first, so the context holds 2^21 + 1 rows: 8 GiB of K/V)."""
+    rows = (1 << 21) + 1
+    c = q35mix.Context(q35mix.qwen35_config(num_layers=1, is_recurrent=[0]), n_seqs=1, kv_capacity=rows)
+    try:
+        c.set_attn_weights(0, synth.attn_weights(256))
+        a = c.array((1, 8))
+        with pytest.raises(q35mix.Q35Error) as ei:
+            c.attn_prefill(0, 0, rows, a, a, a, a)
+        assert ei.value.code == q35mix.ERR_UNSUPPORTED
+    finally:
+        c.close()

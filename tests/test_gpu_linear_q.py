@@ -50,7 +50,7 @@ def run(ctx, qtype, w, x, n_in, n_out):
 SHAPES = [(2560, 8192, 1), (2560, 4096, 1), (2560, 32, 1), (4096, 2560, 1), (2560, 1024, 1),
           (256, 7, 1), (512, 33, 5), (2560, 1024, 3), (16384, 19, 2), (2560, 520, 70),
           (4096, 136, 130), (512, 40, 16), (1024, 72, 15), (2560, 64, 4), (1024, 13, 4), (1536, 24, 8),
-          (768, 33, 20)]
+          (768, 33, 20), (768, 40, 20)]
 
 
 NAMES = {1: "STQ1_0", 2: "Q2_0C", 4: "Q4_K", 5: "Q5_K", 6: "Q6_K", 14: "IQ4_XS"}
