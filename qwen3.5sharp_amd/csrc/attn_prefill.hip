@@ -94,7 +94,10 @@ __global__ __launch_bounds__(512, 1) void attn_prefill_flash(
     const int qb = nqb - 1 - rank / groups, y = rank % groups;
     const int kvh = y * hg / (nh / nkv);
     const int tid = threadIdx.x, lane = tid & 63;
-    const int half = tid >> 8, wave = (tid >> 6) & 3, htid = tid & 255;
+    // Wave-uniform (readfirstlane): the K tile loads take them as scalar
+    // offsets and LDS bases.
+    const int half = __builtin_amdgcn_readfirstlane(tid >> 8);
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6) & 3, htid = tid & 255;
     const int g = lane >> 4, c16 = lane & 15;
     const bool stores = wave < hg;           // uniform per wave
     const int h = hg * y + min(wave, hg - 1);
