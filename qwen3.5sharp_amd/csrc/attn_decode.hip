@@ -64,14 +64,16 @@ __global__ __launch_bounds__(NT, 2) void attn_decode_partial(
     const bool owner = c == 0;               // holds the new row
     const bool writer = owner && y % ng == 0;   // one group per kv head writes it to the cache
     if (!has_rows && !owner) return;
-    const int last = pos - 1;                // last cached row (read only when has_rows)
+    const int last = max(pos - 1, 0);        // last cached row (row 0 when there is none)
     const int nh = nkv * ng * HPW;
     const int kv_dim = nkv * kHd;
     // Cache of one (sequence, kv head): [cap][256], head-major.
     const size_t seq_off = ((size_t)sb.seq[i] * nkv + kvh) * cap * kHd;
     float* K = k_cache + seq_off;
     float* V = v_cache + seq_off;
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // `wave` provably below 4, so per-head branches that every wave takes
+    // (wave + 4 k < HPW for HPW >= 4) fold away.
+    const int tid = threadIdx.x, lane = tid & 63, wave = (tid >> 6) & (NT / kWave - 1);
 
     __shared__ float4 q_s[HPW][kHd / 4];
     __shared__ float4 knew_s[kHd / 4];
@@ -108,6 +110,10 @@ __global__ __launch_bounds__(NT, 2) void attn_decode_partial(
     const float4 rs = *reinterpret_cast<const float4*>(rope_sin + (size_t)pos * kRopeHalf + 4 * (lane & 7));
     const float4 wq = *reinterpret_cast<const float4*>(q_norm + 4 * lane);
     const float4 wk = *reinterpret_cast<const float4*>(k_norm + 4 * lane);
+    // Keeps these loads ahead of the K/V loads below (the compiler would
+    // otherwise sink them to their uses, behind the cache rows, and the q
+    // preparation would then wait for every row).
+    asm volatile("" ::: "memory");
 
     // K/V rows of sub-chunk `S0` into kk / vv, all loads unconditional: rows
     // past the last cached row read that row instead (their scores are masked
@@ -129,18 +135,36 @@ __global__ __launch_bounds__(NT, 2) void attn_decode_partial(
     // so its registers are not held across the K/V loads), the online
     // softmax (lane = position) and P.V.  Score and weight buffers alternate
     // by sub-chunk parity PAR.
+#define Q35_SCORE_ONE(m, h)                                                                      \
+    {                                                                                            \
+        float t = 0.0f;                                                                          \
+        _Pragma("unroll") for (int j = 0; j < 4; ++j) {                                          \
+            const float4 qj = q_s[h][l16 + 16 * j];                                              \
+            t += qj.x * kk[m][j].x + qj.y * kk[m][j].y + qj.z * kk[m][j].z + qj.w * kk[m][j].w;  \
+        }                                                                                        \
+        a[m][h] = group_sum<16>(t);                                                              \
+    }
+    // With one sub-chunk a workgroup, its rows are scored in load order (row
+    // block m outer), so the first blocks are scored while later K rows are
+    // still arriving; pipelined sub-chunks keep each head's q in registers
+    // across the four blocks instead.
 #define Q35_SCORES(PAR)                                                                          \
     {                                                                                            \
         float a[4][HPW];                                                                         \
-        _Pragma("unroll") for (int h = 0; h < HPW; ++h) {                                        \
-            float4 qh[4];                                                                        \
-            _Pragma("unroll") for (int j = 0; j < 4; ++j) qh[j] = q_s[h][l16 + 16 * j];          \
-            _Pragma("unroll") for (int m = 0; m < 4; ++m) {                                      \
-                float t = 0.0f;                                                                  \
-                _Pragma("unroll") for (int j = 0; j < 4; ++j)                                    \
-                    t += qh[j].x * kk[m][j].x + qh[j].y * kk[m][j].y + qh[j].z * kk[m][j].z +    \
-                         qh[j].w * kk[m][j].w;                                                   \
-                a[m][h] = group_sum<16>(t);                                                      \
+        if constexpr (NSUB == 1) {                                                               \
+            _Pragma("unroll") for (int m = 0; m < 4; ++m)                                        \
+                _Pragma("unroll") for (int h = 0; h < HPW; ++h) Q35_SCORE_ONE(m, h)              \
+        } else {                                                                                 \
+            _Pragma("unroll") for (int h = 0; h < HPW; ++h) {                                    \
+                float4 qh[4];                                                                    \
+                _Pragma("unroll") for (int j = 0; j < 4; ++j) qh[j] = q_s[h][l16 + 16 * j];      \
+                _Pragma("unroll") for (int m = 0; m < 4; ++m) {                                  \
+                    float t = 0.0f;                                                              \
+                    _Pragma("unroll") for (int j = 0; j < 4; ++j)                                \
+                        t += qh[j].x * kk[m][j].x + qh[j].y * kk[m][j].y + qh[j].z * kk[m][j].z +\
+                             qh[j].w * kk[m][j].w;                                               \
+                    a[m][h] = group_sum<16>(t);                                                  \
+                }                                                                                \
             }                                                                                    \
         }                                                                                        \
         if (l16 == 0)                                                                            \
@@ -197,10 +221,15 @@ __global__ __launch_bounds__(NT, 2) void attn_decode_partial(
     int s0 = c * SUB;
     float4 kk[4][4];
     float4 vv[16];
-    if (has_rows) {
-        Q35_LOAD_K(s0)
-        Q35_LOAD_V(s0)
-    }
+    // Issued unconditionally (the owner of a sequence with no cached rows
+    // reads row 0 and never uses it): behind a branch, the waits of the q
+    // preparation below would also cover these loads.  K rows go out in
+    // row-block order, then V, and stay in that order, so the scores of a
+    // block wait on its K rows alone.
+    Q35_LOAD_K(s0)
+    __builtin_amdgcn_sched_barrier(0);
+    Q35_LOAD_V(s0)
+    __builtin_amdgcn_sched_barrier(0);
     // q rows (the attention scale 1/sqrt(256) folded in); the owner also
     // rotates/norms the new K row, and the writer writes K and V into the cache.
 #pragma unroll
@@ -242,6 +271,7 @@ __global__ __launch_bounds__(NT, 2) void attn_decode_partial(
 #undef Q35_LOAD_K
 #undef Q35_LOAD_V
 #undef Q35_SCORES
+#undef Q35_SCORE_ONE
 #undef Q35_SOFTMAX_PV
 
     if (owner) {
