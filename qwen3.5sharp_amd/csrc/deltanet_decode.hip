@@ -115,11 +115,16 @@ __global__ __launch_bounds__(NT) void deltanet_decode_kernel(
     const size_t o_off = (size_t)i * value_dim + (size_t)vh * kDk + min(t, kDk - 1);
     const float z_t = zin[o_off], nw_t = ssm_norm[min(t, kDk - 1)];
 
-    // Thread owns columns 4*c4 .. +3 of rows rg + RG*j.
+    // Thread owns columns 4*c4 .. +3 of rows rg + RG*j.  The loads stay in
+    // row order (the scheduler may not reorder them across the barriers), so
+    // the products below can start on the first rows while later ones are
+    // still arriving.
     float4 s[RPT];
 #pragma unroll
-    for (int j = 0; j < RPT; ++j)
+    for (int j = 0; j < RPT; ++j) {
         s[j] = load_nt(S + (size_t)(rg + RG * j) * kDk + 4 * c4);
+        __builtin_amdgcn_sched_barrier(0);
+    }
 
     qk_s[t] = conv_out(oq);
     // Threads t >= 128 recompute the head's last value channel and store the
