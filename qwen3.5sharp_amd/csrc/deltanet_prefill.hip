@@ -257,14 +257,13 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep(
     __shared__ float bet[CH], gam[CH], nrm[CH];
     __shared__ float pre_b[kMaxVPerK][CH], pre_g[kMaxVPerK][CH];
 
-    // beta and g of the R v-heads (thread = (v-head, token); padded tokens
-    // read the last row and are masked below).
-    if (tid < R * CH) {
-        const int rr = tid / CH, j = tid % CH, vh = kh * R + rr;
-        const size_t gi = (size_t)min(t0 + j, T - 1) * nv + vh;
-        pre_b[rr][j] = 1.0f / (1.0f + expf(-bin[gi]));
-        pre_g[rr][j] = ssm_a[vh] * softplus_ref(ain[gi] + dt_bias[vh]);
-    }
+    // Inputs of beta and g of the R v-heads (thread = (v-head, token);
+    // padded tokens read the last row and are masked below; threads past
+    // R * CH repeat the last v-head and store nothing).  They are formed
+    // after the conv loads below are out, so those loads do not wait on these.
+    const int grr = min(tid / CH, R - 1), gj = tid % CH, gvh = kh * R + grr;
+    const size_t gi = (size_t)min(t0 + gj, T - 1) * nv + gvh;
+    const float gb_in = bin[gi], ga_in = ain[gi], g_sa = ssm_a[gvh], g_dt = dt_bias[gvh];
 
     // q, then k: conv'd into Ks (thread = channel tid % 128, tokens 32 (tid /
     // 128) ..), then the per-token sum of squares (thread = (token, quarter)).
@@ -276,6 +275,17 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep(
     float4 wq, wk;
     conv_load<32>(rows, conv_w, cq_q, conv_dim, t0 + 32 * hq, xq, wq);
     conv_load<32>(rows, conv_w, cq_k, conv_dim, t0 + 32 * hq, xk, wk);
+    __builtin_amdgcn_sched_barrier(0);
+    {
+        // Formed by every thread (so the loads above stay where they are)
+        // and stored by the first R * CH.
+        const float bv = 1.0f / (1.0f + expf(-gb_in));
+        const float gv = g_sa * softplus_ref(ga_in + g_dt);
+        if (tid < R * CH) {
+            pre_b[grr][gj] = bv;
+            pre_g[grr][gj] = gv;
+        }
+    }
     auto conv_qk = [&](int ch, float4 wt, float (&x)[35], float (&y)[32]) {
         conv_finish<32>(rows, wt, cs, ch, conv_dim, T, t0 + 32 * hq, x, y);
 #pragma unroll
