@@ -145,7 +145,12 @@ def bench_dn_prefill(steps, warmup, T=2048):
         ctx.deltanet_prefill(0, 0, T, qkv, z, b, a, out)
 
     ms = time_calls(ctx, step, steps, warmup)
-    kt = kernel_times(ctx, step, steps)
+    # Per-kernel times (the roofline) over at least 50 layers: one pass of 10
+    # varies by up to 10 % between runs, 50 agree with a kernel trace.  As
+    # time per step: (per-launch ms x launches) / steps profiled.
+    n_prof = max(steps, 50)
+    kt = kernel_times(ctx, step, n_prof)
+    kt = {k: (v[0] * v[1] / n_prof, 1) for k, v in kt.items()}
     ctx.close()
     return ms, kt, x
 
@@ -536,9 +541,7 @@ def main():
 
     if want("dn_prefill"):
         log("[bench] DeltaNet prefill T=2048 ...")
-        ms, kt, x = bench_dn_prefill(K, W)
-        # Per-step kernel time.
-        kt = {k: (v[0] * v[1] / K, 1) for k, v in kt.items()}
+        ms, kt, x = bench_dn_prefill(K, W)      # kt: per-step kernel times
         tok_s = 2048 / (ms / 1e3)
         kname, kms = dominant(kt)
         log(f"[bench] DeltaNet prefill: {ms:.3f} ms/step, {tok_s:.0f} tok/s; kernels {kt}")
