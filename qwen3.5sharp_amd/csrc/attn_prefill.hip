@@ -227,8 +227,8 @@ __global__ __launch_bounds__(512, 1) void attn_prefill_flash(
                 if (p >= my_len) st[pb][r] = -INFINITY;
                 mt = fmaxf(mt, st[pb][r]);
             }
-        mt = fmaxf(mt, __shfl_xor(mt, 16, kWave));
-        mt = fmaxf(mt, __shfl_xor(mt, 32, kWave));
+        mt = xor16_max(mt);
+        mt = xor32_max(mt);
         const bool live = mt != -INFINITY;
         const float alpha = live ? __expf(m_run - mt) : 1.0f;
         float ls = 0.0f;
@@ -240,8 +240,8 @@ __global__ __launch_bounds__(512, 1) void attn_prefill_flash(
                 st[pb][r] = e;
                 ls += e;
             }
-        ls += __shfl_xor(ls, 16, kWave);
-        ls += __shfl_xor(ls, 32, kWave);
+        ls = xor16_sum(ls);
+        ls = xor32_sum(ls);
         l_run = l_run * alpha + ls;
         m_run = mt;
         // O^T = alpha O^T + V^T P^T.

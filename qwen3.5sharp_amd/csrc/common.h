@@ -38,24 +38,51 @@ __device__ __forceinline__ void lds_barrier() {
     asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
-// Butterfly sum over all 64 lanes of a wave.
+// The values of lanes l and l ^ 16 (rows of 16 lanes swapped in pairs), or
+// l and l ^ 32 (the two halves), as (lower lane's, upper lane's) in both
+// lanes: one v_permlane16_swap / v_permlane32_swap, a register exchange that
+// does not go through the LDS crossbar (a ds_bpermute there queues behind
+// other waves' LDS traffic).
+__device__ __forceinline__ float2 lanes_xor16(float v) {
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return make_float2(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float2 lanes_xor32(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return make_float2(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+// Sum / max of the pair, the same in both lanes and equal to v + shfl_xor(v, o)
+// (fp addition is commutative).
+__device__ __forceinline__ float xor16_sum(float v) { const float2 p = lanes_xor16(v); return p.x + p.y; }
+__device__ __forceinline__ float xor32_sum(float v) { const float2 p = lanes_xor32(v); return p.x + p.y; }
+__device__ __forceinline__ float xor16_max(float v) { const float2 p = lanes_xor16(v); return fmaxf(p.x, p.y); }
+__device__ __forceinline__ float xor32_max(float v) { const float2 p = lanes_xor32(v); return fmaxf(p.x, p.y); }
+
+// Butterfly sum over all 64 lanes of a wave (the 32- and 16-lane steps by
+// lane swaps, the rest by shuffles within rows).
 __device__ __forceinline__ float wave_sum(float v) {
+    v = xor32_sum(v);
+    v = xor16_sum(v);
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+    for (int o = 8; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
     return v;
 }
 
 __device__ __forceinline__ float wave_max(float v) {
+    v = xor32_max(v);
+    v = xor16_max(v);
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+    for (int o = 8; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
     return v;
 }
 
 // Sum over lane groups of `width` consecutive lanes (width a power of two <= 64).
 template <int width>
 __device__ __forceinline__ float group_sum(float v) {
+    if constexpr (width >= 64) v = xor32_sum(v);
+    if constexpr (width >= 32) v = xor16_sum(v);
 #pragma unroll
-    for (int o = width / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+    for (int o = (width < 16 ? width : 16) / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
     return v;
 }
 
