@@ -13,14 +13,14 @@
 // [0, pos) and the new row, which comes from the inputs.
 //
 // Pass 1 (attn_decode_partial): one workgroup per (sequence, kv head, chunk c
-// of NSUB 64-row sub-chunks of the cached rows).  Chunk c holds the
-// sub-chunks c, c + nchunks, c + 2 nchunks, ... so the workgroups of one
-// cache that run together stream adjacent rows; the cached rows are split
-// exactly, so the grid has no second round of workgroups that each hold a
-// single row.  The 4 q heads of the kv head share every K/V row it reads, so
-// each cache byte is read once per token.  A sub-chunk is processed with
-// every K and V load issued before any arithmetic (64 KiB of K and 64 KiB of
-// V in flight per workgroup), which is what keeps HBM busy; the cache rows are
+// of NSUB sub-chunks of R cached rows; R = 64, or 16 for batch-1 shapes).
+// Chunk c holds the sub-chunks c, c + nchunks, c + 2 nchunks, ... so the
+// workgroups of one cache that run together stream adjacent rows; the cached
+// rows are split exactly, so the grid has no second round of workgroups that
+// each hold a single row.  The 4 q heads of the kv head share every K/V row it
+// reads, so each cache byte is read once per token.  A sub-chunk is processed
+// with every K and V load issued before any arithmetic (R KiB of K and of V in
+// flight per workgroup), which is what keeps HBM busy; the cache rows are
 // loaded non-temporally (each is read once per token, and the caches of a
 // long context do not fit the 256 MB MALL); the first
 // sub-chunk's loads go out before the q preparation, so that preparation
@@ -48,7 +48,7 @@ namespace {
 constexpr int NT = 256;
 constexpr int SUB = 64;   // positions per sub-chunk
 
-template <int NSUB, int HPW>
+template <int NSUB, int HPW, int R>
 __global__ __launch_bounds__(NT, 2) void attn_decode_partial(
     const float* __restrict__ q_gate, const float* __restrict__ knew,
     const float* __restrict__ vnew, const float* __restrict__ q_norm,
@@ -60,7 +60,7 @@ __global__ __launch_bounds__(NT, 2) void attn_decode_partial(
     const int c = blockIdx.x, y = blockIdx.y, i = blockIdx.z;
     const int kvh = y / ng;                  // head group y: q heads HPW y .. HPW y + HPW - 1
     const int pos = sb.pos[i];               // cached rows [0, pos); the new row is pos
-    const bool has_rows = c * SUB < pos;     // uniform
+    const bool has_rows = c * R < pos;       // uniform
     const bool owner = c == 0;               // holds the new row
     const bool writer = owner && y % ng == 0;   // one group per kv head writes it to the cache
     if (!has_rows && !owner) return;
@@ -119,13 +119,13 @@ __global__ __launch_bounds__(NT, 2) void attn_decode_partial(
     // past the last cached row read that row instead (their scores are masked
     // to weight 0).
 #define Q35_LOAD_K(S0)                                                                           \
-    _Pragma("unroll") for (int m = 0; m < 4; ++m) {                                              \
+    _Pragma("unroll") for (int m = 0; m < R / 16; ++m) {                                         \
         const float4* krow = reinterpret_cast<const float4*>(                                    \
             K + (size_t)min((S0) + team + 16 * m, last) * kHd);                                  \
         _Pragma("unroll") for (int j = 0; j < 4; ++j) kk[m][j] = load_nt(&krow[l16 + 16 * j].x); \
     }
 #define Q35_LOAD_V(S0)                                                                           \
-    _Pragma("unroll") for (int m = 0; m < 16; ++m) {                                             \
+    _Pragma("unroll") for (int m = 0; m < R / 4; ++m) {                                          \
         const float4* vrow = reinterpret_cast<const float4*>(                                    \
             V + (size_t)min((S0) + ps + 4 * m, last) * kHd);                                     \
         vv[m] = load_nt(&vrow[d4].x);                                                            \
@@ -150,15 +150,15 @@ __global__ __launch_bounds__(NT, 2) void attn_decode_partial(
     // across the four blocks instead.
 #define Q35_SCORES(PAR)                                                                          \
     {                                                                                            \
-        float a[4][HPW];                                                                         \
+        float a[R / 16][HPW];                                                                    \
         if constexpr (NSUB == 1) {                                                               \
-            _Pragma("unroll") for (int m = 0; m < 4; ++m)                                        \
+            _Pragma("unroll") for (int m = 0; m < R / 16; ++m)                                   \
                 _Pragma("unroll") for (int h = 0; h < HPW; ++h) Q35_SCORE_ONE(m, h)              \
         } else {                                                                                 \
             _Pragma("unroll") for (int h = 0; h < HPW; ++h) {                                    \
                 float4 qh[4];                                                                    \
                 _Pragma("unroll") for (int j = 0; j < 4; ++j) qh[j] = q_s[h][l16 + 16 * j];      \
-                _Pragma("unroll") for (int m = 0; m < 4; ++m) {                                  \
+                _Pragma("unroll") for (int m = 0; m < R / 16; ++m) {                             \
                     float t = 0.0f;                                                              \
                     _Pragma("unroll") for (int j = 0; j < 4; ++j)                                \
                         t += qh[j].x * kk[m][j].x + qh[j].y * kk[m][j].y + qh[j].z * kk[m][j].z +\
@@ -168,13 +168,13 @@ __global__ __launch_bounds__(NT, 2) void attn_decode_partial(
             }                                                                                    \
         }                                                                                        \
         if (l16 == 0)                                                                            \
-            _Pragma("unroll") for (int m = 0; m < 4; ++m)                                        \
+            _Pragma("unroll") for (int m = 0; m < R / 16; ++m)                                   \
                 _Pragma("unroll") for (int h = 0; h < HPW; ++h)                                  \
                     sc[PAR][h][team + 16 * m] = a[m][h];                                         \
     }
 #define Q35_SOFTMAX_PV(PAR)                                                                      \
     {                                                                                            \
-        const int np = min(SUB, pos - s0);                                                       \
+        const int np = min(R, pos - s0);                                                         \
         lds_barrier();                                                                           \
         _Pragma("unroll") for (int k = 0; k < QPW; ++k) {                                        \
             const int hh = wave + 4 * k;                                                         \
@@ -195,7 +195,7 @@ __global__ __launch_bounds__(NT, 2) void attn_decode_partial(
             acc[h].x *= alpha; acc[h].y *= alpha; acc[h].z *= alpha; acc[h].w *= alpha;          \
         }                                                                                        \
         /* masked positions carry weight exactly 0 (their V rows are row last) */               \
-        _Pragma("unroll") for (int m = 0; m < 16; ++m) {                                         \
+        _Pragma("unroll") for (int m = 0; m < R / 4; ++m) {                                      \
             const int pp = ps + 4 * m;                                                           \
             _Pragma("unroll") for (int h = 0; h < HPW; ++h) {                                    \
                 const float e = sc[PAR][h][pp];                                                  \
@@ -218,9 +218,9 @@ __global__ __launch_bounds__(NT, 2) void attn_decode_partial(
     for (int h = 0; h < HPW; ++h) acc[h] = make_float4(0.f, 0.f, 0.f, 0.f);
 
     // The first sub-chunk's loads go out before the q preparation.
-    int s0 = c * SUB;
-    float4 kk[4][4];
-    float4 vv[16];
+    int s0 = c * R;
+    float4 kk[R / 16][4];
+    float4 vv[R / 4];
     // Issued unconditionally (the owner of a sequence with no cached rows
     // reads row 0 and never uses it): behind a branch, the waits of the q
     // preparation below would also cover these loads.  K rows go out in
@@ -254,7 +254,7 @@ __global__ __launch_bounds__(NT, 2) void attn_decode_partial(
         // last sub-chunk runs after the loop, without loads for a next one.
         int sub = 0;
         for (;;) {
-            const int s1 = s0 + nchunks * SUB;
+            const int s1 = s0 + nchunks * R;
             if (sub + 1 == NSUB || s1 >= pos) break;     // uniform across the workgroup
             const int par = sub & 1;
             Q35_SCORES(par)
@@ -362,12 +362,13 @@ constexpr int MU = 4;                      // chunks per thread per round
 
 __global__ __launch_bounds__(MT) void attn_decode_merge(
     const float* __restrict__ part_o, const float* __restrict__ part_ml,
-    const float* __restrict__ q_gate, float* __restrict__ out, int nh, int hpw, int nchunks, SeqBatch sb) {
+    const float* __restrict__ q_gate, float* __restrict__ out, int nh, int hpw, int nchunks, int rows,
+    SeqBatch sb) {
     const int h = blockIdx.x / (kHd / MSLICE), slice = blockIdx.x % (kHd / MSLICE);
     const int i = blockIdx.y, t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int y = h / hpw, hl = h % hpw;     // head group of the partials
     const int pos = sb.pos[i];
-    const int nc = max(1, min(nchunks, (pos + SUB - 1) / SUB));   // chunks that ran
+    const int nc = max(1, min(nchunks, (pos + rows - 1) / rows));   // chunks that ran
     const size_t base = ((size_t)i * (nh / hpw) + y) * nchunks;
     __shared__ float4 obuf[4][MD4];
     __shared__ float mbuf[4], lbuf[4];
@@ -427,10 +428,10 @@ __global__ __launch_bounds__(MT) void attn_decode_merge(
     }
 }
 
-// Sub-chunks of the longest cached range in the batch.
-int max_subchunks(const SeqBatch& sb) {
+// Sub-chunks of `rows` rows in the longest cached range in the batch.
+int max_subchunks(const SeqBatch& sb, int rows) {
     int m = 0;
-    for (int i = 0; i < sb.n; ++i) m = max(m, (sb.pos[i] + SUB - 1) / SUB);
+    for (int i = 0; i < sb.n; ++i) m = max(m, (sb.pos[i] + rows - 1) / rows);
     return m;
 }
 
@@ -444,13 +445,35 @@ int pick_nsub(int n, int groups, int max_subs, int n_cu) {
     return 8;
 }
 
-int nchunks_for(int max_subs, int nsub) { return max(1, (max_subs + nsub - 1) / nsub); }
-
 // q heads per workgroup: the whole group of a kv head up to 8 (1, 2, 4 or 8),
 // groups of 8 beyond (each re-reads the kv head's cache).
 int heads_per_wg(const Dims& d) {
     const int g = d.nh / d.nkv;
     return g <= 8 ? g : 8;
+}
+
+// Split of one call: rows per sub-chunk, sub-chunks per workgroup (NSUB),
+// workgroups per head group (chunks).  When one 64-row sub-chunk a workgroup
+// would already give at least one workgroup per CU (batch 1 at long contexts,
+// the 8192-row case among them), the same rows go as 4 sub-chunks of 16 rows
+// instead: each workgroup then holds one 16-row sub-chunk's loads in flight
+// at a time, refilled by the software pipeline, instead of all 64 rows at once
+// (measured at 8193 rows: 14.0 vs 15.6 us for the partial kernel; 32-row
+// sub-chunks 14.5 us; all 64 rows loaded up front as 4 register sets 17.6 us;
+// twice or four times the workgroups with fewer sub-chunks each slower still).
+struct DecodePlan {
+    int rows, nsub, nchunks;
+};
+
+DecodePlan plan_decode(const Dims& d, const SeqBatch& sb, int n_cu) {
+    const int groups = d.nh / heads_per_wg(d);
+    const int max64 = max_subchunks(sb, SUB);
+    const int nsub = pick_nsub(sb.n, groups, max64, n_cu);
+    if (nsub == 1 && (long)sb.n * groups * max64 >= n_cu) {
+        const int max16 = max_subchunks(sb, SUB / 4);
+        return {SUB / 4, 4, max(1, (max16 + 3) / 4)};
+    }
+    return {SUB, nsub, max(1, (max64 + nsub - 1) / nsub)};
 }
 
 }  // namespace
@@ -467,11 +490,8 @@ hipError_t attn_decode_scratch_address(float** ptr) {
 }
 
 size_t attn_decode_work_bytes(const q35m_ctx* c, const SeqBatch& sb) {
-    const int max_subs = max_subchunks(sb);
-    const int groups = c->d.nh / heads_per_wg(c->d);
-    const int nsub = pick_nsub(sb.n, groups, max_subs, c->n_cu);
-    const size_t nchunks = nchunks_for(max_subs, nsub);
-    return (size_t)sb.n * c->d.nh * nchunks * (kHd + 2) * sizeof(float);
+    const DecodePlan p = plan_decode(c->d, sb, c->n_cu);
+    return (size_t)sb.n * c->d.nh * p.nchunks * (kHd + 2) * sizeof(float);
 }
 
 hipError_t launch_attn_decode(q35m_ctx* c, int layer, const SeqBatch& sb, const float* q_gate,
@@ -480,14 +500,14 @@ hipError_t launch_attn_decode(q35m_ctx* c, int layer, const SeqBatch& sb, const 
     const AttnLayer& L = c->full[layer];
     const int hpw = heads_per_wg(d);
     const int groups = d.nh / hpw, ng = groups / d.nkv;
-    const int max_subs = max_subchunks(sb);
-    const int nsub = pick_nsub(sb.n, groups, max_subs, c->n_cu);
-    const int nchunks = nchunks_for(max_subs, nsub);
+    const DecodePlan p = plan_decode(d, sb, c->n_cu);
+    const int nsub = p.nsub, nchunks = p.nchunks;
     float* part_o = work;
     float* part_ml = part_o + (size_t)sb.n * d.nh * nchunks * kHd;
     const dim3 grid(nchunks, groups, sb.n);
     {
-        const int kid = nsub == 8 ? K_ATTN_DECODE_PARTIAL8
+        const int kid = p.rows != SUB ? K_ATTN_DECODE_PARTIAL4R16
+                      : nsub == 8 ? K_ATTN_DECODE_PARTIAL8
                       : nsub == 4 ? K_ATTN_DECODE_PARTIAL4
                       : nsub == 2 ? K_ATTN_DECODE_PARTIAL2 : K_ATTN_DECODE_PARTIAL1;
         ProfScope ps_(c, kid);
@@ -498,10 +518,11 @@ hipError_t launch_attn_decode(q35m_ctx* c, int layer, const SeqBatch& sb, const 
         };
         auto by_nsub = [&](auto h) {
             constexpr int H = decltype(h)::value;
-            if (nsub == 8) go(attn_decode_partial<8, H>);
-            else if (nsub == 4) go(attn_decode_partial<4, H>);
-            else if (nsub == 2) go(attn_decode_partial<2, H>);
-            else go(attn_decode_partial<1, H>);
+            if (p.rows != SUB) go(attn_decode_partial<4, H, SUB / 4>);
+            else if (nsub == 8) go(attn_decode_partial<8, H, SUB>);
+            else if (nsub == 4) go(attn_decode_partial<4, H, SUB>);
+            else if (nsub == 2) go(attn_decode_partial<2, H, SUB>);
+            else go(attn_decode_partial<1, H, SUB>);
         };
         if (hpw == 8) by_nsub(std::integral_constant<int, 8>());
         else if (hpw == 4) by_nsub(std::integral_constant<int, 4>());
@@ -513,7 +534,7 @@ hipError_t launch_attn_decode(q35m_ctx* c, int layer, const SeqBatch& sb, const 
     {
         ProfScope ps_(c, K_ATTN_DECODE_MERGE);
         hipExtLaunchKernelGGL(attn_decode_merge, dim3(d.nh * (kHd / MSLICE), sb.n), dim3(MT), 0, c->stream,
-                              ps_.a, ps_.b, 0, part_o, part_ml, q_gate, out, d.nh, hpw, nchunks, sb);
+                              ps_.a, ps_.b, 0, part_o, part_ml, q_gate, out, d.nh, hpw, nchunks, p.rows, sb);
     }
     return hipGetLastError();
 }

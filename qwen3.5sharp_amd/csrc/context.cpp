@@ -179,7 +179,7 @@ const char* kernel_name(int id) {
         "attn_decode_merge",      "attn_prefill_prep",       "attn_prefill_flash",
         "q8k_quantize",           "linear_q<4>",             "linear_q<6>",
         "q4k_gemm", "q6k_gemm", "add_rmsnorm", "linear_qs<5>", "linear_qs<14>", "linear_f32", "linear_qt<2>",
-        "linear_qt<1>"};
+        "linear_qt<1>", "attn_decode_partial<4,16>"};
     return (id >= 0 && id < K_COUNT) ? names[id] : nullptr;
 }
 

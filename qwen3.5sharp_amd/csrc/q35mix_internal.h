@@ -82,6 +82,7 @@ enum KernelId {
     K_F32_LINEAR,
     K_Q2_0C_LINEAR,
     K_STQ1_0_LINEAR,
+    K_ATTN_DECODE_PARTIAL4R16,   // attn_decode_partial, 4 sub-chunks of 16 rows per workgroup
     K_COUNT
 };
 const char* kernel_name(int id);

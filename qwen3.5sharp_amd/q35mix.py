@@ -462,15 +462,19 @@ def cu_count(device: int = 0) -> int:
     return n.value
 
 
-def attn_decode_variant(n_seqs: int, n_kv_heads: int, lengths, n_cu: int) -> int:
-    """Sub-chunks per workgroup the decode attention picks for a batch whose
-    sequences hold `lengths` cached rows: the fewest (1, 2, 4) keeping the
-    grid within 2 workgroups per CU, else 8."""
+def attn_decode_variant(n_seqs: int, n_kv_heads: int, lengths, n_cu: int) -> str:
+    """Split the decode attention picks for a batch whose sequences hold
+    `lengths` cached rows, as its per-kernel timer names it: sub-chunks of 64
+    rows per workgroup, the fewest (1, 2, 4) keeping the grid within 2
+    workgroups per CU, else 8; when one sub-chunk already gives at least one
+    workgroup per CU, 4 sub-chunks of 16 rows ("4,16") instead."""
     max_subs = max((int(x) + 63) // 64 for x in lengths)
     for ns in (1, 2, 4):
         if n_seqs * n_kv_heads * max(1, -(-max_subs // ns)) <= 2 * n_cu:
-            return ns
-    return 8
+            if ns == 1 and n_seqs * n_kv_heads * max_subs >= n_cu:
+                return "4,16"
+            return str(ns)
+    return "8"
 
 
 class Event:

@@ -4,9 +4,11 @@ context ~32K) and at every split the decode attention picks.
 - The decode attention at 8 sequences x up to 32767 cached rows runs
   attn_decode_partial<8> (asserted through the per-kernel timers) and matches
   the oracle for every sequence, a ragged batch with a 1-row sequence included.
-- Each split variant (1, 2, 4 sub-chunks per workgroup) is selected by a
-  shape that the selection rule maps to it, asserted the same way, and
-  matches the oracle; sequences with no cached rows take only the new row.
+- Each split variant (1, 2, 4 sub-chunks of 64 rows per workgroup, and 4
+  sub-chunks of 16 rows for the batch-1 shapes) is selected by a shape that
+  the selection rule maps to it, asserted the same way, and matches the
+  oracle, ragged batches with 0- and 1-row sequences included; sequences
+  with no cached rows take only the new row.
 - A reduced stack (3 Gated-DeltaNet layers + 1 GQA layer, 8 sequences, KV
   pre-filled to ~32,700 rows, 3 batched decode steps) matches the oracle in
   every layer's output after every step and in the final recurrent states,
@@ -64,7 +66,7 @@ def fill_rows(dst, off):
 def variant_ran(c):
     names = [k for k in c.profile_read() if k.startswith("attn_decode_partial<")]
     assert len(names) == 1, names
-    return int(names[0][len("attn_decode_partial<"):-1])
+    return names[0][len("attn_decode_partial<"):-1]
 
 
 def attn_batch_case(lens, salt, cap=None):
@@ -118,16 +120,18 @@ def test_attn_decode_long_context_split8():
     1-row sequence): the 8-sub-chunk split, checked per sequence."""
     lens = [32700, 30011, 28417, 24576, 20480, 16384, 32767, 1]
     ran = attn_batch_case(lens, salt=11, cap=32768)
-    assert ran == 8
-    assert q35mix.attn_decode_variant(8, NKV, lens, q35mix.cu_count()) == 8
+    assert ran == "8"
+    assert q35mix.attn_decode_variant(8, NKV, lens, q35mix.cu_count()) == "8"
 
 
 @pytest.mark.parametrize("lens", [[8192], [8192, 8192], [8000, 7000, 8000, 6000], [0, 5, 4095],
-                                  [0, 0], [1], [64, 65, 127, 128]])
+                                  [0, 0], [1], [64, 65, 127, 128], [2000, 1999, 37], [4000, 0],
+                                  [4000, 1]])
 def test_attn_decode_split_variants(lens):
-    """Shapes whose selected split is 1, 2 or 4 sub-chunks per workgroup (the
-    batch-1 8192-row shape among them), sequences with no cached rows, and
-    cached lengths at and around sub-chunk boundaries."""
+    """Shapes whose selected split is 1, 2 or 4 sub-chunks of 64 rows or 4
+    of 16 rows per workgroup (the batch-1 8192-row shape among them),
+    sequences with no cached rows, and cached lengths at and around sub-chunk
+    boundaries."""
     want = q35mix.attn_decode_variant(len(lens), NKV, lens, q35mix.cu_count())
     ran = attn_batch_case(lens, salt=20 + len(lens))
     assert ran == want, (ran, want)
@@ -137,9 +141,10 @@ def test_attn_decode_variants_cover_all_splits():
     """The parametrized shapes above reach every split on this device."""
     cu = q35mix.cu_count()
     shapes = [[8192], [8192, 8192], [8000, 7000, 8000, 6000], [0, 5, 4095], [0, 0], [1],
-              [64, 65, 127, 128], [32700, 30011, 28417, 24576, 20480, 16384, 32767, 1]]
+              [64, 65, 127, 128], [2000, 1999, 37], [4000, 0], [4000, 1],
+              [32700, 30011, 28417, 24576, 20480, 16384, 32767, 1]]
     got = {q35mix.attn_decode_variant(len(x), NKV, x, cu) for x in shapes}
-    assert got == {1, 2, 4, 8}, (cu, got)
+    assert got == {"1", "2", "4", "8", "4,16"}, (cu, got)
 
 
 def test_reduced_stack_long_context():
