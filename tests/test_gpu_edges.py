@@ -206,3 +206,33 @@ def test_attn_prefill_row_limit():
         assert ei.value.code == q35mix.ERR_UNSUPPORTED
     finally:
         c.close()
+
+
+def test_deltanet_prefill_long_context():
+    """T = 16421 (257 chunks: an odd count, the last holding 37 tokens) in a
+    2 k-head / 4 v-head geometry, from a non-zero state: the chunk scan's
+    recurrence over a long chain and the workspace offsets at large chunk
+    counts, outputs of every token and the final state against the oracle."""
+    nk, nv, T = 2, 4, 16421
+    d = oracle.dims(n_k_heads=nk, n_v_heads=nv)
+    cfg = q35mix.qwen35_config(num_layers=1, n_k_heads=nk, n_v_heads=nv, is_recurrent=[1])
+    with q35mix.Context(cfg, n_seqs=1, kv_capacity=4) as c:
+        w = synth.deltanet_weights(nk, nv, 128, salt=77)
+        c.set_deltanet_weights(0, w)
+        st = synth.deltanet_state(nk, nv, 128, salt=78)
+        c.state_write(0, 0, q35mix.STATE_RECURRENT, st["state"])
+        c.state_write(0, 0, q35mix.STATE_CONV, st["conv_state"])
+        x = synth.deltanet_inputs(T, nk, nv, 128, salt=79)
+        out = c.array((T, c.value_dim))
+        say(f"deltanet_prefill long T={T}: launching")
+        c.deltanet_prefill(0, 0, T, c.array((T, c.conv_dim), x["qkv"]), c.array((T, c.value_dim), x["z"]),
+                           c.array((T, nv), x["b"]), c.array((T, nv), x["a"]), out)
+        got = out.download()
+        o_ref, cs_ref, st_ref, _ = oracle.deltanet_prefill(d, T, x["qkv"], x["z"], x["b"], x["a"], w,
+                                                           st["state"], st["conv_state"])
+        e_out = rel(got, o_ref)
+        e_last = rel(got[-64:], o_ref[-64:])
+        e_st = rel(c.state_read(0, 0, q35mix.STATE_RECURRENT), st_ref)
+        say(f"  out rel err {e_out:.2e} (last chunk {e_last:.2e}), state rel err {e_st:.2e}")
+        assert e_out <= TOL and e_last <= TOL and e_st <= TOL
+        np.testing.assert_array_equal(c.state_read(0, 0, q35mix.STATE_CONV), cs_ref)
