@@ -131,6 +131,24 @@ int q35m_snapshot_save(q35m_ctx* ctx, int seq, void* dev, size_t bytes, q35m_sna
 int q35m_snapshot_restore(q35m_ctx* ctx, int seq, const void* dev, size_t bytes,
                           q35m_snapshot_info* info);
 int q35m_kv_len(const q35m_ctx* ctx, int seq, int* length);
+/* Prefix reuse: KvCacheAlign.Plan (src/Qwen35Sharp.Model/KvCacheAlign.cs:
+ * 20-28, called by Qwen35Model.AlignPrompt, Qwen35Model.cs:224-229).  Keeps the
+ * longest common prefix of the token ids the sequence holds (cached) and the
+ * new prompt; when the prompt is cached whole, all but its last token, which
+ * is forwarded again so the caller gets fresh logits.  *truncate_to is the
+ * length to cut the sequence to, *suffix_start the first prompt token to
+ * forward (the two are equal).  A truncation moves the KV length only, as in
+ * the reference, so it leaves the DeltaNet state of the longer sequence: with
+ * n_snaps > 0 the plan covers the linear state too.  snap_lens holds the
+ * lengths of the caller's snapshots of the sequence (any order); *snap is the
+ * index of the longest one not past the kept prefix, or -1 when there is none
+ * (then the caller resets the sequence), and *truncate_to / *suffix_start move
+ * back to its length (0 with -1), so restoring that snapshot and forwarding
+ * prompt[*suffix_start..] continues from a consistent state.  With n_snaps = 0,
+ * *snap is -1 and the plan is the reference's.  No context, no device work;
+ * a negative count or a null pointer for a non-empty array is Q35M_ERR_INVALID. */
+int q35m_reuse_plan(const int* cached, int n_cached, const int* prompt, int n_prompt,
+                    const int* snap_lens, int n_snaps, int* truncate_to, int* suffix_start, int* snap);
 
 /* ---- weights (host -> HBM once; Qwen35Model.LoadWeights F32 tensors,
  *      Qwen35Model.cs:468-474) --------------------------------------------- */

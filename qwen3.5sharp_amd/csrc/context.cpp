@@ -770,6 +770,36 @@ int q35m_snapshot_restore(q35m_ctx* ctx, int seq, const void* dev, size_t bytes,
     return Q35M_OK;
 }
 
+int q35m_reuse_plan(const int* cached, int n_cached, const int* prompt, int n_prompt,
+                    const int* snap_lens, int n_snaps, int* truncate_to, int* suffix_start, int* snap) {
+    if (n_cached < 0 || n_prompt < 0 || n_snaps < 0)
+        return fail(Q35M_ERR_INVALID, "negative count (cached %d, prompt %d, snapshots %d)", n_cached, n_prompt,
+                    n_snaps);
+    if ((n_cached && !cached) || (n_prompt && !prompt) || (n_snaps && !snap_lens) || !truncate_to ||
+        !suffix_start || !snap)
+        return fail(Q35M_ERR_INVALID, "null pointer");
+    // KvCacheAlign.Plan: an empty prompt keeps nothing; a prompt cached whole
+    // keeps all but its last token; otherwise the common prefix.
+    int keep = 0;
+    if (n_prompt > 0) {
+        const int n = n_cached < n_prompt ? n_cached : n_prompt;
+        int common = 0;
+        while (common < n && cached[common] == prompt[common]) ++common;
+        keep = common == n_prompt ? n_prompt - 1 : common;
+    }
+    int best = -1;
+    if (n_snaps > 0) {
+        for (int i = 0; i < n_snaps; ++i)
+            if (snap_lens[i] >= 0 && snap_lens[i] <= keep && (best < 0 || snap_lens[i] > snap_lens[best]))
+                best = i;
+        keep = best < 0 ? 0 : snap_lens[best];
+    }
+    *truncate_to = keep;
+    *suffix_start = keep;
+    *snap = best;
+    return Q35M_OK;
+}
+
 int q35m_add_rmsnorm(q35m_ctx* ctx, float* hidden, const float* delta, const float* weight, float* y, void* q8,
                      int dim, int tokens, float eps) {
     int r = check_ctx(ctx);

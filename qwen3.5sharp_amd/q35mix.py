@@ -91,7 +91,20 @@ def lib() -> ctypes.CDLL:
                                            ctypes.c_int, ctypes.c_int]
         _lib.q35m_q8k_bytes.restype = ctypes.c_size_t
         _lib.q35m_q8k_bytes.argtypes = [ctypes.c_int, ctypes.c_int]
+        _lib.q35m_reuse_plan.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_int,
+                                         ctypes.c_void_p, ctypes.c_int] + [ctypes.POINTER(ctypes.c_int)] * 3
     return _lib
+
+
+def reuse_plan(cached, prompt, snap_lens=()):
+    """(truncate_to, suffix_start, snapshot index or -1) of q35m_reuse_plan
+    (KvCacheAlign.Plan, extended to the caller's snapshot lengths)."""
+    arrs = [np.ascontiguousarray(np.asarray(a, dtype=np.int32)) for a in (cached, prompt, snap_lens)]
+    ptr = lambda a: ctypes.c_void_p(a.ctypes.data) if a.size else None  # noqa: E731
+    out = [ctypes.c_int(-7) for _ in range(3)]
+    check(lib().q35m_reuse_plan(ptr(arrs[0]), arrs[0].size, ptr(arrs[1]), arrs[1].size, ptr(arrs[2]),
+                                arrs[2].size, *[ctypes.byref(o) for o in out]))
+    return tuple(o.value for o in out)
 
 
 def check(code: int) -> None:

@@ -215,3 +215,46 @@ def test_grow_extends_rope_table():
     assert rel(a.state_read(1, 0, q35mix.STATE_KEYS, 4102)[4100:], ref.ck[4100:4102]) <= TOL
     a.close()
     b.close()
+
+
+def test_prefix_reuse_plan_with_snapshots():
+    """Prompt reuse as Qwen35Model.AlignPrompt does it (KvCacheAlign.Plan),
+    with the linear state rolled back too: a sequence holding tokens 10..17
+    (snapshots at lengths 3 and 6), then the prompt 10..14, 20, 21.  The
+    reference's plan keeps 5 tokens; q35m_reuse_plan picks the snapshot at 3,
+    and restoring it and decoding prompt[3:] matches the oracle run of the
+    prompt from scratch at every step, while truncating to 5 alone (the
+    reference's TruncateCache) would keep the state of all 8 cached tokens."""
+    say("prefix reuse with snapshots")
+    xd = synth.deltanet_inputs(16, NK, NV, 128, salt=91)
+    xa = synth.attn_inputs(16, NH, NKV, HD, salt=92)
+    row = lambda tok: tok - 10   # noqa: E731  (token id -> its input row)
+    c = make_ctx(64)
+    cached = list(range(10, 18))
+    snaps = {}
+    ref = OracleSeq(64)
+    for i, tok in enumerate(cached):
+        step(c, 0, xd, xa, row(tok), ref)
+        if i + 1 in (3, 6):
+            snaps[i + 1] = c.snapshot_save(0)
+    st_after_cached = c.state_read(0, 0, q35mix.STATE_RECURRENT)
+    prompt = [10, 11, 12, 13, 14, 20, 21]
+    assert q35mix.reuse_plan(cached, prompt)[:2] == (5, 5)
+    lens = sorted(snaps)
+    keep, start, idx = q35mix.reuse_plan(cached, prompt, lens)
+    assert (keep, start) == (3, 3) and lens[idx] == 3
+    buf, info = snaps[lens[idx]]
+    c.snapshot_restore(0, buf, info)
+    assert c.kv_len(0) == 3
+    # The oracle from scratch over the prompt: its first 3 tokens, then the rest.
+    fresh = OracleSeq(64)
+    for tok in prompt[:start]:
+        fresh.step(xd, xa, row(tok))
+    assert rel(c.state_read(0, 0, q35mix.STATE_RECURRENT), fresh.st) <= TOL
+    assert not bits_equal(c.state_read(0, 0, q35mix.STATE_RECURRENT), st_after_cached)
+    for tok in prompt[start:]:
+        step(c, 0, xd, xa, row(tok), fresh)
+    assert c.kv_len(0) == len(prompt)
+    for b, _ in snaps.values():
+        b.free()
+    c.close()
