@@ -2,7 +2,7 @@
 the oracle: the gated GQA layer with 1, 2, 8 and 16 q heads per kv head
 (ModelConfig.NumHeads / NumKvHeads, ModelConfig.cs:19-31, are free in the
 reference; the 4B shape has 4), decode over every split of the cached rows
-and prefill with a continuation; and the Gated-DeltaNet layer with 1 and 4
+(batch 1 at 8192 rows included) and prefill with a continuation; and the Gated-DeltaNet layer with 1 and 4
 v-heads per k-head (SsmTimeStepRank / SsmGroupCount), decode and prefill.
 
 Tolerance: max|gpu - oracle| / max|oracle| <= 1e-4 per tensor (fp32); V rows
@@ -89,6 +89,44 @@ def test_attention_group_sizes(nh, nkv):
             start += T
         assert rel(c.state_read(0, 3, q35mix.STATE_KEYS, start), ck[:start]) <= TOL
         np.testing.assert_array_equal(c.state_read(0, 3, q35mix.STATE_VALUES, start), cv[:start])
+
+
+@pytest.mark.parametrize("nh,nkv", [(4, 4), (8, 4), (16, 2), (32, 2)])
+def test_attention_group_sizes_batch1_long(nh, nkv):
+    """Batch-1 decode at 8192 cached rows in each geometry: the split of 4
+    pipelined 16-row sub-chunks per workgroup (asserted through the kernel
+    timers), for 1, 2 and 8 q heads a workgroup and a group of 16 taken as two
+    head groups of 8; output, new K row and V row against the oracle."""
+    g = nh // nkv
+    say(f"GQA geometry batch 1 long: {nh} q heads, {nkv} kv heads (group {g})")
+    d = oracle.dims(n_heads=nh, n_kv_heads=nkv)
+    kv_dim = nkv * HD
+    cfg = q35mix.qwen35_config(num_layers=1, num_heads=nh, num_kv_heads=nkv, is_recurrent=[0])
+    L = 8192
+    with q35mix.Context(cfg, n_seqs=1, kv_capacity=L + 1) as c:
+        w = synth.attn_weights(HD, salt=50 + g)
+        c.set_attn_weights(0, w)
+        k, v = synth.kv_prefill(L + 1, kv_dim, salt=500 + g)
+        c.state_write(0, 0, q35mix.STATE_KEYS, k[:L])
+        c.state_write(0, 0, q35mix.STATE_VALUES, v[:L])
+        c.advance(0, L)
+        x = synth.attn_inputs(1, nh, nkv, HD, salt=600 + g)
+        out = c.array((1, nh * HD))
+        c.profile(True)
+        c.attn_decode(0, [0], c.array((1, 2 * nh * HD), x["q_gate"]), c.array((1, kv_dim), x["k"]),
+                      c.array((1, kv_dim), x["v"]), out)
+        ran = [n for n in c.profile_read() if n.startswith("attn_decode_partial<")]
+        c.profile(False)
+        assert ran == ["attn_decode_partial<4,16>"], ran
+        ck = np.zeros((L + 1, kv_dim), np.float32)
+        cv = np.zeros_like(ck)
+        ck[:L], cv[:L] = k[:L], v[:L]
+        ref, ck2, cv2 = oracle.attn_decode(d, L, x["q_gate"][0], x["k"][0], x["v"][0], w, ck, cv, n_threads=8)
+        e = rel(out.download()[0], ref)
+        say(f"  decode len {L}: out rel err {e:.2e}")
+        assert e <= TOL
+        assert rel(c.state_read(0, 0, q35mix.STATE_KEYS, L + 1)[L], ck2[L]) <= TOL
+        np.testing.assert_array_equal(c.state_read(0, 0, q35mix.STATE_VALUES, L + 1)[L], cv2[L])
 
 
 @pytest.mark.parametrize("nk,nv", [(16, 16), (8, 32)])
