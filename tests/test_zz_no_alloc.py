@@ -3,7 +3,10 @@ the library's fixed device scratch instead of an allocated workspace)
 against q35m_attn_decode on the same state, through the C ABI: bit-identical
 outputs and new cache rows on two calls in a row, the second with a smaller
 batch and shorter contexts; both also within 1e-4 of the oracle; a batch
-whose partials would not fit the scratch is refused with Q35M_ERR_CAPACITY."""
+whose partials would not fit the scratch is refused with Q35M_ERR_CAPACITY;
+and the entry point captured into a HIP graph replays bit-identically to the
+eager call."""
+import ctypes
 import sys
 
 import numpy as np
@@ -91,3 +94,45 @@ def test_noalloc_refuses_batches_beyond_the_scratch():
         say(f"refused: {e.value}")
         c.attn_decode(0, list(range(n)), qg, kk, vv, out)
         assert np.isfinite(out.download()).all()
+
+
+def test_noalloc_under_graph_capture():
+    """The no-allocation entry point captured into a HIP graph on the
+    context's stream: three replays, with eager copies and synchronisations
+    between them, each equal bit for bit to the eager call (same inputs, same
+    position: the same new cache row and output)."""
+    hip = q35mix.hip()
+    L = 3000
+    with q35mix.Context(q35mix.qwen35_config(num_layers=1, is_recurrent=[0]), n_seqs=1, kv_capacity=L + 1) as c:
+        c.set_attn_weights(0, synth.attn_weights(HD, salt=8))
+        k, v = synth.kv_prefill(L, KV_DIM, salt=9)
+        c.state_write(0, 0, q35mix.STATE_KEYS, k)
+        c.state_write(0, 0, q35mix.STATE_VALUES, v)
+        c.advance(0, L)
+        x = synth.attn_inputs(1, NH, NKV, HD, salt=10)
+        qg, kk, vv = c.array((1, 2 * c.q_dim), x["q_gate"]), c.array((1, c.kv_dim), x["k"]), \
+            c.array((1, c.kv_dim), x["v"])
+        out = c.array((1, c.q_dim))
+        c.attn_decode_noalloc(0, [0], qg, kk, vv, out)
+        c.sync()
+        ref = out.download()
+        stream = ctypes.c_void_p(c.stream)
+        graph, exe = ctypes.c_void_p(), ctypes.c_void_p()
+        assert hip.hipStreamBeginCapture(stream, 0) == 0          # hipStreamCaptureModeGlobal
+        try:
+            c.attn_decode_noalloc(0, [0], qg, kk, vv, out)
+        finally:
+            r_end = hip.hipStreamEndCapture(stream, ctypes.byref(graph))
+        assert r_end == 0
+        assert hip.hipGraphInstantiate(ctypes.byref(exe), graph, None, None, ctypes.c_size_t(0)) == 0
+        try:
+            for rep in range(3):
+                out.upload(np.zeros((1, c.q_dim), np.float32))    # eager work between replays
+                c.sync()
+                assert hip.hipGraphLaunch(exe, stream) == 0
+                c.sync()
+                got = out.download()
+                assert bits_equal(got, ref), rep
+        finally:
+            hip.hipGraphExecDestroy(exe)
+            hip.hipGraphDestroy(graph)
