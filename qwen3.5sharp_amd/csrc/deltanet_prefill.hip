@@ -292,14 +292,19 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep(
         for (int j = 0; j < 32; ++j) Ks[32 * hq + j][cq] = y[j];
         lds_barrier();
         {
-            const int row = tid >> 2, part = tid & 3;
+            // Lanes l, l + 16, l + 32, l + 48 of a wave take the four quarters
+            // of one row (16 rows a wave), so the 16 lanes of each LDS read
+            // pass touch 16 rows at one column offset: no bank conflicts.
+            // The quarter sums combine as (p0 + p1) + (p2 + p3).
+            const int row = (tid & 15) + 16 * wave, part = lane >> 4;
             float acc = 0.0f;
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 const float4 v = *reinterpret_cast<const float4*>(&Ks[row][32 * part + 4 * e]);
                 acc += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
             }
-            acc = group_sum<4>(acc);
+            acc = xor16_sum(acc);
+            acc = xor32_sum(acc);
             if (part == 0) nrm[row] = __builtin_amdgcn_rsqf(acc + eps);   // 1 / |x|
         }
         lds_barrier();
