@@ -256,17 +256,35 @@ def bench_boundary(dim, tokens, steps, warmup):
     return ms, kt, 16 * tokens * dim + 4 * dim + q35mix.lib().q35m_q8k_bytes(dim, tokens)
 
 
-def bench_stack(n_steps=128, warmup=4, n_seqs=8, ctx_len=32768, n_layers=32):
-    """32-layer mixer stack, 8 sequences decoding from context 32640 to 32768."""
-    is_rec = [(i + 1) % 4 != 0 for i in range(n_layers)]
-    ctx = q35mix.Context(q35mix.qwen35_config(num_layers=n_layers, is_recurrent=is_rec), n_seqs,
-                         ctx_len)
-    start = ctx_len - n_steps
-    # Pre-filled KV rows ~N(0,1) (a 16 MiB block of normals tiled over the cache).
-    block = synth.normal(1234, 4 << 20)
+def memcpy_d2d(ctx, dst_ptr, src_ptr, nbytes):
+    hip = q35mix.hip()
+    hip.hipMemcpyAsync.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int,
+                                   ctypes.c_void_p]
+    r = hip.hipMemcpyAsync(ctypes.c_void_p(dst_ptr), ctypes.c_void_p(src_ptr), nbytes, 3,
+                           ctypes.c_void_p(ctx.stream))
+    if r != 0:
+        raise RuntimeError(f"hipMemcpyAsync failed: {r}")
+
+
+def bench_decode_stack(is_rec, n_seqs, start, n_steps, warmup=4, eager=True, n_sets=8):
+    """Decode steps of a mixer stack (layer l is Gated-DeltaNet when is_rec[l],
+    GQA otherwise) for n_seqs sequences from context `start`, n_steps tokens.
+
+    Timed two ways over the same inputs: (1) the whole step captured once as
+    a decode graph (q35m_decode_graph_create) and replayed per token; its
+    inputs sit in one fixed staging block, and each step first copies one of
+    n_sets pre-generated input images into it (one device-to-device copy of
+    every layer's inputs, inside the timed region; timed alone too); (2) the
+    per-layer entry points called one by one (q35m_deltanet_decode /
+    q35m_attn_decode, then q35m_advance per sequence), reading the images
+    directly.  Lengths are put back to `start` before each timed pass."""
+    L = len(is_rec)
+    cap = start + n_steps
+    ctx = q35mix.Context(q35mix.qwen35_config(num_layers=L, is_recurrent=is_rec), n_seqs, cap)
+    block = synth.normal(1234, 4 << 20)       # KV rows ~N(0,1): a 16 MiB block of normals tiled
     wd, wa = synth.deltanet_weights(NK, NV, DK), synth.attn_weights(HD)
     st = synth.deltanet_state(NK, NV, DK)
-    for layer in range(n_layers):
+    for layer in range(L):
         if is_rec[layer]:
             ctx.set_deltanet_weights(layer, wd)
             for s in range(n_seqs):
@@ -276,62 +294,121 @@ def bench_stack(n_steps=128, warmup=4, n_seqs=8, ctx_len=32768, n_layers=32):
             ctx.set_attn_weights(layer, wa)
             for s in range(n_seqs):
                 for kind in (q35mix.STATE_KEYS, q35mix.STATE_VALUES):
-                    # The whole head-major [kv_heads][capacity][256] block of the
-                    # (layer, seq) gets data (rows past `start` are rewritten by decode).
+                    # the whole head-major [kv_heads][capacity][256] block of the (layer, seq)
                     ptr, nbytes = ctx.state_device_ptr(layer, s, kind)
-                    fill = nbytes
                     off = 0
-                    while off < fill:
-                        n = min(block.nbytes, fill - off)
-                        q35mix.check(q35mix.lib().q35m_copy_h2d(ctx.handle, ptr + off,
-                                                                block.ctypes.data, n))
+                    while off < nbytes:
+                        n = min(block.nbytes, nbytes - off)
+                        q35mix.check(q35mix.lib().q35m_copy_h2d(ctx.handle, ptr + off, block.ctypes.data, n))
                         off += n
-    for s in range(n_seqs):
-        ctx.advance(s, start)
-    seqs = list(range(n_seqs))
-    # Eight distinct input sets, cycled over (step, layer).
-    pools = []
-    for j in range(8):
+    # One input image: every layer's inputs, contiguous.
+    shapes = []
+    for layer in range(L):
+        if is_rec[layer]:
+            shapes.append([(n_seqs, CONV_DIM), (n_seqs, VALUE_DIM), (n_seqs, NV), (n_seqs, NV)])
+        else:
+            shapes.append([(n_seqs, 2 * Q_DIM), (n_seqs, KV_DIM), (n_seqs, KV_DIM)])
+    offs, total = [], 0
+    for shp in shapes:
+        o = []
+        for sh in shp:
+            o.append(total)
+            total += int(np.prod(sh))
+        offs.append(o)
+    sets = []
+    for j in range(n_sets):
         xd = synth.deltanet_inputs(n_seqs, NK, NV, DK, salt=500 + j)
         xa = synth.attn_inputs(n_seqs, NH, NKV, HD, salt=600 + j)
-        pools.append((
-            [ctx.array((n_seqs, CONV_DIM), xd["qkv"]), ctx.array((n_seqs, VALUE_DIM), xd["z"]),
-             ctx.array((n_seqs, NV), xd["b"]), ctx.array((n_seqs, NV), xd["a"])],
-            [ctx.array((n_seqs, 2 * Q_DIM), xa["q_gate"]), ctx.array((n_seqs, KV_DIM), xa["k"]),
-             ctx.array((n_seqs, KV_DIM), xa["v"])]))
-    out_d = ctx.array((n_seqs, VALUE_DIM))
-    out_a = ctx.array((n_seqs, Q_DIM))
+        sets.append(([xd["qkv"], xd["z"], xd["b"], xd["a"]], [xa["q_gate"], xa["k"], xa["v"]]))
+    images = []
+    for j in range(n_sets):
+        host = np.empty(total, np.float32)
+        for layer in range(L):
+            xs = sets[(j * L + layer) % n_sets][0 if is_rec[layer] else 1]
+            for o, x in zip(offs[layer], xs):
+                host[o:o + x.size] = x.ravel()
+        images.append(ctx.array((total,), host))
+    stage = ctx.array((total,))
+    outs = [ctx.array((n_seqs, VALUE_DIM if is_rec[layer] else Q_DIM)) for layer in range(L)]
 
-    def one_step(step):
-        for layer in range(n_layers):
-            pd, pa = pools[(step * n_layers + layer) % 8]
+    def views(img):
+        return [[q35mix.DeviceView(img, o, sh) for o, sh in zip(offs[layer], shapes[layer])]
+                for layer in range(L)]
+    stage_v = views(stage)
+    img_v = [views(img) for img in images]
+    io = [tuple(stage_v[layer]) + ((None,) if not is_rec[layer] else ()) + (outs[layer],) for layer in range(L)]
+    seqs = list(range(n_seqs))
+    for s in seqs:
+        ctx.advance(s, start)
+
+    def rewind():
+        ctx.sync()
+        for s in seqs:
+            ctx.truncate(s, start)
+
+    g = q35mix.DecodeGraph(ctx, seqs, io, cap)
+
+    def graph_step(i):
+        memcpy_d2d(ctx, stage.ptr, images[i % n_sets].ptr, total * 4)
+        g.run(replay=True)
+
+    def eager_step(i):
+        v = img_v[i % n_sets]
+        for layer in range(L):
             if is_rec[layer]:
-                ctx.deltanet_decode(layer, seqs, *pd, out_d)
+                ctx.deltanet_decode(layer, seqs, *v[layer], outs[layer])
             else:
-                ctx.attn_decode(layer, seqs, *pa, out_a)
+                ctx.attn_decode(layer, seqs, *v[layer], outs[layer])
         for s in seqs:
             ctx.advance(s, 1)
 
-    for i in range(warmup):
-        one_step(i)
-    ctx.sync()
-    for s in seqs:
-        ctx.truncate(s, start)
+    def timed(fn):
+        for i in range(warmup):
+            fn(i)
+        rewind()
+        e0, e1 = q35mix.Event(), q35mix.Event()
+        e0.record(ctx.stream)
+        for i in range(n_steps):
+            fn(i)
+        e1.record(ctx.stream)
+        ms = e0.elapsed_ms(e1)
+        rewind()
+        return ms
+
+    res = {"graph_ms": timed(graph_step)}
+    # the staging copies alone
     e0, e1 = q35mix.Event(), q35mix.Event()
     e0.record(ctx.stream)
     for i in range(n_steps):
-        one_step(i)
+        memcpy_d2d(ctx, stage.ptr, images[i % n_sets].ptr, total * 4)
     e1.record(ctx.stream)
-    ms = e0.elapsed_ms(e1)
-    for s in seqs:
-        ctx.truncate(s, start)
-    kt = kernel_times(ctx, one_step, 4)
+    res["staging_ms"] = e0.elapsed_ms(e1)
+    res["staging_bytes_per_step"] = 2 * total * 4
+    if eager:
+        res["eager_ms"] = timed(eager_step)
+    # Per-kernel times: the graph's launches issued one by one with the timers on.
+    ctx.profile(True)
+    for i in range(4):
+        g.run(replay=False)
+    kt = ctx.profile_read()
+    ctx.profile(False)
+    rewind()
+    res["kernels"] = {k: (ms / n, n / 4) for k, (ms, n) in kt.items()}
+    g.close()
     ctx.close()
-    bytes_total = 0
+    by = 0
+    n_dn = sum(1 for r in is_rec if r)
+    n_at = L - n_dn
     for i in range(n_steps):
-        kv_len = start + i + 1
-        bytes_total += n_seqs * (24 * DN_DECODE_BYTES + 8 * attn_decode_bytes(kv_len))
-    return ms, kt, bytes_total
+        by += n_seqs * (n_dn * DN_DECODE_BYTES + n_at * attn_decode_bytes(start + i + 1))
+    res["bytes"] = by
+    return res
+
+
+def bench_stack(n_steps=128, warmup=4, n_seqs=8, ctx_len=32768, n_layers=32):
+    """32-layer mixer stack, 8 sequences decoding from context 32640 to 32768."""
+    is_rec = [(i + 1) % 4 != 0 for i in range(n_layers)]
+    return bench_decode_stack(is_rec, n_seqs, ctx_len - n_steps, n_steps, warmup)
 
 
 # --------------------------------------------------------------------------
@@ -503,7 +580,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--only", default="", help="comma list of: dn_prefill,dn_decode,attn_decode,"
-                                               "attn_prefill,linear_q,stack,peaks")
+                                               "attn_prefill,linear_q,boundary,stack,stack_b1,peaks")
     ap.add_argument("--stack-steps", type=int, default=128,
                     help="decode steps of the mixer-stack workload (the context ends at 32768 rows)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -677,11 +754,18 @@ def main():
     if want("stack"):
         ns = args.stack_steps
         log(f"[bench] 32-layer mixer stack, 8 seqs x ctx 32768, {ns} decode steps ...")
-        ms, kt, by = bench_stack(n_steps=ns)
+        r = bench_stack(n_steps=ns)
+        ms, by = r["graph_ms"], r["bytes"]
         workloads["stack_decode_8x32k"] = {
             "us_per_token": ms * 1e3 / (ns * 8), "ms_per_step": ms / ns, "steps": ns,
+            "timing": "one decode graph (24 DeltaNet + 8 GQA mixers and the length advance) captured once and "
+                      "replayed per token; each step first copies its inputs into the graph's staging block "
+                      "(included; staging_us_per_step alone)",
             "hbm_frac": by / (ms / 1e3) / HBM_PEAK, "gb_per_step": by / ns / 1e9,
-            "kernels_us": {k: v[0] * 1e3 for k, v in kt.items()}}
+            "staging_us_per_step": r["staging_ms"] * 1e3 / ns,
+            "eager_us_per_token": r["eager_ms"] * 1e3 / (ns * 8),
+            "eager_hbm_frac": by / (r["eager_ms"] / 1e3) / HBM_PEAK,
+            "kernels_us": {k: v[0] * 1e3 for k, v in r["kernels"].items()}}
         if not args.no_cpu:
             log("[bench] CPU restatement, 4 steps of the stack ...")
             us, sec = cpu_baseline_stack(threads)
@@ -691,6 +775,43 @@ def main():
                           f"extrapolated linearly to 128 steps; DeltaNet on one thread, attention on "
                           f"{threads} workers ({cpu_desc})"}
         log(f"[bench] stack: {workloads['stack_decode_8x32k']}")
+
+    if want("stack_b1"):
+        ns = args.stack_steps
+        is_rec = [(i + 1) % 4 != 0 for i in range(32)]
+        log(f"[bench] 32-layer mixer stack, batch 1 from ctx 8192, {ns} decode steps ...")
+        r = bench_decode_stack(is_rec, 1, 8192, ns)
+        ms, by = r["graph_ms"], r["bytes"]
+        workloads["stack_decode_b1_8k"] = {
+            "us_per_token": ms * 1e3 / ns, "steps": ns,
+            "timing": "decode graph of the 32 layers replayed per token (staging copy included), contexts "
+                      "8193 to 8320 rows",
+            "hbm_frac": by / (ms / 1e3) / HBM_PEAK, "mb_per_token": by / ns / 1e6,
+            "staging_us_per_step": r["staging_ms"] * 1e3 / ns,
+            "eager_us_per_token": r["eager_ms"] * 1e3 / ns,
+            "eager_hbm_frac": by / (r["eager_ms"] / 1e3) / HBM_PEAK,
+            "kernels_us": {k: v[0] * 1e3 for k, v in r["kernels"].items()}}
+        log(f"[bench] stack b1: {workloads['stack_decode_b1_8k']}")
+        # One mixer kind per graph, per layer: DeltaNet decode (160 layers, so
+        # the states exceed the MALL) and GQA decode at 8193-8320 rows.
+        log("[bench] per-layer decode in a graph: 160 DeltaNet layers, batch 1 ...")
+        r = bench_decode_stack([True] * 160, 1, 0, ns)
+        per = (r["graph_ms"] - r["staging_ms"]) * 1e3 / (ns * 160)
+        workloads.setdefault("deltanet_decode_b1", {}).update({
+            "graph_us_per_layer": per, "graph_hbm_frac": DN_DECODE_BYTES / (per / 1e6) / HBM_PEAK,
+            "graph_timing": "160-layer decode graph replayed 128 times; (time - staging copies) / 160 layers",
+            "eager_us_per_layer_in_loop": r["eager_ms"] * 1e3 / (ns * 160)})
+        log(f"[bench] DeltaNet decode per layer in a graph: {per:.2f} us")
+        log("[bench] per-layer decode in a graph: 8 GQA layers at 8193-8320 rows, batch 1 ...")
+        r = bench_decode_stack([False] * 8, 1, 8192, ns)
+        per = (r["graph_ms"] - r["staging_ms"]) * 1e3 / (ns * 8)
+        workloads.setdefault("attn_decode_8193", {}).update({
+            "graph_us_per_layer": per,
+            "graph_hbm_frac": (r["bytes"] / (ns * 8)) / (per / 1e6) / HBM_PEAK,
+            "graph_timing": "8-layer decode graph replayed 128 times (rows 8193-8320); "
+                            "(time - staging copies) / 8 layers",
+            "eager_us_per_layer_in_loop": r["eager_ms"] * 1e3 / (ns * 8)})
+        log(f"[bench] GQA decode per layer in a graph: {per:.2f} us")
 
     if result is None:
         result = {"metric": "token-mixer µs/token decode + % HBM peak; prefill tokens/s @T=2048",

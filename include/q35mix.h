@@ -10,12 +10,14 @@
  * and the K/V cache of every full-attention layer (the reference's
  * [capacity][kv_heads*head_dim] rows, held head-major on the device), per
  * sequence.  Around the mixers it also offers what the reference runs on
- * either side of them: the quantized projections (Q4_K / Q6_K weights,
- * activations quantized to Q8_K), the layer boundary (residual add +
- * zero-centred RMSNorm, optionally emitting Q8_K), KV growth and a
- * linear-state snapshot, and a GGUF reader that uploads the mixers' F32
- * weights.  Paths in citations are relative to the reference repository
- * root.
+ * either side of them: the projections over every weight type its dispatch
+ * knows (Q4_K, Q5_K, Q6_K, IQ4_XS, Q2_0C, STQ1_0 with activations quantized
+ * to Q8_K, and F32), the layer boundary (residual add + zero-centred
+ * RMSNorm, optionally emitting Q8_K), KV growth, a linear-state snapshot and
+ * prefix-reuse planning, a GGUF reader that uploads the mixers' F32 weights,
+ * and a whole decode step (every layer's mixer and the length advance)
+ * captured once into a HIP graph and replayed per token.  Paths in
+ * citations are relative to the reference repository root.
  *
  * Conventions
  *  - Every entry point returns an int status: Q35M_OK (0) or a negative
@@ -29,7 +31,9 @@
  *    may be driven from separate threads.
  *  - Positions follow the reference: every layer of a forward pass writes
  *    K/V at the sequence's current length, and q35m_advance() moves the
- *    length once per pass (Qwen35Model.cs:235, 287).
+ *    length once per pass (Qwen35Model.cs:235, 287).  The decode kernels
+ *    read the lengths from device memory, so a captured decode step (see
+ *    q35m_decode_graph_create) stays valid as they move.
  */
 #ifndef Q35MIX_H
 #define Q35MIX_H
@@ -112,24 +116,29 @@ int q35m_grow(q35m_ctx* ctx, int kv_capacity);
  * too (the reference cannot: TruncateCache moves the KV length only,
  * Qwen35Model.cs:214-222).  save copies sequence seq's DeltaNet state and
  * conv window of every linear layer into a device buffer of
- * q35m_snapshot_bytes() bytes and fills info (length, epoch); restore copies
- * them back and sets the length to info->kv_len.  K/V rows are not copied:
- * restore needs the rows below that length unchanged since the save, and
- * refuses (Q35M_ERR_RANGE) after a reset, a truncate below the current length,
- * a restore to a shorter length or a K/V state write of that sequence, and
- * when the sequence is shorter than the snapshot.  A restore that shortens the
- * sequence starts a new epoch (the rows above the restored length will be
- * written again, so snapshots taken at a longer length must no longer be
- * accepted) and writes it into *info, which keeps the snapshot just restored
- * usable.  Copies are asynchronous on the context stream. */
+ * q35m_snapshot_bytes() bytes and fills info (its length and a stamp of the
+ * save); restore copies them back into the same sequence and sets the length
+ * to info->kv_len.  K/V rows are not copied: restore needs the rows below
+ * that length unchanged since the save, i.e. the sequence never shorter than
+ * the snapshot since then, and refuses (Q35M_ERR_RANGE) a snapshot saved
+ * before a reset, a truncate or restore to a length below its own, or a K/V
+ * state write of that sequence, and one longer than the sequence.  Snapshots
+ * at or below every length the sequence was cut to stay restorable, the one
+ * just restored included, any number of times.  Copies are asynchronous on
+ * the context stream. */
 typedef struct q35m_snapshot_info {
     int kv_len;
-    unsigned int epoch;
+    unsigned int epoch;   /* stamp of the save in the sequence's history */
 } q35m_snapshot_info;
 size_t q35m_snapshot_bytes(const q35m_ctx* ctx);
 int q35m_snapshot_save(q35m_ctx* ctx, int seq, void* dev, size_t bytes, q35m_snapshot_info* info);
 int q35m_snapshot_restore(q35m_ctx* ctx, int seq, const void* dev, size_t bytes,
                           q35m_snapshot_info* info);
+/* Q35M_OK when q35m_snapshot_restore would accept the snapshot `info` of
+ * sequence seq now, Q35M_ERR_RANGE when it would refuse it.  No device work;
+ * a host keeping several snapshots passes only the accepted ones' lengths to
+ * q35m_reuse_plan. */
+int q35m_snapshot_valid(const q35m_ctx* ctx, int seq, const q35m_snapshot_info* info);
 int q35m_kv_len(const q35m_ctx* ctx, int seq, int* length);
 /* Prefix reuse: KvCacheAlign.Plan (src/Qwen35Sharp.Model/KvCacheAlign.cs:
  * 20-28, called by Qwen35Model.AlignPrompt, Qwen35Model.cs:224-229).  Keeps the
@@ -144,7 +153,8 @@ int q35m_kv_len(const q35m_ctx* ctx, int seq, int* length);
  * index of the longest one not past the kept prefix, or -1 when there is none
  * (then the caller resets the sequence), and *truncate_to / *suffix_start move
  * back to its length (0 with -1), so restoring that snapshot and forwarding
- * prompt[*suffix_start..] continues from a consistent state.  With n_snaps = 0,
+ * prompt[*suffix_start..] continues from a consistent state (pass only
+ * snapshots q35m_snapshot_valid accepts).  With n_snaps = 0,
  * *snap is -1 and the plan is the reference's.  No context, no device work;
  * a negative count or a null pointer for a non-empty array is Q35M_ERR_INVALID. */
 int q35m_reuse_plan(const int* cached, int n_cached, const int* prompt, int n_prompt,
@@ -197,8 +207,11 @@ int q35m_attn_decode(q35m_ctx* ctx, int layer, int n, const int* seqs, const flo
  * routine.  No counterpart in the reference.  The split-K partials go to a
  * fixed device array of Q35M_NOALLOC_SCRATCH_BYTES that the library holds
  * on every GPU it runs on until the process ends; a call that would need
- * more (roughly n * kv_heads * ceil(longest cached length / 512) * 16.5 KiB)
- * is refused with Q35M_ERR_CAPACITY.  Every call on one GPU shares that
+ * more is refused with Q35M_ERR_CAPACITY.  The partials take
+ * n * num_heads * nchunks * 1032 bytes, nchunks = ceil(longest cached length /
+ * 512) once the batch is large enough to split each cache into 8-sub-chunk
+ * workgroups (8 sequences at 32K rows: 8.5 MB); smaller batches split into
+ * fewer, shorter chunks and stay under about 2 MB.  Every call on one GPU shares that
  * array: calls that overlap on one GPU (other contexts or streams) race.
  * The per-kernel timers are not used by this entry point. */
 #define Q35M_NOALLOC_SCRATCH_BYTES ((size_t)16 << 20)
@@ -212,6 +225,47 @@ int q35m_attn_decode_noalloc(q35m_ctx* ctx, int layer, int n, const int* seqs, c
  * may reach 2097152 rows at most (Q35M_ERR_UNSUPPORTED beyond). */
 int q35m_attn_prefill(q35m_ctx* ctx, int layer, int seq, int T, const float* q_gate,
                       const float* k, const float* v, float* out);
+
+/* ---- one decode step of every layer, captured once, replayed per token ---- */
+
+/* Per-layer activations of a decode step, device pointers fixed for the life
+ * of the graph (each run reads the inputs found there and writes the outputs
+ * there).  DeltaNet layers take q35m_deltanet_decode's arguments: in0 = qkv
+ * [n][conv_dim], in1 = z [n][H_v*dv], in2 = b [n][H_v], in3 = a [n][H_v],
+ * out [n][H_v*dv].  Full-attention layers take q35m_attn_decode's: in0 = q_gate
+ * [n][heads*2*head_dim], in1 = k, in2 = v [n][kv_heads*head_dim], in3 unused,
+ * out [n][heads*head_dim]. */
+typedef struct q35m_decode_io {
+    const float* in0;
+    const float* in1;
+    const float* in2;
+    const float* in3;
+    float* out;
+} q35m_decode_io;
+
+typedef struct q35m_decode_graph q35m_decode_graph;
+
+/* The decode forward of one token for each of n sequences, mixers only
+ * (Qwen35Model.Forward, Qwen35Model.cs:231-291): every layer's mixer in layer
+ * order, as q35m_deltanet_decode / q35m_attn_decode run them, then every
+ * sequence's length advanced by one (`_cacheLen += seq`, :287), captured once
+ * into a HIP graph on the context stream (io: [num_layers] entries, seqs: HOST
+ * array of n distinct ids).  Replays read the lengths from the device, so one
+ * graph serves every token.  The attention split is chosen for lengths up to
+ * max_len rows (1 <= max_len <= the KV capacity); a run at which a sequence
+ * already holds max_len rows is refused (Q35M_ERR_CAPACITY).  The graph owns
+ * its split-K partials (allocated here); runs allocate nothing.  No
+ * counterpart in the reference, which has no device to capture for. */
+int q35m_decode_graph_create(q35m_ctx* ctx, int n, const int* seqs, const q35m_decode_io* io, int max_len,
+                             q35m_decode_graph** out);
+/* Enqueues one step on the context stream: replay != 0 launches the captured
+ * graph; replay == 0 issues the same kernel launches one by one (identical
+ * results; the per-kernel timers see them).  Advances the lengths the host
+ * reports (q35m_kv_len) as well.  Refused (Q35M_ERR_RANGE) once q35m_grow has
+ * moved the caches: create the graph again. */
+int q35m_decode_graph_run(q35m_decode_graph* g, int replay);
+/* Waits for the context stream, then frees the graph (before q35m_destroy). */
+int q35m_decode_graph_destroy(q35m_decode_graph* g);
 
 /* ---- GGUF weights (GgufFile, src/Qwen35Sharp.Gguf/GgufFile.cs:27-170) ---- */
 
@@ -250,10 +304,11 @@ int q35m_load_mixer_weights(q35m_ctx* ctx, const q35m_gguf* g, int num_layers, c
 int q35m_state_read(q35m_ctx* ctx, int layer, int seq, int kind, void* host, size_t bytes);
 int q35m_state_write(q35m_ctx* ctx, int layer, int seq, int kind, const void* host,
                      size_t bytes);
-/* Device address and size of one state buffer, for zero-copy callers.  The
- * conv window is double-buffered on the device (decode reads one buffer and
- * writes the shifted window to the other), so the Q35M_STATE_CONV address is
- * valid until the next q35m_deltanet_decode of that layer and sequence. */
+/* Device address and size of one state buffer, for zero-copy callers.  For
+ * Q35M_STATE_CONV it is the window in the reference layout; the decode also
+ * keeps one more copy of the q/k channels' windows per further v-head of a
+ * k-head (after that block), so write windows with q35m_state_write, which
+ * updates every copy, rather than through this address. */
 int q35m_state_device_ptr(q35m_ctx* ctx, int layer, int seq, int kind, void** dptr,
                           size_t* bytes);
 

@@ -54,12 +54,14 @@ __global__ __launch_bounds__(NT, 2) void attn_decode_partial(
     const float* __restrict__ vnew, const float* __restrict__ q_norm,
     const float* __restrict__ k_norm, float* __restrict__ k_cache, float* __restrict__ v_cache,
     const float* __restrict__ rope_cos, const float* __restrict__ rope_sin,
-    float* __restrict__ part_o, float* __restrict__ part_ml, int nkv, int ng, int cap, int nchunks,
-    float eps, SeqBatch sb) {
+    float* __restrict__ part_o, float* __restrict__ part_ml, const int* __restrict__ lens, int nkv, int ng,
+    int cap, int nchunks, float eps, SeqBatch sb) {
     constexpr int QPW = (HPW + 3) / 4;       // q heads of the group per wave in per-head phases
     const int c = blockIdx.x, y = blockIdx.y, i = blockIdx.z;
     const int kvh = y / ng;                  // head group y: q heads HPW y .. HPW y + HPW - 1
-    const int pos = sb.pos[i];               // cached rows [0, pos); the new row is pos
+    // Cached rows [0, pos); the new row is pos.  The host keeps every length
+    // below the capacity; the clamp only keeps the row addresses in the cache.
+    const int pos = min(lens[sb.seq[i]], cap - 1);
     const bool has_rows = c * R < pos;       // uniform
     const bool owner = c == 0;               // holds the new row
     const bool writer = owner && y % ng == 0;   // one group per kv head writes it to the cache
@@ -362,12 +364,12 @@ constexpr int MU = 4;                      // chunks per thread per round
 
 __global__ __launch_bounds__(MT) void attn_decode_merge(
     const float* __restrict__ part_o, const float* __restrict__ part_ml,
-    const float* __restrict__ q_gate, float* __restrict__ out, int nh, int hpw, int nchunks, int rows,
-    SeqBatch sb) {
+    const float* __restrict__ q_gate, float* __restrict__ out, const int* __restrict__ lens, int nh, int hpw,
+    int nchunks, int rows, int cap, SeqBatch sb) {
     const int h = blockIdx.x / (kHd / MSLICE), slice = blockIdx.x % (kHd / MSLICE);
     const int i = blockIdx.y, t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int y = h / hpw, hl = h % hpw;     // head group of the partials
-    const int pos = sb.pos[i];
+    const int pos = min(lens[sb.seq[i]], cap - 1);
     const int nc = max(1, min(nchunks, (pos + rows - 1) / rows));   // chunks that ran
     const size_t base = ((size_t)i * (nh / hpw) + y) * nchunks;
     __shared__ float4 obuf[4][MD4];
@@ -428,22 +430,8 @@ __global__ __launch_bounds__(MT) void attn_decode_merge(
     }
 }
 
-// Sub-chunks of `rows` rows in the longest cached range in the batch.
-int max_subchunks(const SeqBatch& sb, int rows) {
-    int m = 0;
-    for (int i = 0; i < sb.n; ++i) m = max(m, (sb.pos[i] + rows - 1) / rows);
-    return m;
-}
-
-// Sub-chunks per workgroup: the fewest that keep the grid within one round of
-// resident workgroups (2 per CU), at most 8 (beyond, longer workgroups were
-// not faster, and the partials stay small next to the cache they summarise).
-int pick_nsub(int n, int groups, int max_subs, int n_cu) {
-    const long slots = 2L * n_cu;
-    for (int ns = 1; ns < 8; ns <<= 1)
-        if ((long)n * groups * max(1, (max_subs + ns - 1) / ns) <= slots) return ns;
-    return 8;
-}
+// Sub-chunks of `rows` rows in a cached range of max_cached rows.
+int max_subchunks(int max_cached, int rows) { return (max_cached + rows - 1) / rows; }
 
 // q heads per workgroup: the whole group of a kv head up to 8 (1, 2, 4 or 8),
 // groups of 8 beyond (each re-reads the kv head's cache).
@@ -453,30 +441,45 @@ int heads_per_wg(const Dims& d) {
 }
 
 // Split of one call: rows per sub-chunk, sub-chunks per workgroup (NSUB),
-// workgroups per head group (chunks).  When one 64-row sub-chunk a workgroup
-// would already give at least one workgroup per CU (batch 1 at long contexts,
-// the 8192-row case among them), the same rows go as 4 sub-chunks of 16 rows
-// instead: each workgroup then holds one 16-row sub-chunk's loads in flight
-// at a time, refilled by the software pipeline, instead of all 64 rows at once
-// (measured at 8193 rows: 14.0 vs 15.6 us for the partial kernel; 32-row
-// sub-chunks 14.5 us; all 64 rows loaded up front as 4 register sets 17.6 us;
-// twice or four times the workgroups with fewer sub-chunks each slower still).
-struct DecodePlan {
-    int rows, nsub, nchunks;
-};
-
-DecodePlan plan_decode(const Dims& d, const SeqBatch& sb, int n_cu) {
-    const int groups = d.nh / heads_per_wg(d);
-    const int max64 = max_subchunks(sb, SUB);
-    const int nsub = pick_nsub(sb.n, groups, max64, n_cu);
-    if (nsub == 1 && (long)sb.n * groups * max64 >= n_cu) {
-        const int max16 = max_subchunks(sb, SUB / 4);
-        return {SUB / 4, 4, max(1, (max16 + 3) / 4)};
-    }
-    return {SUB, nsub, max(1, (max64 + nsub - 1) / nsub)};
+// workgroups per head group (chunks), for ng = sequences x head groups and
+// the longest cached range.  Two workgroups fit a CU (slots = 2 x CUs):
+//  - fewer 64-row sub-chunks than CUs in all: one sub-chunk a workgroup;
+//  - else 16-row sub-chunks spread over one round of workgroups (slots / ng
+//    per head group), when at most 8 per workgroup cover the rows: each
+//    workgroup holds one 16-row sub-chunk's loads in flight at a time,
+//    refilled by the software pipeline, instead of 64 rows at once.  Up to 4
+//    a workgroup, the rows go as 4 per workgroup (fewer, longer workgroups);
+//  - else 64-row sub-chunks, 4 a workgroup if that keeps one round, else 8.
+// Measured per call, partial + merge, batch 1 unless stated: 8193 rows 17.9 us
+// as 4 x 16 rows (15.6 us partial as 1 x 64 before: 19.5 us); 8320 rows 19.5
+// us as 8 x 16 (2 x 64 rows: 24.5, 1 x 64: 21.7); 12288 rows 22.9 (2 x 64:
+// 26.3); 16384 rows 28.0 (4 x 64: 28.2, 2 x 64: 28.9); two sequences at 8192
+// rows 28.0 (2 x 64: 28.7); four at 4096 rows 28.3 (4 x 64: 28.3, 2 x 64:
+// 29.0); 32767 rows 47.8 as 4 x 64 (8 x 64: 46.7, 8 x 16: 49.4).  For the
+// 8-sequence 32K stack, 16 sub-chunks of 32 rows or 32 of 16 measured
+// 332-334 against 327 us as 8 x 64.
+DecodePlan plan_decode(const Dims& d, int n, int max_cached, int n_cu) {
+    const long ng = (long)n * (d.nh / heads_per_wg(d));
+    const long slots = 2L * n_cu;
+    const int max64 = max_subchunks(max_cached, SUB);
+    const int max16 = max_subchunks(max_cached, SUB / 4);
+    // (With 8 q heads a workgroup the one-sub-chunk kernel needs more than
+    // 256 VGPRs; the same 64 rows a workgroup go as 4 x 16 rows instead.)
+    if (ng * max64 < n_cu)
+        return heads_per_wg(d) >= 8 ? DecodePlan{SUB / 4, 4, max(1, (max16 + 3) / 4)} : DecodePlan{SUB, 1, max(1, max64)};
+    const int nch = (int)max(1L, slots / ng);
+    const int need = (max16 + nch - 1) / nch;
+    if (need <= 4) return {SUB / 4, 4, max(1, (max16 + 3) / 4)};
+    if (need <= 8) return {SUB / 4, 8, nch};
+    if (ng * ((max64 + 3) / 4) <= slots) return {SUB, 4, (max64 + 3) / 4};
+    return {SUB, 8, (max64 + 7) / 8};
 }
 
 }  // namespace
+
+DecodePlan plan_attn_decode(const q35m_ctx* c, int n, int max_cached) {
+    return plan_decode(c->d, n, max_cached, c->n_cu);
+}
 
 // Fixed device scratch of q35m_attn_decode_noalloc: the split-K partials of
 // one call (kNoAllocScratchBytes).  Every GPU the library runs on holds its
@@ -489,40 +492,39 @@ hipError_t attn_decode_scratch_address(float** ptr) {
     return hipGetSymbolAddress(reinterpret_cast<void**>(ptr), HIP_SYMBOL(scratch));
 }
 
-size_t attn_decode_work_bytes(const q35m_ctx* c, const SeqBatch& sb) {
-    const DecodePlan p = plan_decode(c->d, sb, c->n_cu);
-    return (size_t)sb.n * c->d.nh * p.nchunks * (kHd + 2) * sizeof(float);
+size_t attn_decode_work_bytes(const q35m_ctx* c, int n, const DecodePlan& p) {
+    return (size_t)n * c->d.nh * p.nchunks * (kHd + 2) * sizeof(float);
 }
 
-hipError_t launch_attn_decode(q35m_ctx* c, int layer, const SeqBatch& sb, const float* q_gate,
-                              const float* k, const float* v, float* out, float* work) {
+hipError_t launch_attn_decode(q35m_ctx* c, int layer, const SeqBatch& sb, const DecodePlan& p,
+                              const float* q_gate, const float* k, const float* v, float* out, float* work) {
     const Dims& d = c->d;
     const AttnLayer& L = c->full[layer];
     const int hpw = heads_per_wg(d);
     const int groups = d.nh / hpw, ng = groups / d.nkv;
-    const DecodePlan p = plan_decode(d, sb, c->n_cu);
     const int nsub = p.nsub, nchunks = p.nchunks;
     float* part_o = work;
     float* part_ml = part_o + (size_t)sb.n * d.nh * nchunks * kHd;
     const dim3 grid(nchunks, groups, sb.n);
     {
-        const int kid = p.rows != SUB ? K_ATTN_DECODE_PARTIAL4R16
+        const int kid = p.rows != SUB ? (nsub == 8 ? K_ATTN_DECODE_PARTIAL8R16 : K_ATTN_DECODE_PARTIAL4R16)
                       : nsub == 8 ? K_ATTN_DECODE_PARTIAL8
-                      : nsub == 4 ? K_ATTN_DECODE_PARTIAL4
-                      : nsub == 2 ? K_ATTN_DECODE_PARTIAL2 : K_ATTN_DECODE_PARTIAL1;
+                      : nsub == 4 ? K_ATTN_DECODE_PARTIAL4 : K_ATTN_DECODE_PARTIAL1;
         ProfScope ps_(c, kid);
         auto go = [&](auto kern) {
             hipExtLaunchKernelGGL(kern, grid, dim3(NT), 0, c->stream, ps_.a, ps_.b, 0, q_gate, k, v, L.q_norm,
                                   L.k_norm, L.k_cache, L.v_cache, c->rope_cos, c->rope_sin, part_o, part_ml,
-                                  d.nkv, ng, c->cap, nchunks, d.eps, sb);
+                                  c->dev_len, d.nkv, ng, c->cap, nchunks, d.eps, sb);
         };
         auto by_nsub = [&](auto h) {
             constexpr int H = decltype(h)::value;
-            if (p.rows != SUB) go(attn_decode_partial<4, H, SUB / 4>);
+            if (p.rows != SUB) {
+                if (nsub == 8) go(attn_decode_partial<8, H, SUB / 4>);
+                else go(attn_decode_partial<4, H, SUB / 4>);
+            }
             else if (nsub == 8) go(attn_decode_partial<8, H, SUB>);
             else if (nsub == 4) go(attn_decode_partial<4, H, SUB>);
-            else if (nsub == 2) go(attn_decode_partial<2, H, SUB>);
-            else go(attn_decode_partial<1, H, SUB>);
+            else if constexpr (H < 8) go(attn_decode_partial<1, H, SUB>);
         };
         if (hpw == 8) by_nsub(std::integral_constant<int, 8>());
         else if (hpw == 4) by_nsub(std::integral_constant<int, 4>());
@@ -534,7 +536,8 @@ hipError_t launch_attn_decode(q35m_ctx* c, int layer, const SeqBatch& sb, const 
     {
         ProfScope ps_(c, K_ATTN_DECODE_MERGE);
         hipExtLaunchKernelGGL(attn_decode_merge, dim3(d.nh * (kHd / MSLICE), sb.n), dim3(MT), 0, c->stream,
-                              ps_.a, ps_.b, 0, part_o, part_ml, q_gate, out, d.nh, hpw, nchunks, p.rows, sb);
+                              ps_.a, ps_.b, 0, part_o, part_ml, q_gate, out, c->dev_len, d.nh, hpw, nchunks,
+                              p.rows, c->cap, sb);
     }
     return hipGetLastError();
 }

@@ -145,9 +145,13 @@ __global__ __launch_bounds__(512, 1) void attn_prefill_flash(
     // Rows past blk_len read row 0 instead (finite data; their scores are
     // masked), so no select waits on the loads, and the refill is
     // unconditional.
-    // (The host keeps start + T <= kPrefillMaxRows, so row offsets fit 31 bits.)
-    const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<float*>(Kh), 0, (int)std::min<size_t>((size_t)cap * kHd * sizeof(float), 0x7fffffff), 0x00020000);
+    // The host keeps start + T <= kPrefillMaxRows = 2^21 rows, so a row's
+    // offset fits 31 bits and its last 16-byte load ends at most at byte 2^31:
+    // the range is whole rows, up to exactly 2^31 bytes (the 32-bit
+    // num_records field is unsigned; 0x80000000 as its bit pattern).
+    const uint32_t krange = (uint32_t)(std::min<size_t>((size_t)cap, (size_t)kPrefillMaxRows) * kHd * sizeof(float));
+    const __amdgpu_buffer_rsrc_t krs =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(Kh), 0, (int)krange, 0x00020000);
     auto load_k = [&](int p0) {
 #pragma unroll
         for (int i = 0; i < KT / 4; ++i) {

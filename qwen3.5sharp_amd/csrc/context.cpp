@@ -104,27 +104,37 @@ void build_rope_table(int cap, int half, float base, std::vector<float>& cs,
         }
 }
 
-int build_seq_batch(const q35m_ctx* c, int n, const int* seqs, bool with_pos, q35::SeqBatch* sb) {
+// The batch of sequence ids of a decode call (distinct, in range).  With
+// max_cached non-null, every sequence must have room for the new row, and
+// *max_cached receives the longest cached length in the batch.
+int build_seq_batch(const q35m_ctx* c, int n, const int* seqs, q35::SeqBatch* sb, int* max_cached) {
     if (n < 1 || n > q35::kMaxBatch)
         return fail(Q35M_ERR_CAPACITY, "batch of %d sequences (1..%d per call)", n, q35::kMaxBatch);
     if (!seqs) return fail(Q35M_ERR_INVALID, "null seqs");
     sb->n = n;
+    int mx = 0;
     for (int i = 0; i < n; i++) {
         int r = check_seq(c, seqs[i]);
         if (r) return r;
         for (int j = 0; j < i; j++)
             if (seqs[j] == seqs[i]) return fail(Q35M_ERR_INVALID, "sequence %d repeated", seqs[i]);
         sb->seq[i] = seqs[i];
-        sb->pos[i] = 0;
-        if (with_pos) {
-            int p = c->kv_len[seqs[i]];
+        if (max_cached) {
+            const int p = c->kv_len[seqs[i]];
             if (p >= c->cap)
-                return fail(Q35M_ERR_CAPACITY, "sequence %d: KV cache full (%d rows)", seqs[i],
-                            c->cap);
-            sb->pos[i] = p;
+                return fail(Q35M_ERR_CAPACITY, "sequence %d: KV cache full (%d rows)", seqs[i], c->cap);
+            mx = p > mx ? p : mx;
         }
     }
+    if (max_cached) *max_cached = mx;
     return Q35M_OK;
+}
+
+// A sequence's length changed on the host: its device copy is rewritten
+// before the next launch that reads it.
+void set_len(q35m_ctx* c, int seq, int len) {
+    c->kv_len[seq] = len;
+    c->len_dirty[seq] = 1;
 }
 
 // Device address of the decode attention's fixed scratch, looked up once per
@@ -175,11 +185,11 @@ const char* kernel_name(int id) {
     static const char* names[K_COUNT] = {
         "deltanet_decode_kernel", "deltanet_conv_writeback", "dn_chunk_prep",
         "dn_chunk_scan",          "dn_chunk_out",            "attn_decode_partial<1>",
-        "attn_decode_partial<2>", "attn_decode_partial<4>",  "attn_decode_partial<8>",
+        "attn_decode_partial<4>",  "attn_decode_partial<8>",
         "attn_decode_merge",      "attn_prefill_prep",       "attn_prefill_flash",
         "q8k_quantize",           "linear_q<4>",             "linear_q<6>",
         "q4k_gemm", "q6k_gemm", "add_rmsnorm", "linear_qs<5>", "linear_qs<14>", "linear_f32", "linear_qt<2>",
-        "linear_qt<1>", "attn_decode_partial<4,16>"};
+        "linear_qt<1>", "attn_decode_partial<4,16>", "attn_decode_partial<8,16>"};
     return (id >= 0 && id < K_COUNT) ? names[id] : nullptr;
 }
 
@@ -328,7 +338,8 @@ int q35m_create(const q35m_config* cfg, int n_seqs, int kv_capacity, q35m_ctx** 
         c->is_recurrent[l] = cfg->is_recurrent ? (cfg->is_recurrent[l] != 0)
                                                : ((l + 1) % cfg->full_attention_interval != 0);
     c->kv_len.assign(n_seqs, 0);
-    c->epoch.assign(n_seqs, 0u);
+    c->len_dirty.assign(n_seqs, 0);
+    c->marks.assign(n_seqs, q35::DropMarks());
 
     int r = Q35M_OK;
     hipError_t e = hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking);
@@ -348,14 +359,14 @@ int q35m_create(const q35m_config* cfg, int n_seqs, int kv_capacity, q35m_ctx** 
     c->lin.resize(cfg->num_layers);
     c->full.resize(cfg->num_layers);
     size_t state_bytes = (size_t)n_seqs * d.nv * q35::kDk * q35::kDk * sizeof(float);
-    size_t conv_bytes = (size_t)n_seqs * d.conv_dim * q35::kConvState * sizeof(float);
+    size_t conv_bytes = (size_t)n_seqs * d.win_floats() * sizeof(float);
     size_t kv_bytes = (size_t)n_seqs * kv_capacity * d.kv_dim * sizeof(float);
+    r = alloc_zero(c, (void**)&c->dev_len, (size_t)n_seqs * sizeof(int));
     for (int l = 0; l < cfg->num_layers && r == Q35M_OK; l++) {
         if (c->is_recurrent[l]) {
             q35::DeltaNetLayer& L = c->lin[l];
             r = alloc_zero(c, (void**)&L.state, state_bytes);
-            if (!r) r = alloc_zero(c, (void**)&L.conv, 2 * conv_bytes);
-            L.conv_cur.assign(n_seqs, 0);
+            if (!r) r = alloc_zero(c, (void**)&L.conv, conv_bytes);
             if (!r) r = alloc_zero(c, (void**)&L.conv_w, (size_t)q35::kConvK * d.conv_dim * 4);
             if (!r) r = alloc_zero(c, (void**)&L.ssm_a, (size_t)d.nv * 4);
             if (!r) r = alloc_zero(c, (void**)&L.dt_bias, (size_t)d.nv * 4);
@@ -408,16 +419,14 @@ int q35m_reset(q35m_ctx* ctx, int seq) {
     if (r) return r;
     const q35::Dims& d = ctx->d;
     size_t sb = (size_t)d.nv * q35::kDk * q35::kDk * sizeof(float);
-    size_t cb = (size_t)d.conv_dim * q35::kConvState * sizeof(float);
+    size_t cb = d.win_floats() * sizeof(float);
     for (int l = 0; l < ctx->cfg.num_layers; l++) {
         if (!ctx->is_recurrent[l]) continue;
         HIP_TRY(hipMemsetAsync((char*)ctx->lin[l].state + sb * seq, 0, sb, ctx->stream), "reset");
-        HIP_TRY(hipMemsetAsync(ctx->lin[l].conv_window(seq, ctx->n_seqs, d.conv_dim), 0, cb,
-                               ctx->stream),
-                "reset");
+        HIP_TRY(hipMemsetAsync(ctx->lin[l].conv_window(seq, d.win_floats()), 0, cb, ctx->stream), "reset");
     }
-    ctx->kv_len[seq] = 0;
-    ctx->epoch[seq]++;
+    set_len(ctx, seq, 0);
+    ctx->marks[seq].drop(0);
     return Q35M_OK;
 }
 
@@ -428,8 +437,8 @@ int q35m_truncate(q35m_ctx* ctx, int seq, int length) {
     if (length < 0) return fail(Q35M_ERR_INVALID, "negative length %d", length);
     if (length > ctx->kv_len[seq])
         return fail(Q35M_ERR_RANGE, "cannot extend cache from %d to %d", ctx->kv_len[seq], length);
-    if (length < ctx->kv_len[seq]) ctx->epoch[seq]++;
-    ctx->kv_len[seq] = length;
+    if (length < ctx->kv_len[seq]) ctx->marks[seq].drop(length);
+    set_len(ctx, seq, length);
     return Q35M_OK;
 }
 
@@ -441,7 +450,7 @@ int q35m_advance(q35m_ctx* ctx, int seq, int n) {
     if ((long)ctx->kv_len[seq] + n > ctx->cap)
         return fail(Q35M_ERR_CAPACITY, "sequence %d: length %d + %d exceeds capacity %d", seq,
                     ctx->kv_len[seq], n, ctx->cap);
-    ctx->kv_len[seq] += n;
+    set_len(ctx, seq, ctx->kv_len[seq] + n);
     return Q35M_OK;
 }
 
@@ -498,13 +507,9 @@ int q35m_deltanet_decode(q35m_ctx* ctx, int layer, int n, const int* seqs, const
     if (!ctx->lin[layer].has_weights) return fail(Q35M_ERR_INVALID, "layer %d has no weights", layer);
     if (!qkv || !z || !b || !a || !out) return fail(Q35M_ERR_INVALID, "null activation pointer");
     q35::SeqBatch sb;
-    r = build_seq_batch(ctx, n, seqs, false, &sb);
+    r = build_seq_batch(ctx, n, seqs, &sb, nullptr);
     if (r) return r;
-    q35::DeltaNetLayer& L = ctx->lin[layer];
-    for (int i = 0; i < n; i++) sb.pos[i] = L.conv_cur[seqs[i]];
     HIP_TRY(q35::launch_deltanet_decode(ctx, layer, sb, qkv, z, b, a, out), "deltanet_decode");
-    // The step wrote the shifted windows into the other buffer.
-    for (int i = 0; i < n; i++) L.conv_cur[seqs[i]] ^= 1;
     return Q35M_OK;
 }
 
@@ -530,10 +535,13 @@ int q35m_attn_decode(q35m_ctx* ctx, int layer, int n, const int* seqs, const flo
     if (!ctx->full[layer].has_weights) return fail(Q35M_ERR_INVALID, "layer %d has no weights", layer);
     if (!q_gate || !k || !v || !out) return fail(Q35M_ERR_INVALID, "null activation pointer");
     q35::SeqBatch sb;
-    r = build_seq_batch(ctx, n, seqs, true, &sb);
+    int max_cached = 0;
+    r = build_seq_batch(ctx, n, seqs, &sb, &max_cached);
     if (r) return r;
-    HIP_TRY(q35::ensure_work(ctx, q35::attn_decode_work_bytes(ctx, sb)), "workspace");
-    HIP_TRY(q35::launch_attn_decode(ctx, layer, sb, q_gate, k, v, out, ctx->work), "attn_decode");
+    const q35::DecodePlan p = q35::plan_attn_decode(ctx, n, max_cached);
+    HIP_TRY(q35::ensure_work(ctx, q35::attn_decode_work_bytes(ctx, n, p)), "workspace");
+    HIP_TRY(q35::flush_lengths(ctx), "attn_decode lengths");
+    HIP_TRY(q35::launch_attn_decode(ctx, layer, sb, p, q_gate, k, v, out, ctx->work), "attn_decode");
     return Q35M_OK;
 }
 
@@ -546,9 +554,11 @@ int q35m_attn_decode_noalloc(q35m_ctx* ctx, int layer, int n, const int* seqs, c
     if (!q_gate || !k || !v || !out) return fail(Q35M_ERR_INVALID, "null activation pointer");
     if (!ctx->noalloc_scratch) return fail(Q35M_ERR_NO_DEVICE, "no device scratch");
     q35::SeqBatch sb;
-    r = build_seq_batch(ctx, n, seqs, true, &sb);
+    int max_cached = 0;
+    r = build_seq_batch(ctx, n, seqs, &sb, &max_cached);
     if (r) return r;
-    const size_t need = q35::attn_decode_work_bytes(ctx, sb);
+    const q35::DecodePlan p = q35::plan_attn_decode(ctx, n, max_cached);
+    const size_t need = q35::attn_decode_work_bytes(ctx, n, p);
     if (need > q35::kNoAllocScratchBytes)
         return fail(Q35M_ERR_CAPACITY,
                     "attn_decode_noalloc: this batch needs %zu bytes of split-K partials, the fixed scratch "
@@ -557,7 +567,8 @@ int q35m_attn_decode_noalloc(q35m_ctx* ctx, int layer, int n, const int* seqs, c
     // No per-kernel timers here: they may create events.
     const bool prof = ctx->profile;
     ctx->profile = false;
-    hipError_t e = q35::launch_attn_decode(ctx, layer, sb, q_gate, k, v, out, ctx->noalloc_scratch);
+    hipError_t e = q35::flush_lengths(ctx);
+    if (e == hipSuccess) e = q35::launch_attn_decode(ctx, layer, sb, p, q_gate, k, v, out, ctx->noalloc_scratch);
     ctx->profile = prof;
     HIP_TRY(e, "attn_decode_noalloc");
     return Q35M_OK;
@@ -696,13 +707,14 @@ int q35m_grow(q35m_ctx* ctx, int kv_capacity) {
         ctx->rope_cap = kv_capacity;
     }
     ctx->cap = kv_capacity;
+    ctx->generation++;
     return Q35M_OK;
 }
 
 size_t q35m_snapshot_bytes(const q35m_ctx* ctx) {
     if (!ctx) return 0;
     const q35::Dims& d = ctx->d;
-    const size_t per = ((size_t)d.nv * q35::kDk * q35::kDk + (size_t)d.conv_dim * q35::kConvState) * sizeof(float);
+    const size_t per = ((size_t)d.nv * q35::kDk * q35::kDk + d.win_floats()) * sizeof(float);
     size_t n = 0;
     for (int l = 0; l < ctx->cfg.num_layers; l++) n += ctx->is_recurrent[l] ? 1 : 0;
     return n * per;
@@ -714,11 +726,11 @@ size_t q35m_snapshot_bytes(const q35m_ctx* ctx) {
 static int snapshot_copy(q35m_ctx* ctx, int seq, char* dev, bool save) {
     const q35::Dims& d = ctx->d;
     const size_t sb = (size_t)d.nv * q35::kDk * q35::kDk * sizeof(float);
-    const size_t cb = (size_t)d.conv_dim * q35::kConvState * sizeof(float);
+    const size_t cb = d.win_floats() * sizeof(float);
     for (int l = 0; l < ctx->cfg.num_layers; l++) {
         if (!ctx->is_recurrent[l]) continue;
         char* st = (char*)ctx->lin[l].state + sb * seq;
-        char* cw = (char*)ctx->lin[l].conv_window(seq, ctx->n_seqs, d.conv_dim);
+        char* cw = (char*)ctx->lin[l].conv_window(seq, d.win_floats());
         HIP_TRY(hipMemcpyAsync(save ? dev : st, save ? st : dev, sb, hipMemcpyDeviceToDevice, ctx->stream),
                 "snapshot");
         dev += sb;
@@ -744,7 +756,24 @@ int q35m_snapshot_save(q35m_ctx* ctx, int seq, void* dev, size_t bytes, q35m_sna
     if (r) return r;
     if ((r = snapshot_copy(ctx, seq, (char*)dev, true))) return r;
     info->kv_len = ctx->kv_len[seq];
-    info->epoch = ctx->epoch[seq];
+    info->epoch = ctx->marks[seq].save();
+    return Q35M_OK;
+}
+
+static int snapshot_refused(const q35m_ctx* ctx, int seq, const q35m_snapshot_info* info) {
+    return fail(Q35M_ERR_RANGE,
+                "snapshot at length %d no longer matches sequence %d at length %d (the sequence was shorter "
+                "than that since the save: reset, truncate, restore to a shorter length, or K/V rows written)",
+                info->kv_len, seq, ctx->kv_len[seq]);
+}
+
+int q35m_snapshot_valid(const q35m_ctx* ctx, int seq, const q35m_snapshot_info* info) {
+    int r = check_ctx(ctx);
+    if (!r) r = check_seq(ctx, seq);
+    if (r) return r;
+    if (!info) return fail(Q35M_ERR_INVALID, "null snapshot info");
+    if (!ctx->marks[seq].restorable(info->epoch, info->kv_len, ctx->kv_len[seq]))
+        return snapshot_refused(ctx, seq, info);
     return Q35M_OK;
 }
 
@@ -752,21 +781,13 @@ int q35m_snapshot_restore(q35m_ctx* ctx, int seq, const void* dev, size_t bytes,
                           q35m_snapshot_info* info) {
     int r = snapshot_check(ctx, seq, dev, bytes, info);
     if (r) return r;
-    if (info->epoch != ctx->epoch[seq] || info->kv_len > ctx->kv_len[seq])
-        return fail(Q35M_ERR_RANGE,
-                    "snapshot at length %d no longer matches sequence %d at length %d (reset, truncate, "
-                    "restore to a shorter length or K/V write since the save)",
-                    info->kv_len, seq, ctx->kv_len[seq]);
+    if (!ctx->marks[seq].restorable(info->epoch, info->kv_len, ctx->kv_len[seq]))
+        return snapshot_refused(ctx, seq, info);
     if ((r = snapshot_copy(ctx, seq, const_cast<char*>((const char*)dev), false))) return r;
-    if (info->kv_len < ctx->kv_len[seq]) {
-        // Rows at and above the restored length will be written again, so
-        // snapshots taken at a longer length (which hold a linear state that
-        // went with the old rows) must be refused from now on: a new epoch.
-        // The snapshot just restored stays usable: it gets the new epoch.
-        ctx->epoch[seq]++;
-        info->epoch = ctx->epoch[seq];
-    }
-    ctx->kv_len[seq] = info->kv_len;
+    // Rows at and above the restored length will be written again: snapshots
+    // longer than it no longer hold (this one and shorter ones still do).
+    if (info->kv_len < ctx->kv_len[seq]) ctx->marks[seq].drop(info->kv_len);
+    set_len(ctx, seq, info->kv_len);
     return Q35M_OK;
 }
 
@@ -913,7 +934,7 @@ static int state_locate(q35m_ctx* ctx, int layer, int seq, int kind, char** base
             *base = (char*)ctx->lin[layer].state + *bytes * seq;
         } else {
             *bytes = (size_t)d.conv_dim * q35::kConvState * sizeof(float);
-            *base = (char*)ctx->lin[layer].conv_window(seq, ctx->n_seqs, d.conv_dim);
+            *base = (char*)ctx->lin[layer].conv_window(seq, d.win_floats());
         }
         return Q35M_OK;
     }
@@ -982,11 +1003,22 @@ int q35m_state_write(q35m_ctx* ctx, int layer, int seq, int kind, const void* ho
     if (is_kv(kind)) {
         if (bytes % ((size_t)ctx->d.kv_dim * sizeof(float)))
             return fail(Q35M_ERR_INVALID, "K/V writes move whole rows of %d floats", ctx->d.kv_dim);
-        // Rows are about to change: snapshots of this sequence no longer hold.
-        ctx->epoch[seq]++;
+        // Rows from 0 are about to change: as a drop of the length to 0.
+        ctx->marks[seq].drop(0);
         HIP_TRY(kv_copy(ctx, base, const_cast<void*>(host), bytes, false), "state_write");
     } else {
         HIP_TRY(hipMemcpyAsync(base, host, bytes, hipMemcpyHostToDevice, ctx->stream), "state_write");
+        if (kind == Q35M_STATE_CONV) {
+            // The q/k channels' windows (the block's first 2 * key_dim rows)
+            // into the decode copies after the [conv_dim][3] block.
+            const size_t qk = (size_t)2 * ctx->d.key_dim * q35::kConvState * sizeof(float);
+            const size_t nq = bytes < qk ? bytes : qk;
+            const size_t blk = (size_t)ctx->d.conv_dim * q35::kConvState * sizeof(float);
+            for (int r = 1; r < ctx->d.nv / ctx->d.nk && nq; r++)
+                HIP_TRY(hipMemcpyAsync(base + blk + (size_t)(r - 1) * qk, base, nq, hipMemcpyDeviceToDevice,
+                                       ctx->stream),
+                        "state_write");
+        }
     }
     HIP_TRY(hipStreamSynchronize(ctx->stream), "state_write");
     return Q35M_OK;

@@ -19,10 +19,14 @@
 // The conv operands are loaded before the state so that the conv, the norms
 // and the gates run while the state is in flight.
 //
-// Conv windows are double-buffered: a step reads the window from buffer p and
-// writes the shifted window to buffer 1 - p, so the workgroups that read one
-// q/k window never race its single writer.  The host flips p per
-// (layer, sequence) after each step.
+// Conv windows: the q/k windows of a k-head are held once per v-head that
+// shares it (copy vh % R; copy 0 is the reference layout's), so each
+// workgroup reads and rewrites only windows that no other workgroup touches,
+// in place.  Inside the workgroup, the shifted windows are stored after the
+// first barrier, by which point every thread has consumed its window loads
+// (threads 128-255 also read value channel 127, whose window thread 127
+// rewrites).  Nothing about the windows depends on the host or on a step
+// count, so a captured step replays correctly any number of times.
 //
 // Column slices of a head (more, smaller workgroups) were measured slower at
 // batch 1 and 8: the gated norm then needs a second launch.
@@ -63,9 +67,9 @@ __device__ __forceinline__ float conv_out(const ConvOperands& o) {
     return silu(acc);
 }
 
-// Window shift (GatedDeltaNetOps.cs:86-89), written to the other buffer.
-__device__ __forceinline__ void conv_shift(const ConvOperands& o, float* __restrict__ wout, int c) {
-    float* dd = wout + (size_t)c * kConvState;
+// Window shift (GatedDeltaNetOps.cs:86-89), in place.
+__device__ __forceinline__ void conv_shift(const ConvOperands& o, float* __restrict__ win, int c) {
+    float* dd = win + (size_t)c * kConvState;
     dd[0] = o.c1;
     dd[1] = o.c2;
     dd[2] = o.x;
@@ -76,22 +80,22 @@ __global__ __launch_bounds__(NT) void deltanet_decode_kernel(
     const float* __restrict__ ain, float* __restrict__ out, const float* __restrict__ conv_w,
     const float* __restrict__ ssm_a, const float* __restrict__ dt_bias,
     const float* __restrict__ ssm_norm, float* __restrict__ state, float* __restrict__ conv,
-    int nk, int nv, int n_seqs, float eps, SeqBatch sb) {
+    int nk, int nv, float eps, SeqBatch sb) {
     constexpr int C4N = kDk / 4;      // float4 columns
     constexpr int RG = NT / C4N;      // row groups
     constexpr int RPT = kDk / RG;     // rows per thread
     const int vh = blockIdx.x % nv;
     const int i = blockIdx.x / nv;
-    const int R = nv / nk, kh = vh / R;
+    const int R = nv / nk, kh = vh / R, rep = vh % R;
     const int key_dim = nk * kDk, value_dim = nv * kDk, conv_dim = 2 * key_dim + value_dim;
-    const int seq = sb.seq[i], par = sb.pos[i];
+    const int seq = sb.seq[i];
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int c4 = t % C4N, rg = t / C4N;
 
     float* S = state + ((size_t)seq * nv + vh) * kDk * kDk;
-    const size_t cstride = (size_t)conv_dim * kConvState;
-    const float* win = conv + ((size_t)par * n_seqs + seq) * cstride;
-    float* wout = conv + ((size_t)(1 - par) * n_seqs + seq) * cstride;
+    // This sequence's window block; the q/k windows of copy `rep`.
+    float* win = conv + (size_t)seq * ((size_t)conv_dim + (size_t)(R - 1) * 2 * key_dim) * kConvState;
+    float* win_qk = rep == 0 ? win : win + ((size_t)conv_dim + (size_t)(rep - 1) * 2 * key_dim) * kConvState;
     const float* x = qkv + (size_t)i * conv_dim;
 
     __shared__ float qk_s[2 * kDk];            // SiLU(conv) of q (0..127) and k (128..255)
@@ -106,7 +110,7 @@ __global__ __launch_bounds__(NT) void deltanet_decode_kernel(
     // still in flight (the barriers before its first use wait on LDS only).
     const int qk_c = t < kDk ? kh * kDk + t : key_dim + kh * kDk + (t - kDk);
     const int v_c = 2 * key_dim + vh * kDk + min(t, kDk - 1);
-    const ConvOperands oq = conv_load(conv_w, win, x, qk_c, conv_dim);
+    const ConvOperands oq = conv_load(conv_w, win_qk, x, qk_c, conv_dim);
     const ConvOperands ov = conv_load(conv_w, win, x, v_c, conv_dim);
     const float b_in = bin[(size_t)i * nv + vh], a_in = ain[(size_t)i * nv + vh];
     const float sa = ssm_a[vh], dtb = dt_bias[vh];
@@ -134,11 +138,12 @@ __global__ __launch_bounds__(NT) void deltanet_decode_kernel(
     // (Decode.cs:378-386); uniform, computed by every thread.
     const float beta = 1.0f / (1.0f + expf(-b_in));
     const float decay = expf(sa * softplus_ref(a_in + dtb));
-    // Single writer per channel: the q/k windows by the k-head's first
-    // v-head, the value windows by their head.
-    if (vh % R == 0) conv_shift(oq, wout, qk_c);
-    if (t < kDk) conv_shift(ov, wout, v_c);
     lds_barrier();
+    // Every thread's window loads are consumed (their conv outputs are in
+    // LDS), so the windows are rewritten in place: this workgroup's q/k copy
+    // and its head's value windows, one thread per channel.
+    conv_shift(oq, win_qk, qk_c);
+    if (t < kDk) conv_shift(ov, win, v_c);
 
     // L2 norms of q and k, and q.k (GatedDeltaNetOps.cs:144-151): waves 0-1
     // hold q, waves 2-3 hold k.
@@ -233,7 +238,7 @@ hipError_t launch_deltanet_decode(q35m_ctx* c, int layer, const SeqBatch& sb, co
     ProfScope ps_(c, K_DN_DECODE);
     hipExtLaunchKernelGGL(deltanet_decode_kernel, dim3(sb.n * d.nv), dim3(NT), 0, c->stream, ps_.a, ps_.b, 0, qkv, z,
                        b, a, out, L.conv_w, L.ssm_a, L.dt_bias, L.ssm_norm, L.state, L.conv, d.nk,
-                       d.nv, c->n_seqs, d.eps, sb);
+                       d.nv, d.eps, sb);
     return hipGetLastError();
 }
 

@@ -159,17 +159,27 @@ __device__ __forceinline__ void conv_load(const QkvRows& q, const float* __restr
 
 // The window write-back reloads the three raw inputs rather than selecting
 // them from x: a select by the uniform T - ts becomes one scalar mask per
-// element, which the compiler keeps live across the caller's loops.
+// element, which the compiler keeps live across the caller's loops.  A q/k
+// channel's window is also written to the `nextra` further copies that the
+// decode of the k-head's other v-heads reads (after the [conv_dim][3]
+// block, qk_dim channels each); value channels pass nextra = 0.
 template <int N>
 __device__ __forceinline__ void conv_finish(const QkvRows& q, float4 wt, float* __restrict__ cs, int c,
-                                            int conv_dim, int T, int ts, float (&x)[N + 3], float (&y)[N]) {
+                                            int conv_dim, int T, int ts, float (&x)[N + 3], float (&y)[N],
+                                            int nextra, int qk_dim) {
     if (T >= kConvState && ts <= T - 1 && T - 1 < ts + N) {
+        float wv[kConvState];
 #pragma unroll
         for (int j = 0; j < kConvState; ++j) {
             const int row = T - kConvState + j - q.r0;
-            cs[(size_t)c * kConvState + j] = __builtin_bit_cast(
+            wv[j] = __builtin_bit_cast(
                 float, __builtin_amdgcn_raw_buffer_load_b32(q.rsrc, (row * conv_dim + c) * 4, 0, 0));
+            cs[(size_t)c * kConvState + j] = wv[j];
         }
+        for (int r = 0; r < nextra; ++r)
+#pragma unroll
+            for (int j = 0; j < kConvState; ++j)
+                cs[((size_t)conv_dim + (size_t)r * qk_dim + c) * kConvState + j] = wv[j];
     }
 #pragma unroll
     for (int j = 0; j < N; ++j) {
@@ -184,10 +194,11 @@ __device__ __forceinline__ void conv_finish(const QkvRows& q, float4 wt, float* 
 
 // cs[c][j] = qkvCh[c*T + tail + j] over the channel-major copy qkvCh [C][T]
 // followed (64-byte aligned, as the reference's arena) by the conv output
-// [C][T]; for T >= 3 this is x[T-3+j][c].
+// [C][T]; for T >= 3 this is x[T-3+j][c].  The windows of the qk_dim q/k
+// channels also go to the nextra copies after the [conv_dim][3] block.
 __global__ void deltanet_conv_writeback(const float* __restrict__ qkv,
                                         const float* __restrict__ conv_w, float* __restrict__ cs,
-                                        int T, int conv_dim) {
+                                        int T, int conv_dim, int nextra, int qk_dim) {
     const int c = blockIdx.x * blockDim.x + threadIdx.x;
     if (c >= conv_dim) return;
     const long ct = (long)conv_dim * T;
@@ -209,6 +220,8 @@ __global__ void deltanet_conv_writeback(const float* __restrict__ qkv,
             val = acc / (1.0f + expf(-acc));
         }
         cs[(size_t)c * kConvState + j] = val;
+        if (c < qk_dim)
+            for (int r = 0; r < nextra; ++r) cs[((size_t)conv_dim + (size_t)r * qk_dim + c) * kConvState + j] = val;
     }
 }
 
@@ -287,7 +300,7 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep(
         }
     }
     auto conv_qk = [&](int ch, float4 wt, float (&x)[35], float (&y)[32]) {
-        conv_finish<32>(rows, wt, cs, ch, conv_dim, T, t0 + 32 * hq, x, y);
+        conv_finish<32>(rows, wt, cs, ch, conv_dim, T, t0 + 32 * hq, x, y, R - 1, 2 * key_dim);
 #pragma unroll
         for (int j = 0; j < 32; ++j) Ks[32 * hq + j][cq] = y[j];
         lds_barrier();
@@ -474,7 +487,7 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep(
             {
                 float y[16];
                 const int ch = 2 * key_dim + vh * kDk + 64 * h + cl;
-                conv_finish<16>(rows, wv[h], cs, ch, conv_dim, T, t0 + 16 * qt, xv[h], y);
+                conv_finish<16>(rows, wv[h], cs, ch, conv_dim, T, t0 + 16 * qt, xv[h], y, 0, 0);
                 if (h == 1) lds_barrier();   // every wave is past the first half
 #pragma unroll
                 for (int j = 0; j < 16; ++j) Vs[16 * qt + j][cl] = y[j];
@@ -834,12 +847,13 @@ hipError_t launch_deltanet_prefill(q35m_ctx* c, int layer, int seq, int T, const
     const int nch = (T + CH - 1) / CH;
     PrefillWork w = carve(c->work, d, nch);
     float* state = L.state + (size_t)seq * d.nv * kDk * kDk;
-    float* cs = L.conv_window(seq, c->n_seqs, d.conv_dim);
+    float* cs = L.conv_window(seq, d.win_floats());
     hipError_t e;
     if (T < kConvState) {
         ProfScope ps_(c, K_DN_CONV_WRITEBACK);
         hipExtLaunchKernelGGL(deltanet_conv_writeback, dim3((d.conv_dim + 255) / 256), dim3(256), 0,
-                           c->stream, ps_.a, ps_.b, 0, qkv, L.conv_w, cs, T, d.conv_dim);
+                           c->stream, ps_.a, ps_.b, 0, qkv, L.conv_w, cs, T, d.conv_dim, d.nv / d.nk - 1,
+                           2 * d.key_dim);
         if ((e = hipGetLastError()) != hipSuccess) return e;
     }
     {

@@ -9,6 +9,7 @@
 #include <vector>
 
 #include "../../include/q35mix.h"
+#include "snapshot_marks.h"
 
 namespace q35 {
 
@@ -25,25 +26,31 @@ constexpr int kMaxVPerK = 4;    // DeltaNet v-heads per k-head (chunk prep stage
 // K tiles come through a buffer descriptor (32-bit byte offsets, 1 KiB a row).
 constexpr int kPrefillMaxRows = 1 << 21;
 
-// Per-launch sequence batch, passed by value in the kernel arguments.
+// Per-launch sequence batch (sequence ids only), passed by value in the
+// kernel arguments.  Positions are not in it: kernels read each sequence's
+// length from the context's device array, so a captured launch stays valid
+// as the lengths move.
 struct SeqBatch {
     int n;
     int seq[kMaxBatch];
-    int pos[kMaxBatch];  // attention: row the new token is written to;
-                         // DeltaNet decode: conv-window buffer holding the window
 };
 
+// Conv windows of one (layer, sequence): the reference's [conv_dim][3]
+// (oldest first), followed by R - 1 more copies of the windows of the
+// 2 * key_dim q/k channels ([R - 1][2 * key_dim][3]), R = v-heads per k-head.
+// Decode workgroup (sequence, v-head vh) reads and rewrites copy vh % R of its
+// k-head's q/k windows (copy 0 is the one inside the reference block) and its
+// own head's value windows, each in place and by no other workgroup, so the
+// window update needs no double buffer and no host-held parity.  Every copy
+// holds the same values; state I/O reads the reference block and writes all.
 struct DeltaNetLayer {
     float* conv_w = nullptr;   // [K][conv_dim]
     float* ssm_a = nullptr;    // [H_v]
     float* dt_bias = nullptr;  // [H_v]
     float* ssm_norm = nullptr; // [dv]
     float* state = nullptr;    // [n_seqs][H_v][dk][dv]
-    float* conv = nullptr;     // [2][n_seqs][conv_dim][3], double-buffered windows
-    std::vector<unsigned char> conv_cur;  // [n_seqs] buffer holding the current window
-    float* conv_window(int seq, int n_seqs, int conv_dim) const {
-        return conv + ((size_t)conv_cur[seq] * n_seqs + seq) * conv_dim * kConvState;
-    }
+    float* conv = nullptr;     // [n_seqs][win_floats], the layout above
+    float* conv_window(int seq, size_t win_floats) const { return conv + (size_t)seq * win_floats; }
     bool has_weights = false;
 };
 
@@ -64,8 +71,7 @@ enum KernelId {
     K_DN_CHUNK_PREP,
     K_DN_CHUNK_SCAN,
     K_DN_CHUNK_OUT,
-    K_ATTN_DECODE_PARTIAL1,   // attn_decode_partial<NSUB> by sub-chunks per workgroup
-    K_ATTN_DECODE_PARTIAL2,
+    K_ATTN_DECODE_PARTIAL1,   // attn_decode_partial<NSUB> by sub-chunks (of 64 rows) per workgroup
     K_ATTN_DECODE_PARTIAL4,
     K_ATTN_DECODE_PARTIAL8,
     K_ATTN_DECODE_MERGE,
@@ -83,6 +89,7 @@ enum KernelId {
     K_Q2_0C_LINEAR,
     K_STQ1_0_LINEAR,
     K_ATTN_DECODE_PARTIAL4R16,   // attn_decode_partial, 4 sub-chunks of 16 rows per workgroup
+    K_ATTN_DECODE_PARTIAL8R16,   // attn_decode_partial, up to 8 sub-chunks of 16 rows per workgroup
     K_COUNT
 };
 const char* kernel_name(int id);
@@ -94,6 +101,9 @@ struct Dims {
     int q_dim, kv_dim;
     float eps;
     float rope_base;
+    // Floats of one (layer, sequence) conv-window block: the reference window
+    // plus nv / nk - 1 copies of the q/k channels' windows.
+    size_t win_floats() const { return ((size_t)conv_dim + (size_t)(nv / nk - 1) * 2 * key_dim) * kConvState; }
 };
 
 }  // namespace q35
@@ -109,8 +119,20 @@ struct q35m_ctx {
     std::vector<unsigned char> is_recurrent;
     std::vector<q35::DeltaNetLayer> lin;   // indexed by layer (empty for GQA layers)
     std::vector<q35::AttnLayer> full;      // indexed by layer (empty for DeltaNet layers)
-    std::vector<int> kv_len;           // per seq
-    std::vector<unsigned> epoch;       // per seq: bumped when cached K/V rows may change below the length
+    std::vector<int> kv_len;           // per seq (host copy; exact, see dev_len)
+    // Per seq: the drops of its length (and rewrites of its rows from 0), which
+    // decide whether a linear-state snapshot still matches its K/V rows.
+    std::vector<q35::DropMarks> marks;
+    // Per-sequence lengths on the device, which the decode attention kernels
+    // read (so a captured decode step replays at the current position).  The
+    // host changes kv_len and marks the sequence in len_dirty; flush_lengths
+    // enqueues one small kernel that writes every marked length before the
+    // next launch that reads them.  A decode graph's replay advances both.
+    int* dev_len = nullptr;
+    std::vector<unsigned char> len_dirty;
+    // Bumped whenever the K/V caches or the RoPE table move (q35m_grow): a
+    // decode graph captured before holds their old addresses and refuses to run.
+    unsigned generation = 0;
     float* rope_cos = nullptr;         // [rope_cap][32]
     float* rope_sin = nullptr;
     int rope_cap = 0;
@@ -140,11 +162,26 @@ hipError_t launch_deltanet_decode(q35m_ctx* c, int layer, const SeqBatch& sb, co
 hipError_t launch_deltanet_prefill(q35m_ctx* c, int layer, int seq, int T, const float* qkv,
                                    const float* z, const float* b, const float* a, float* out);
 size_t deltanet_prefill_work_bytes(const Dims& d, int T);
+// Split of one decode-attention launch: rows per sub-chunk, sub-chunks per
+// workgroup, workgroups (chunks) per head group.  It is chosen from the
+// batch size and the longest cached length the launch must cover; the
+// kernels take each sequence's actual length from the device, so one plan
+// serves every length up to that bound (chunks past a sequence's rows exit).
+struct DecodePlan {
+    int rows, nsub, nchunks;
+};
+DecodePlan plan_attn_decode(const q35m_ctx* c, int n, int max_cached);
+// Bytes of split-K partials a launch of n sequences under plan p writes.
+size_t attn_decode_work_bytes(const q35m_ctx* c, int n, const DecodePlan& p);
 // Decode attention: the split-K partials live in `work`, of at least
-// attn_decode_work_bytes(c, sb) bytes.
-hipError_t launch_attn_decode(q35m_ctx* c, int layer, const SeqBatch& sb, const float* q_gate,
-                              const float* k, const float* v, float* out, float* work);
-size_t attn_decode_work_bytes(const q35m_ctx* c, const SeqBatch& sb);
+// attn_decode_work_bytes(c, sb.n, p) bytes.
+hipError_t launch_attn_decode(q35m_ctx* c, int layer, const SeqBatch& sb, const DecodePlan& p,
+                              const float* q_gate, const float* k, const float* v, float* out, float* work);
+// Writes the lengths marked in c->len_dirty to c->dev_len (one small kernel
+// per 64 sequences; nothing when none is marked).
+hipError_t flush_lengths(q35m_ctx* c);
+// dev_len[seq] += k for the sequences of sb, on the context stream.
+hipError_t launch_lengths_add(q35m_ctx* c, const SeqBatch& sb, int k);
 // Size of the fixed device scratch of q35m_attn_decode_noalloc.
 constexpr size_t kNoAllocScratchBytes = Q35M_NOALLOC_SCRATCH_BYTES;
 // Device address of that scratch on the current device (call with the device

@@ -93,6 +93,11 @@ def lib() -> ctypes.CDLL:
         _lib.q35m_q8k_bytes.argtypes = [ctypes.c_int, ctypes.c_int]
         _lib.q35m_reuse_plan.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_int,
                                          ctypes.c_void_p, ctypes.c_int] + [ctypes.POINTER(ctypes.c_int)] * 3
+        _lib.q35m_decode_graph_create.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p,
+                                                  ctypes.POINTER(DecodeIO), ctypes.c_int,
+                                                  ctypes.POINTER(ctypes.c_void_p)]
+        _lib.q35m_decode_graph_run.argtypes = [ctypes.c_void_p, ctypes.c_int]
+        _lib.q35m_decode_graph_destroy.argtypes = [ctypes.c_void_p]
     return _lib
 
 
@@ -172,6 +177,22 @@ class DeviceArray:
             self.ptr = None
 
 
+class DeviceView(DeviceArray):
+    """fp32 window [offset, offset + prod(shape)) of another device buffer
+    (shares its memory; frees nothing)."""
+
+    def __init__(self, base: DeviceArray, offset: int, shape):
+        self.ctx = base.ctx
+        self.shape = tuple(int(s) for s in np.atleast_1d(shape))
+        self.nbytes = int(np.prod(self.shape)) * 4
+        assert 0 <= offset and offset * 4 + self.nbytes <= base.nbytes
+        self.ptr = base.ptr + 4 * offset
+        self._base = base
+
+    def free(self) -> None:
+        self.ptr = None
+
+
 class Gguf:
     """A GGUF file opened by the library (q35m_gguf_open); tensors are views
     of the read-only mapping."""
@@ -209,6 +230,42 @@ class Gguf:
         v = ctypes.c_char_p()
         check(lib().q35m_gguf_string(ctypes.c_void_p(self.handle), key.encode(), ctypes.byref(v)))
         return v.value.decode()
+
+
+class DecodeIO(ctypes.Structure):
+    """q35m_decode_io: one layer's activations in a decode graph (DeltaNet:
+    qkv, z, b, a, out; full attention: q_gate, k, v, unused, out)."""
+    _fields_ = [("in0", ctypes.c_void_p), ("in1", ctypes.c_void_p), ("in2", ctypes.c_void_p),
+                ("in3", ctypes.c_void_p), ("out", ctypes.c_void_p)]
+
+
+class DecodeGraph:
+    """q35m_decode_graph: one decode step of every layer for a fixed batch,
+    captured once (q35m_decode_graph_create) and run per token.  `io` holds,
+    per layer, the device arrays (in0, in1, in2, in3, out) of that layer's
+    mixer (in3 None for full-attention layers)."""
+
+    def __init__(self, ctx: "Context", seqs, io, max_len: int):
+        self.ctx = ctx
+        arr = (DecodeIO * len(io))()
+        for l, bufs in enumerate(io):
+            arr[l] = DecodeIO(*[None if b is None else b.ptr for b in bufs])
+        h = ctypes.c_void_p()
+        check(lib().q35m_decode_graph_create(ctypes.c_void_p(ctx.handle), len(seqs), _seqs(seqs), arr, max_len,
+                                             ctypes.byref(h)))
+        self.handle = h.value
+        self._io = io
+
+    def run(self, replay: bool = True) -> None:
+        check(lib().q35m_decode_graph_run(ctypes.c_void_p(self.handle), int(replay)))
+
+    def try_run(self, replay: bool = True) -> int:
+        return lib().q35m_decode_graph_run(ctypes.c_void_p(self.handle), int(replay))
+
+    def close(self) -> None:
+        if self.handle:
+            check(lib().q35m_decode_graph_destroy(ctypes.c_void_p(self.handle)))
+            self.handle = None
 
 
 class SnapshotInfo(ctypes.Structure):
@@ -475,19 +532,29 @@ def cu_count(device: int = 0) -> int:
     return n.value
 
 
-def attn_decode_variant(n_seqs: int, n_kv_heads: int, lengths, n_cu: int) -> str:
+def attn_decode_variant(n_seqs: int, n_kv_heads: int, lengths, n_cu: int, q_per_kv: int = 4) -> str:
     """Split the decode attention picks for a batch whose sequences hold
-    `lengths` cached rows, as its per-kernel timer names it: sub-chunks of 64
-    rows per workgroup, the fewest (1, 2, 4) keeping the grid within 2
-    workgroups per CU, else 8; when one sub-chunk already gives at least one
-    workgroup per CU, 4 sub-chunks of 16 rows ("4,16") instead."""
-    max_subs = max((int(x) + 63) // 64 for x in lengths)
-    for ns in (1, 2, 4):
-        if n_seqs * n_kv_heads * max(1, -(-max_subs // ns)) <= 2 * n_cu:
-            if ns == 1 and n_seqs * n_kv_heads * max_subs >= n_cu:
-                return "4,16"
-            return str(ns)
-    return "8"
+    `lengths` cached rows, as its per-kernel timer names it: one 64-row
+    sub-chunk per workgroup ("1") while there are fewer than n_cu of them;
+    else 16-row sub-chunks over one round of 2 workgroups per CU, 4 ("4,16")
+    or 8 ("8,16") per workgroup, when 8 cover the rows; else 4 or 8 sub-chunks
+    of 64 rows ("4", "8"), the fewest that keep one round.  A workgroup takes
+    the q heads of one kv head, at most 8 (q_per_kv / 8 workgroups a kv head
+    beyond); with 8 the one-sub-chunk split goes as 4 of 16 rows."""
+    hpw = min(q_per_kv, 8)
+    ng = n_seqs * n_kv_heads * (q_per_kv // hpw)
+    max_cached = max(int(x) for x in lengths)
+    max64, max16 = -(-max_cached // 64), -(-max_cached // 16)
+    slots = 2 * n_cu
+    if ng * max64 < n_cu:
+        return "4,16" if hpw >= 8 else "1"
+    nch = max(1, slots // ng)
+    need = -(-max16 // nch)
+    if need <= 4:
+        return "4,16"
+    if need <= 8:
+        return "8,16"
+    return "4" if ng * -(-max64 // 4) <= slots else "8"
 
 
 class Event:

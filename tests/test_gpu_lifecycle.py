@@ -122,7 +122,7 @@ def test_snapshot_rolls_back_state():
     # without the restore the continuation differs (the state really moved on)
     other = step(c, 1, xd, xa, 5, ref)
     assert not bits_equal(other[0], first[0][0])
-    c.snapshot_restore(1, buf, info)            # still valid: the restore above refreshed info
+    c.snapshot_restore(1, buf, info)            # still valid: the restore above cut the length only to its own
     c.truncate(1, 4)
     with pytest.raises(q35mix.Q35Error) as e:
         c.snapshot_restore(1, buf, info)

@@ -4,8 +4,9 @@ context ~32K) and at every split the decode attention picks.
 - The decode attention at 8 sequences x up to 32767 cached rows runs
   attn_decode_partial<8> (asserted through the per-kernel timers) and matches
   the oracle for every sequence, a ragged batch with a 1-row sequence included.
-- Each split variant (1, 2, 4 sub-chunks of 64 rows per workgroup, and 4
-  sub-chunks of 16 rows for the batch-1 shapes) is selected by a shape that
+- Each split variant (1, 4 or 8 sub-chunks of 64 rows per workgroup, and 4
+  or up to 8 sub-chunks of 16 rows for small batches at long contexts) is
+  selected by a shape that
   the selection rule maps to it, asserted the same way, and matches the
   oracle, ragged batches with 0- and 1-row sequences included; sequences
   with no cached rows take only the new row.
@@ -124,14 +125,16 @@ def test_attn_decode_long_context_split8():
     assert q35mix.attn_decode_variant(8, NKV, lens, q35mix.cu_count()) == "8"
 
 
-@pytest.mark.parametrize("lens", [[8192], [8192, 8192], [8000, 7000, 8000, 6000], [0, 5, 4095],
-                                  [0, 0], [1], [64, 65, 127, 128], [2000, 1999, 37], [4000, 0],
-                                  [4000, 1]])
+SPLIT_SHAPES = [[8192], [8193], [8320], [16384], [8192, 8192], [8000, 7000, 8000, 6000], [0, 5, 4095],
+                [0, 0], [1], [64, 65, 127, 128], [2000, 1999, 37], [4000, 0], [4000, 1], [32767]]
+
+
+@pytest.mark.parametrize("lens", SPLIT_SHAPES)
 def test_attn_decode_split_variants(lens):
-    """Shapes whose selected split is 1, 2 or 4 sub-chunks of 64 rows or 4
-    of 16 rows per workgroup (the batch-1 8192-row shape among them),
-    sequences with no cached rows, and cached lengths at and around sub-chunk
-    boundaries."""
+    """Shapes whose selected split is 1 or 4 sub-chunks of 64 rows, or 4 or
+    up to 8 of 16 rows per workgroup (the batch-1 8192-row shape and the
+    lengths just past it among them), sequences with no cached rows, and
+    cached lengths at and around sub-chunk boundaries."""
     want = q35mix.attn_decode_variant(len(lens), NKV, lens, q35mix.cu_count())
     ran = attn_batch_case(lens, salt=20 + len(lens))
     assert ran == want, (ran, want)
@@ -140,11 +143,9 @@ def test_attn_decode_split_variants(lens):
 def test_attn_decode_variants_cover_all_splits():
     """The parametrized shapes above reach every split on this device."""
     cu = q35mix.cu_count()
-    shapes = [[8192], [8192, 8192], [8000, 7000, 8000, 6000], [0, 5, 4095], [0, 0], [1],
-              [64, 65, 127, 128], [2000, 1999, 37], [4000, 0], [4000, 1],
-              [32700, 30011, 28417, 24576, 20480, 16384, 32767, 1]]
+    shapes = SPLIT_SHAPES + [[32700, 30011, 28417, 24576, 20480, 16384, 32767, 1]]
     got = {q35mix.attn_decode_variant(len(x), NKV, x, cu) for x in shapes}
-    assert got == {"1", "2", "4", "8", "4,16"}, (cu, got)
+    assert got == {"1", "4", "8", "4,16", "8,16"}, (cu, got)
 
 
 def test_reduced_stack_long_context():
