@@ -218,10 +218,12 @@ def bench_attn_prefill(steps, warmup, T=2048):
     return ms, kt
 
 
-def bench_linear_q(qtype, n_in, n_out, steps, warmup, copies, tokens=1):
+def bench_linear_q(qtype, n_in, n_out, steps, warmup, copies, tokens=1, order=0):
     """Projection of `tokens` rows (1: the decode GEMV) rotating over `copies`
-    weight copies, more bytes than the 256 MB MALL."""
+    weight copies, more bytes than the 256 MB MALL; `order` is the
+    projection order (q35m_set_projection_order)."""
     ctx = q35mix.Context(q35mix.qwen35_config(num_layers=1, is_recurrent=[1]), 1, 16)
+    ctx.set_projection_order(order)
     w = synth.quant_weights(qtype, n_out, n_in)
     ws = [ctx.bytes_array(w) for _ in range(copies)]
     x = ctx.array((tokens, n_in), synth.normal(310, tokens * n_in))
@@ -722,10 +724,14 @@ def main():
         log("[bench] Q6_K projection 4096 -> 2560, 2048 tokens ...")
         ms, kt, by = bench_linear_q(6, 4096, 2560, K, W, 1, tokens=2048)
         macs = 2048 * 4096 * 2560
+        msb, ktb, _ = bench_linear_q(6, 4096, 2560, K, W, 1, tokens=2048, order=q35mix.PROJ_BLOCK)
         workloads["linear_q6k_4096x2560_t2048"] = {
             "ms": ms, "tokens_per_s": 2048 / (ms / 1e3),
             "int8_mfma_frac": 2 * macs / (ms / 1e3) / INT8_PEAK,
-            "kernels_ms": {k: v[0] for k, v in kt.items()}}
+            "kernels_ms": {k: v[0] for k, v in kt.items()},
+            "block_order_ms": msb, "block_order_tokens_per_s": 2048 / (msb / 1e3),
+            "block_order_int8_mfma_frac": 2 * macs / (msb / 1e3) / INT8_PEAK,
+            "block_order_kernels_ms": {k: v[0] for k, v in ktb.items()}}
         log(f"[bench] linear_q6k_4096x2560_t2048: {workloads['linear_q6k_4096x2560_t2048']}")
     if want("boundary"):
         log("[bench] layer boundary (add + RMSNorm + Q8_K), 2048 x 2560 ...")

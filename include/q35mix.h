@@ -367,6 +367,20 @@ int q35m_linear_stq1_0(q35m_ctx* ctx, const void* w, const float* x, float* y, i
 int q35m_linear_f32(q35m_ctx* ctx, const float* w, const float* x, float* y, int n_in, int n_out,
                     int tokens);
 
+/* Accumulation order of the quantized projections for several tokens.
+ * Q35M_PROJ_REFERENCE (the default): the reference's fp32 order, bit for bit
+ * (see above).  Q35M_PROJ_BLOCK: for Q6_K with tokens >= 16 (and n_out * n_in
+ * / 256 even), the exact integer sum of each 256-value block (scale * (v -
+ * 32) * q8 over all its sub-blocks, in int32) times its fp32 scales, once per
+ * block: the reference's integer part exactly, its 8 per-lane fp32 chains
+ * regrouped, so results agree with it within fp32 rounding of the exact value
+ * rather than bit for bit (about 1.5x faster at 2048 tokens).  Other formats,
+ * one token and the other Q6_K shapes keep the reference's order.  No
+ * counterpart in the reference (it has one order per path). */
+#define Q35M_PROJ_REFERENCE 0
+#define Q35M_PROJ_BLOCK 1
+int q35m_set_projection_order(q35m_ctx* ctx, int order);
+
 /* The layer boundary around a mixer: hidden[t] += delta[t] (fp32 adds,
  * written back; delta NULL: no add), then y[t] = RmsNormZeroCentered(hidden[t],
  * weight) = (h * scale) * (1 + weight) with scale = 1 / sqrt(mean(h^2) + eps),

@@ -189,7 +189,7 @@ const char* kernel_name(int id) {
         "attn_decode_merge",      "attn_prefill_prep",       "attn_prefill_flash",
         "q8k_quantize",           "linear_q<4>",             "linear_q<6>",
         "q4k_gemm", "q6k_gemm", "add_rmsnorm", "linear_qs<5>", "linear_qs<14>", "linear_f32", "linear_qt<2>",
-        "linear_qt<1>", "attn_decode_partial<4,16>", "attn_decode_partial<8,16>"};
+        "linear_qt<1>", "attn_decode_partial<4,16>", "attn_decode_partial<8,16>", "q6k_gemm_blk"};
     return (id >= 0 && id < K_COUNT) ? names[id] : nullptr;
 }
 
@@ -621,6 +621,15 @@ static int linear_q(q35m_ctx* ctx, int qtype, const void* w, const float* x, flo
     if ((r = check_linear_type(qtype, n_in))) return r;
     HIP_TRY(q35::ensure_work(ctx, q35::linear_q_work_bytes(n_in, tokens)), "workspace");
     HIP_TRY(q35::launch_linear_q(ctx, qtype, w, x, y, n_in, n_out, tokens), "linear_q");
+    return Q35M_OK;
+}
+
+int q35m_set_projection_order(q35m_ctx* ctx, int order) {
+    int r = check_ctx(ctx);
+    if (r) return r;
+    if (order != Q35M_PROJ_REFERENCE && order != Q35M_PROJ_BLOCK)
+        return fail(Q35M_ERR_INVALID, "unknown projection order %d", order);
+    ctx->proj_order = order;
     return Q35M_OK;
 }
 

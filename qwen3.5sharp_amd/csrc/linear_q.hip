@@ -1267,6 +1267,179 @@ void q6k_gemm(const unsigned char* __restrict__ w, const uint32_t* __restrict__ 
 }
 
 
+// ---------------------------------------------------------------- block order, several tokens
+
+// Opt-in order for Q6_K with several tokens (q35m_set_projection_order,
+// block order): per (token, row) and 256-value block, the whole integer sum
+//   isum = sum over the block of scale(sub-block) * (v - 32) * q8
+// is formed exactly in int32 (|isum| < 2^31), and the fp32 scales apply once
+// per block: acc = fma((float)isum, dw * dx, acc).  The integer part is the
+// reference's, exactly; only the fp32 accumulation order differs from its 8
+// per-lane chains and their horizontal sum, within fp32 rounding of the
+// exact value.  The sub-block scales fold into the weights as two int8
+// planes, scale * (v - 32) = 128 hi + lo, so one v_mfma_i32_16x16x64_i8 per
+// plane covers 64 values of every sub-block it meets and the 4 K-steps of a
+// block accumulate in the MFMA's own int32 registers: no VALU work per
+// sub-block or lane, only per block (half the MFMAs of the reference-order
+// kernel, which needs one product set per lane).  Operand layout of a
+// 64-value K-step ks: lane (n = l16, lane group lg) holds values 64 ks +
+// 16 lg .. + 15 of its token (A: 16 consecutive Q8_K bytes) and of its row
+// (B: the same values of the row's block, scale-folded), which lie in one
+// sub-block, so a lane needs one scale per K-step.  A workgroup of 8 waves
+// takes 128 tokens x 128 rows, a wave 128 tokens x 16 rows (8 token tiles,
+// so each row's planes serve 8 MFMAs); blocks are double-buffered in LDS,
+// the next one loaded by buffer loads straight into LDS.
+//
+// The same scheme for Q4_K (sc * q4 <= 945 as two planes) gives no gain: its
+// reference kernel already needs one 16x16x32 product per sub-block, and on
+// gfx950 a 16x16x64 product takes the cycles of a 16x16x32 one, so the planes
+// double the MFMA work that the saved VALU pays for (190-200 vs 188-205 us
+// at 2048 tokens x 2560 -> 8192; one 16x16x32 product per sub-block with
+// the scale applied by an int32 multiply-add measured 207 us).  Q4_K keeps
+// the reference's order.
+constexpr int BT = 128, BR = 128;
+constexpr int BTHREADS = 512, BWAVES = BTHREADS / 64;
+constexpr int BX_CHUNKS = BT * Q8K_WORDS / 4;                               // 2432
+constexpr int BX_RUNS = (BX_CHUNKS + 64 * BWAVES - 1) / (64 * BWAVES);      // 5
+
+// Per-lane offsets of block 0 for the activation staging of a workgroup
+// (wave-wide load m covers chunks 64 (wave + BWAVES m) ..).
+__device__ __forceinline__ void blk_x_offsets(uint32_t (&xvo)[BX_RUNS], int tok0, int tokens, int nb, int wave,
+                                              int lane) {
+#pragma unroll
+    for (int m = 0; m < BX_RUNS; ++m) {
+        const int i = 64 * (wave + BWAVES * m) + lane;
+        xvo[m] = (uint32_t)min(tok0 + i / 19, tokens - 1) * nb * Q8K_WORDS * 4 + 16 * (i % 19);
+    }
+}
+
+// Q6_K in block order.  Weight value w = scale(sub-block of 16) * (v - 32)
+// (v the 6-bit value), |w| <= 4096, split as 128 hi + lo (hi in [-32, 32],
+// lo in [0, 127]): 2 w = scale * 2v - 64 scale is formed in 16-bit pairs and
+// its high byte and bits 1-7 of its low byte are the planes.  The bsums term
+// of the reference's lanes is the -32 inside w.  Lane group lg of K-step ks
+// takes the 16 values of part (n = ks / 2, j = 2 (ks % 2) + lg / 2) at bytes
+// 16 (lg % 2) .. + 15: low (j < 2) or high nibbles of ql bytes 64 n +
+// 32 (j % 2) + 16 (lg % 2) .., with bits 2j, 2j + 1 of qh bytes 32 n +
+// 16 (lg % 2) ..; they are values 128 n + 32 j + 16 (lg % 2) .., one
+// sub-block, i.e. the Q8_K bytes 64 ks + 16 lg .. (as the A operand reads
+// them).  Weights are staged per row as the 53 dwords from the 4-byte
+// boundary below the row's 2-byte-aligned block (realigned on read).
+constexpr int BW6_STRIDE = 53;
+
+__device__ __forceinline__ void q6_split_signed(uint32_t v2, int sc, uint32_t& lo, uint32_t& hi) {
+    const s16x2 s2 = {(short)sc, (short)sc};
+    const s16x2 o2 = {(short)(64 * sc), (short)(64 * sc)};
+    const uint32_t a = __builtin_bit_cast(
+        uint32_t, __builtin_bit_cast(s16x2, __builtin_amdgcn_perm(0u, v2, 0x0c010c00u)) * s2 - o2);
+    const uint32_t b = __builtin_bit_cast(
+        uint32_t, __builtin_bit_cast(s16x2, __builtin_amdgcn_perm(0u, v2, 0x0c030c02u)) * s2 - o2);
+    lo = (__builtin_amdgcn_perm(b, a, 0x06040200u) >> 1) & 0x7f7f7f7fu;
+    hi = __builtin_amdgcn_perm(b, a, 0x07050301u);
+}
+
+__global__ __launch_bounds__(BTHREADS) __attribute__((amdgpu_waves_per_eu(2)))
+void q6k_gemm_blk(const unsigned char* __restrict__ w, const uint32_t* __restrict__ q8, float* __restrict__ y,
+                  int n_in, int n_rows, int n_out, int tokens) {
+#pragma clang fp contract(off)
+    const int nb = n_in / QK;
+    const int row0 = blockIdx.x * BR, tok0 = blockIdx.y * BT;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int l16 = lane & 15, lg = lane >> 4;
+
+    __shared__ uint32_t wsh[2][BR * BW6_STRIDE];
+    __shared__ uint4 xsh[2][BX_CHUNKS];
+
+    const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<unsigned char*>(w), 0, (int)((uint32_t)n_rows * nb * Q6K_BYTES), 0x00020000);
+    const __amdgpu_buffer_rsrc_t xrs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint32_t*>(q8), 0, (int)((uint32_t)tokens * nb * Q8K_WORDS * 4), 0x00020000);
+    uint32_t xvo[BX_RUNS];
+    blk_x_offsets(xvo, tok0, tokens, nb, wave, lane);
+    auto stage = [&](int b, int buf) {
+        // rows wave, wave + 8, ...: one wave-wide load of 53 dwords each
+#pragma unroll
+        for (int i = 0; i < BR / BWAVES; ++i) {
+            const int r = wave + BWAVES * i;
+            const uint32_t so = (((uint32_t)min(row0 + r, n_rows - 1) * nb + b) * Q6K_BYTES) & ~3u;
+            if (lane < BW6_STRIDE) dma_b32(wrs, &wsh[buf][BW6_STRIDE * r], 4u * lane, so);
+        }
+#pragma unroll
+        for (int m = 0; m < BX_RUNS; ++m)
+            if (64 * (wave + BWAVES * m) < BX_CHUNKS)
+                dma_b128(xrs, &xsh[buf][64 * (wave + BWAVES * m)], xvo[m], (uint32_t)b * Q8K_WORDS * 4);
+    };
+    // Byte offset of the row's block in its staged dwords: 0 or 2, alternating with b.
+    const int rpar = (min(row0 + 16 * wave + l16, n_rows - 1) * nb) & 1;
+
+    float acc[8][4];
+#pragma unroll
+    for (int tt = 0; tt < 8; ++tt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[tt][r] = 0.0f;
+
+    const int h = lg & 1;
+    stage(0, 0);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    for (int b = 0; b < nb; ++b) {
+        const int buf = b & 1;
+        if (b + 1 < nb) stage(b + 1, buf ^ 1);
+        const uint32_t* wr = &wsh[buf][BW6_STRIDE * (16 * wave + l16)];
+        const int shift = 2 * (rpar ^ (b & 1));
+        const unsigned char* wb = reinterpret_cast<const unsigned char*>(wr) + shift;
+        auto wd = [&](int f) { return __builtin_amdgcn_alignbyte(wr[f + 1], wr[f], shift); };
+        const uint32_t* X = reinterpret_cast<const uint32_t*>(xsh[buf]);
+        i32x4 dh[8], dl[8];
+#pragma unroll
+        for (int tt = 0; tt < 8; ++tt) dh[tt] = dl[tt] = i32x4{0, 0, 0, 0};
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) {
+            const int n = ks >> 1, j = 2 * (ks & 1) + (lg >> 1);
+            const int sc = (int)(int8_t)wb[192 + 8 * n + 2 * j + h];
+            // rotations: the nibble to bits 1-4, the qh bit pair to bits 5-6
+            const uint32_t rq = (j >> 1) ? 3 : 31, rh = (uint32_t)(27 + 2 * j) & 31;
+            uint32_t lo[4], hi[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const uint32_t ql = wd(16 * n + 8 * (j & 1) + 4 * h + i), qh = wd(32 + 8 * n + 4 * h + i);
+                const uint32_t v2 = (__builtin_amdgcn_alignbit(ql, ql, rq) & 0x1e1e1e1eu) |
+                                    (__builtin_amdgcn_alignbit(qh, qh, rh) & 0x60606060u);
+                q6_split_signed(v2, sc, lo[i], hi[i]);
+            }
+            const i32x4 bh = {(int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
+            const i32x4 bl = {(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3]};
+#pragma unroll
+            for (int tt = 0; tt < 8; ++tt) {
+                const i32x4 a = *reinterpret_cast<const i32x4*>(X + (16 * tt + l16) * Q8K_WORDS + Q8K_QS + 16 * ks + 4 * lg);
+                dh[tt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, bh, dh[tt], 0, 0, 0);
+                dl[tt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, bl, dl[tt], 0, 0, 0);
+            }
+        }
+        const float dw = half_bits_to_float((uint32_t)wb[208] | ((uint32_t)wb[209] << 8));
+#pragma unroll
+        for (int tt = 0; tt < 8; ++tt)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float dxr = __builtin_bit_cast(float, X[(16 * tt + 4 * lg + r) * Q8K_WORDS]);
+                const int isum = (int)((uint32_t)dh[tt][r] << 7) + dl[tt][r];
+                acc[tt][r] = fmaf((float)isum, dw * dxr, acc[tt][r]);
+            }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+    }
+    const int row = row0 + 16 * wave + l16;
+#pragma unroll
+    for (int tt = 0; tt < 8; ++tt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int t = tok0 + 16 * tt + 4 * lg + r;
+            if (row < n_rows && t < tokens) y[(size_t)t * n_out + row] = acc[tt][r];
+        }
+}
+
+
 // ---------------------------------------------------------------- layer boundary
 
 // Ops.AddInPlace (Ops.cs:677-710) then Qwen35Ops.RmsNormZeroCentered
@@ -1450,8 +1623,11 @@ hipError_t launch_linear_q_prequant(q35m_ctx* c, int qtype, const void* w, const
     // Q6_K: the tiled kernel from 16 tokens when n_out * n_in / 256 is even
     // (see q6k_gemm), the per-token GEMV otherwise; both keep the same
     // per-token arithmetic, so the results are identical.
-    if (qtype == 6 && tokens >= 16 && (((size_t)n_out * nb) & 1) == 0)
+    if (qtype == 6 && tokens >= 16 && (((size_t)n_out * nb) & 1) == 0) {
+        if (c->proj_order == Q35M_PROJ_BLOCK)
+            return tiled(q6k_gemm_blk, K_Q6K_GEMM_BLK, Q6K_BYTES, BR, BT, BTHREADS, n_out);
         return tiled(q6k_gemm, K_Q6K_GEMM, Q6K_BYTES, SGR, SGT, 256, n_out);
+    }
     const int rows_per_wg = min(LQ_THREADS / nb, LQ_MAX_ROWS);
     const int grid = (n_out - row_base + rows_per_wg - 1) / rows_per_wg;
     const int bb = qtype == 4 ? Q4K_BYTES : Q6K_BYTES;

@@ -90,6 +90,7 @@ enum KernelId {
     K_STQ1_0_LINEAR,
     K_ATTN_DECODE_PARTIAL4R16,   // attn_decode_partial, 4 sub-chunks of 16 rows per workgroup
     K_ATTN_DECODE_PARTIAL8R16,   // attn_decode_partial, up to 8 sub-chunks of 16 rows per workgroup
+    K_Q6K_GEMM_BLK,              // block-order Q6_K projection (q35m_set_projection_order)
     K_COUNT
 };
 const char* kernel_name(int id);
@@ -144,6 +145,9 @@ struct q35m_ctx {
     // Q35M_TILE_LIMIT_BYTES, read at create, lowers it (tests use it to make
     // ordinary shapes go in pieces).
     size_t tile_limit = (size_t)1 << 31;
+    // Accumulation order of the projections for several tokens
+    // (q35m_set_projection_order): Q35M_PROJ_REFERENCE or Q35M_PROJ_BLOCK.
+    int proj_order = Q35M_PROJ_REFERENCE;
     std::vector<void*> allocations;
     // Per-kernel event timers (off unless q35m_profile enables them).
     bool profile = false;

@@ -21,6 +21,7 @@ OK = 0
 ERR_INVALID, ERR_UNSUPPORTED, ERR_CAPACITY, ERR_NO_DEVICE, ERR_HIP, ERR_OOM, ERR_RANGE = \
     -1, -2, -3, -4, -5, -6, -7
 STATE_RECURRENT, STATE_CONV, STATE_KEYS, STATE_VALUES = 0, 1, 2, 3
+PROJ_REFERENCE, PROJ_BLOCK = 0, 1
 
 _lib = None
 _hip = None
@@ -450,6 +451,10 @@ class Context:
         fn = getattr(lib(), f"q35m_linear_{self._LINEAR[qtype]}")
         check(fn(ctypes.c_void_p(self.handle), ctypes.c_void_p(w.ptr), ctypes.c_void_p(x.ptr),
                  ctypes.c_void_p(y.ptr), n_in, n_out, tokens))
+
+    def set_projection_order(self, order: int) -> None:
+        """PROJ_REFERENCE (0, default) or PROJ_BLOCK (1): q35m_set_projection_order."""
+        check(lib().q35m_set_projection_order(ctypes.c_void_p(self.handle), order))
 
     def linear_f32(self, w, x, y, n_in, n_out, tokens) -> None:
         """y[tokens][n_out] = W x for F32 weights W [n_out][n_in] (Ops.DotF32 order)."""

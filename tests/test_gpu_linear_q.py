@@ -182,3 +182,48 @@ def test_tiled_pieces_match_whole_launch(monkeypatch, qtype):
         assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
     finally:
         c.close()
+
+
+BLOCK_SHAPES = [(2560, 8192, 2048), (4096, 2560, 2048), (2560, 520, 70), (512, 33, 5), (4096, 136, 130),
+                (16384, 19, 2), (1024, 72, 16), (2560, 1024, 3), (256, 7, 129)]
+
+
+@pytest.mark.parametrize("qtype", [4, 6])
+@pytest.mark.parametrize("n_in,n_out,tokens", BLOCK_SHAPES)
+def test_linear_q_block_order(ctx, qtype, n_in, n_out, tokens):
+    """q35m_set_projection_order(PROJ_BLOCK): Q6_K from 16 tokens (n_out *
+    n_in / 256 even) accumulates each block's exact integer sum and applies
+    its fp32 scales once.  Checked against the exact value of the quantized
+    product (fp64 of the dequantized weights and Q8_K activations: |y - exact|
+    <= 2e-6 sum |w x|, the bound the reference's own order meets) and against
+    the oracle's reference order (max|d| / max|ref| <= 1e-4); Q4_K and the
+    shapes outside the block-order condition stay bit-identical to the
+    reference order."""
+    say(f"linear_q block order {NAMES[qtype]} n_in={n_in} n_out={n_out} tokens={tokens}")
+    rng = np.random.default_rng(7000 + 1000 * qtype + n_in + n_out + tokens)
+    w = qb.random_blocks(rng, qtype, qb.nblocks(qtype, n_out * n_in))
+    x = rng.standard_normal((tokens, n_in)).astype(np.float32)
+    ctx.set_projection_order(q35mix.PROJ_BLOCK)
+    try:
+        got = run(ctx, qtype, w, x, n_in, n_out)
+    finally:
+        ctx.set_projection_order(q35mix.PROJ_REFERENCE)
+    blocked = qtype == 6 and tokens >= 16 and (n_out * n_in // 256) % 2 == 0
+    check_rows = min(tokens, 24)
+    sel = np.unique(np.linspace(0, tokens - 1, check_rows).astype(int))
+    want = oracle.linear_q(qtype, w, x[sel], n_in, n_out)
+    if not blocked:
+        assert np.array_equal(got[sel].view(np.uint32), want.view(np.uint32))
+        return
+    e = float(np.max(np.abs(got[sel] - want)) / np.max(np.abs(want)))
+    wd = qb.dequant_f64(qtype, w).reshape(n_out, n_in)
+    worst = 0.0
+    for i, t in enumerate(sel):
+        d, q, _ = qb.parse_q8k(oracle.q8k_quantize(x[t]))
+        xd = (d[:, None].astype(np.float64) * q).ravel()
+        exact = wd @ xd
+        scale = np.abs(wd) @ np.abs(xd)
+        worst = max(worst, float(np.max(np.abs(got[t] - exact) / scale)))
+    say(f"  vs reference order {e:.2e}; worst |y - exact| / sum|w x| {worst:.2e}")
+    assert e <= 1e-4
+    assert worst <= 2e-6
