@@ -23,8 +23,9 @@
  *  - Every entry point returns an int status: Q35M_OK (0) or a negative
  *    Q35M_ERR_* code; q35m_last_error() returns a thread-local message.
  *  - Activation pointers (qkv, z, b, a, q_gate, k, v, out) are DEVICE
- *    pointers to fp32, row-major, last index fastest.  Weight setters and
- *    state read/write take HOST pointers.
+ *    pointers to fp32, row-major, last index fastest, 16-byte aligned (the
+ *    kernels move them as 16-byte vectors; q35m_malloc's buffers are).
+ *    Weight setters and state read/write take HOST pointers.
  *  - One context = one device and one HIP stream.  Mixer calls enqueue on
  *    that stream and return; q35m_sync() waits.  A context has no internal
  *    locking (the reference model is single-threaded too); separate contexts

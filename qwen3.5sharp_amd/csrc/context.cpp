@@ -9,6 +9,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <initializer_list>
 #include <mutex>
 #include <string>
 
@@ -127,6 +128,15 @@ int build_seq_batch(const q35m_ctx* c, int n, const int* seqs, q35::SeqBatch* sb
         }
     }
     if (max_cached) *max_cached = mx;
+    return Q35M_OK;
+}
+
+// Mixer activations are read and written as 16-byte vectors.
+int check_activations(std::initializer_list<const void*> ptrs) {
+    for (const void* p : ptrs) {
+        if (!p) return fail(Q35M_ERR_INVALID, "null activation pointer");
+        if ((uintptr_t)p & 15) return fail(Q35M_ERR_INVALID, "activation pointers must be 16-byte aligned");
+    }
     return Q35M_OK;
 }
 
@@ -505,7 +515,7 @@ int q35m_deltanet_decode(q35m_ctx* ctx, int layer, int n, const int* seqs, const
     if (!r) r = check_layer(ctx, layer, true);
     if (r) return r;
     if (!ctx->lin[layer].has_weights) return fail(Q35M_ERR_INVALID, "layer %d has no weights", layer);
-    if (!qkv || !z || !b || !a || !out) return fail(Q35M_ERR_INVALID, "null activation pointer");
+    if ((r = check_activations({qkv, z, b, a, out}))) return r;
     q35::SeqBatch sb;
     r = build_seq_batch(ctx, n, seqs, &sb, nullptr);
     if (r) return r;
@@ -521,7 +531,7 @@ int q35m_deltanet_prefill(q35m_ctx* ctx, int layer, int seq, int T, const float*
     if (r) return r;
     if (!ctx->lin[layer].has_weights) return fail(Q35M_ERR_INVALID, "layer %d has no weights", layer);
     if (T < 1) return fail(Q35M_ERR_INVALID, "T must be >= 1 (got %d)", T);
-    if (!qkv || !z || !b || !a || !out) return fail(Q35M_ERR_INVALID, "null activation pointer");
+    if ((r = check_activations({qkv, z, b, a, out}))) return r;
     HIP_TRY(q35::ensure_work(ctx, q35::deltanet_prefill_work_bytes(ctx->d, T)), "workspace");
     HIP_TRY(q35::launch_deltanet_prefill(ctx, layer, seq, T, qkv, z, b, a, out), "deltanet_prefill");
     return Q35M_OK;
@@ -533,7 +543,7 @@ int q35m_attn_decode(q35m_ctx* ctx, int layer, int n, const int* seqs, const flo
     if (!r) r = check_layer(ctx, layer, false);
     if (r) return r;
     if (!ctx->full[layer].has_weights) return fail(Q35M_ERR_INVALID, "layer %d has no weights", layer);
-    if (!q_gate || !k || !v || !out) return fail(Q35M_ERR_INVALID, "null activation pointer");
+    if ((r = check_activations({q_gate, k, v, out}))) return r;
     q35::SeqBatch sb;
     int max_cached = 0;
     r = build_seq_batch(ctx, n, seqs, &sb, &max_cached);
@@ -551,7 +561,7 @@ int q35m_attn_decode_noalloc(q35m_ctx* ctx, int layer, int n, const int* seqs, c
     if (!r) r = check_layer(ctx, layer, false);
     if (r) return r;
     if (!ctx->full[layer].has_weights) return fail(Q35M_ERR_INVALID, "layer %d has no weights", layer);
-    if (!q_gate || !k || !v || !out) return fail(Q35M_ERR_INVALID, "null activation pointer");
+    if ((r = check_activations({q_gate, k, v, out}))) return r;
     if (!ctx->noalloc_scratch) return fail(Q35M_ERR_NO_DEVICE, "no device scratch");
     q35::SeqBatch sb;
     int max_cached = 0;
@@ -582,7 +592,7 @@ int q35m_attn_prefill(q35m_ctx* ctx, int layer, int seq, int T, const float* q_g
     if (r) return r;
     if (!ctx->full[layer].has_weights) return fail(Q35M_ERR_INVALID, "layer %d has no weights", layer);
     if (T < 1) return fail(Q35M_ERR_INVALID, "T must be >= 1 (got %d)", T);
-    if (!q_gate || !k || !v || !out) return fail(Q35M_ERR_INVALID, "null activation pointer");
+    if ((r = check_activations({q_gate, k, v, out}))) return r;
     int start = ctx->kv_len[seq];
     if ((long)start + T > ctx->cap)
         return fail(Q35M_ERR_CAPACITY, "sequence %d: %d + %d rows exceed KV capacity %d", seq, start,

@@ -176,6 +176,11 @@ int q35m_decode_graph_create(q35m_ctx* ctx, int n, const int* seqs, const q35m_d
             delete g;
             return gfail(Q35M_ERR_INVALID, "layer %d: null activation pointer", l);
         }
+        if (((uintptr_t)x.in0 | (uintptr_t)x.in1 | (uintptr_t)x.in2 | (uintptr_t)x.out |
+             (uintptr_t)(rec ? x.in3 : nullptr)) & 15) {
+            delete g;
+            return gfail(Q35M_ERR_INVALID, "layer %d: activation pointers must be 16-byte aligned", l);
+        }
         any_attn |= !rec;
     }
     g->max_len = max_len;

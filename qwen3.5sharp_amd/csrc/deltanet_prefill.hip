@@ -266,15 +266,15 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep(
     __shared__ float Vs[CH][LDA];      // 64 channels of v, row-major
     __shared__ float Am[CH][LDA];      // -A (strictly lower part of the lower blocks)
     __shared__ float Td[4][16][17];    // inverses of the 16x16 diagonal blocks of I + A
-    __shared__ double Gd[CH];
-    __shared__ float bet[CH], gam[CH], nrm[CH];
-    __shared__ float pre_b[kMaxVPerK][CH], pre_g[kMaxVPerK][CH];
+    __shared__ double Gd[kMaxVPerK][CH];
+    __shared__ float bet[kMaxVPerK][CH], gam[kMaxVPerK][CH];
+    __shared__ float nrm[CH];
 
-    // Inputs of beta and g of the R v-heads (thread = (v-head, token);
-    // padded tokens read the last row and are masked below; threads past
-    // R * CH repeat the last v-head and store nothing).  They are formed
-    // after the conv loads below are out, so those loads do not wait on these.
-    const int grr = min(tid / CH, R - 1), gj = tid % CH, gvh = kh * R + grr;
+    // Inputs of beta and g of the R v-heads (wave = v-head, lane = token;
+    // padded tokens read the last row and are masked below; waves past R
+    // repeat the last v-head and store nothing).  They are formed after the
+    // conv loads below are out, so those loads do not wait on these.
+    const int grr = min(wave, R - 1), gj = lane, gvh = kh * R + grr;
     const size_t gi = (size_t)min(t0 + gj, T - 1) * nv + gvh;
     const float gb_in = bin[gi], ga_in = ain[gi], g_sa = ssm_a[gvh], g_dt = dt_bias[gvh];
 
@@ -290,13 +290,28 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep(
     conv_load<32>(rows, conv_w, cq_k, conv_dim, t0 + 32 * hq, xk, wk);
     __builtin_amdgcn_sched_barrier(0);
     {
-        // Formed by every thread (so the loads above stay where they are)
-        // and stored by the first R * CH.
+        // Gates of every v-head at once, one wave each, formed by every
+        // thread (so the loads above stay where they are) and stored by the
+        // waves below R: beta, g, the fp64 running sum G of g (padded tokens
+        // get beta = g = 0), gamma = e^G and e^{G_last - G}.
+        const bool valid = gj < tn;
         const float bv = 1.0f / (1.0f + expf(-gb_in));
         const float gv = g_sa * softplus_ref(ga_in + g_dt);
-        if (tid < R * CH) {
-            pre_b[grr][gj] = bv;
-            pre_g[grr][gj] = gv;
+        double G = valid ? (double)gv : 0.0;
+#pragma unroll
+        for (int o = 1; o < 64; o <<= 1) {
+            const double up = __shfl_up(G, o, kWave);
+            if (lane >= o) G += up;
+        }
+        const double Glast = __shfl(G, CH - 1, kWave);
+        if (wave < R) {
+            const size_t cidx = (size_t)gvh * nch + n;
+            Gd[wave][lane] = G;
+            bet[wave][lane] = valid ? bv : 0.0f;
+            const float gm = __expf((float)G);
+            gam[wave][lane] = gm;
+            w.gam[cidx * CH + lane] = gm;
+            w.gdec[cidx * CH + lane] = __expf((float)(Glast - G));
         }
     }
     auto conv_qk = [&](int ch, float4 wt, float (&x)[35], float (&y)[32]) {
@@ -413,24 +428,9 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep(
         for (int h = 0; h < 2; ++h)
             conv_load<16>(rows, conv_w, 2 * key_dim + vh * kDk + 64 * h + cl, conv_dim, t0 + 16 * qt,
                           xv[h], wv[h]);
-        // Gates and the fp64 running sum of g; padded tokens get beta = g = 0.
-        if (wave == 0) {
-            const bool valid = lane < tn;
-            const float bv = pre_b[rr][lane], gv = pre_g[rr][lane];
-            double G = valid ? (double)gv : 0.0;
-#pragma unroll
-            for (int o = 1; o < 64; o <<= 1) {
-                const double up = __shfl_up(G, o, kWave);
-                if (lane >= o) G += up;
-            }
-            Gd[lane] = G;
-            bet[lane] = valid ? bv : 0.0f;
-            const float gm = __expf((float)G);
-            gam[lane] = gm;
-            w.gam[cidx * CH + lane] = gm;
-        }
-        lds_barrier();
-        if (wave == 1) w.gdec[cidx * CH + lane] = __expf((float)(Gd[CH - 1] - Gd[lane]));
+        const double* Gh = Gd[rr];
+        const float* bh = bet[rr];
+        const float* gh = gam[rr];
         // Decay masks on the register blocks: -A into LDS, M o QK^T to the workspace.
         float* aqk = w.aqk + cidx * CH * CH;
 #pragma unroll
@@ -442,7 +442,7 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep(
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const int i = 16 * rb + 4 * g + r;
-                    Am[i][j] = j < i ? -bet[i] * __expf((float)(Gd[i] - Gd[j])) * blk[m][r] : 0.0f;
+                    Am[i][j] = j < i ? -bh[i] * __expf((float)(Gh[i] - Gh[j])) * blk[m][r] : 0.0f;
                 }
             } else {
                 const int iq = 16 * rb + c16;   // query token
@@ -451,26 +451,39 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep(
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const int jk = 16 * cb + 4 * g + r;   // key token
-                    vp[r] = jk <= iq ? __expf((float)(Gd[iq] - Gd[jk])) * blk[m][r] : 0.0f;
+                    vp[r] = jk <= iq ? __expf((float)(Gh[iq] - Gh[jk])) * blk[m][r] : 0.0f;
                 }
                 reinterpret_cast<float4*>(aqk)[(rb * 4 + cb) * 64 + lane] = v;
             }
         }
         lds_barrier();
-        // Inverse of each unit-lower 16x16 diagonal block of I + A by forward
-        // substitution: column j of the inverse, x_i = [i == j] + sum_{m<i} (-A)_im x_m.
-        if (lane < 16) {
-            const int j = lane, b0 = 16 * wave;
-            float x[16];
+        // Inverse of the unit-lower 16x16 diagonal block `wave` of I + A on
+        // MFMA: with L its strictly lower part (L^16 = 0),
+        //   (I + L)^-1 = sum_{k<16} (-L)^k = (I + L^8)(I + L^4)(I + L^2)(I - L)
+        // exactly; the factors commute.  A product X Y takes X in the A
+        // layout, which is the D layout of X^T, so the powers of L^T are
+        // formed beside those of L (L^8 is needed transposed only).
+        {
+            const int b0 = 16 * wave;
+            f32x4 dl, dt, id;                // D layouts of L, L^T and I
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                float acc = i == j ? 1.0f : 0.0f;
-#pragma unroll
-                for (int m = 0; m < i; ++m) acc += Am[b0 + i][b0 + m] * x[m];
-                x[i] = i < j ? 0.0f : acc;
+            for (int r = 0; r < 4; ++r) {
+                dl[r] = -Am[b0 + 4 * g + r][b0 + c16];
+                dt[r] = -Am[b0 + c16][b0 + 4 * g + r];
+                id[r] = 4 * g + r == c16 ? 1.0f : 0.0f;
             }
+            auto mm = [](f32x4 xt, f32x4 y) {    // X Y from D(X^T) and D(Y)
+                return mfma16x4(make_float4(xt[0], xt[1], xt[2], xt[3]), y, f32x4{0.f, 0.f, 0.f, 0.f});
+            };
+            const f32x4 l2 = mm(dt, dl), l2t = mm(dl, dt);
+            const f32x4 l4 = mm(l2t, l2), l4t = mm(l2, l2t);
+            const f32x4 l8t = mm(l4, l4t);
+            f32x4 x = id - dl;                   // I - L
+            x = mm(id + l2t, x);
+            x = mm(id + l4t, x);
+            x = mm(id + l8t, x);
 #pragma unroll
-            for (int i = 0; i < 16; ++i) Td[wave][i][j] = x[i];
+            for (int r = 0; r < 4; ++r) Td[wave][4 * g + r][c16] = x[r];
         }
         lds_barrier();
         // Y = (I + A)^-1 X for X = diag(beta gamma) K^ (-> W) and diag(beta) V (-> U),
@@ -500,8 +513,8 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep(
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const int row = 16 * ib + 4 * g + r;
-                    const float bt = bet[row];
-                    accK[r] = Ks[row][16 * kb + c16] * bt * gam[row];
+                    const float bt = bh[row];
+                    accK[r] = Ks[row][16 * kb + c16] * bt * gh[row];
                     accV[r] = Vs[row][16 * wave + c16] * bt;
                 }
 #pragma unroll

@@ -327,3 +327,30 @@ def test_graph_refusals():
         assert e.value.code == q35mix.ERR_INVALID           # no weights
     finally:
         fresh.close()
+
+
+def test_misaligned_activations_refused():
+    """Activation pointers must be 16-byte aligned (the kernels move 16-byte
+    vectors): a pointer 4 bytes past an aligned buffer is refused by the
+    mixer entry points and by the decode graph."""
+    st = Stack([1, 0], 1, [10], 64, salt=13)
+    c = st.c
+    try:
+        base = c.array((1, c.conv_dim + 4))
+        bad = q35mix.DeviceView(base, 1, (1, c.conv_dim))
+        d = st.io[0]
+        with pytest.raises(q35mix.Q35Error) as e:
+            c.deltanet_decode(0, [0], bad, d[1], d[2], d[3], d[4])
+        assert e.value.code == q35mix.ERR_INVALID and "aligned" in str(e.value)
+        abase = c.array((1, 2 * c.q_dim + 4))
+        abad = q35mix.DeviceView(abase, 1, (1, 2 * c.q_dim))
+        a = st.io[1]
+        with pytest.raises(q35mix.Q35Error) as e:
+            c.attn_decode(1, [0], abad, a[1], a[2], a[4])
+        assert e.value.code == q35mix.ERR_INVALID
+        with pytest.raises(q35mix.Q35Error) as e:
+            q35mix.DecodeGraph(c, [0], [(bad,) + tuple(d[1:]), a], 64)
+        assert e.value.code == q35mix.ERR_INVALID
+        assert c.kv_len(0) == 10
+    finally:
+        st.close()
