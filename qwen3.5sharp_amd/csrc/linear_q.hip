@@ -1286,9 +1286,11 @@ void q6k_gemm(const unsigned char* __restrict__ w, const uint32_t* __restrict__ 
 // 16 lg .. + 15 of its token (A: 16 consecutive Q8_K bytes) and of its row
 // (B: the same values of the row's block, scale-folded), which lie in one
 // sub-block, so a lane needs one scale per K-step.  A workgroup of 8 waves
-// takes 128 tokens x 128 rows, a wave 128 tokens x 16 rows (8 token tiles,
-// so each row's planes serve 8 MFMAs); blocks are double-buffered in LDS,
-// the next one loaded by buffer loads straight into LDS.
+// takes 192 tokens x 128 rows, a wave 192 tokens x 16 rows (12 token tiles,
+// so each row's planes serve 12 MFMAs); blocks are double-buffered in LDS
+// (155 KiB), the next one loaded by buffer loads straight into LDS.  192
+// tokens make 2048 tokens x 2560 rows one round of 220 workgroups, one per
+// CU (128 tokens took 320 workgroups, 1.25 rounds: 130 us).
 //
 // The same scheme for Q4_K (sc * q4 <= 945 as two planes) gives no gain: its
 // reference kernel already needs one 16x16x32 product per sub-block, and on
@@ -1297,10 +1299,13 @@ void q6k_gemm(const unsigned char* __restrict__ w, const uint32_t* __restrict__ 
 // at 2048 tokens x 2560 -> 8192; one 16x16x32 product per sub-block with
 // the scale applied by an int32 multiply-add measured 207 us).  Q4_K keeps
 // the reference's order.
-constexpr int BT = 128, BR = 128;
+constexpr int BT = 192, BR = 128, BTILES = BT / 16;
 constexpr int BTHREADS = 512, BWAVES = BTHREADS / 64;
-constexpr int BX_CHUNKS = BT * Q8K_WORDS / 4;                               // 2432
-constexpr int BX_RUNS = (BX_CHUNKS + 64 * BWAVES - 1) / (64 * BWAVES);      // 5
+// Only d and qs of a Q8_K block are staged (17 of its 19 16-byte chunks;
+// the block sums are not used), 68 words a token.
+constexpr int BX_TOK_CHUNKS = Q8K_BS / 4, BX_TOK_WORDS = 4 * BX_TOK_CHUNKS;
+constexpr int BX_CHUNKS = BT * BX_TOK_CHUNKS;                               // 3264
+constexpr int BX_RUNS = (BX_CHUNKS + 64 * BWAVES - 1) / (64 * BWAVES);      // 7
 
 // Per-lane offsets of block 0 for the activation staging of a workgroup
 // (wave-wide load m covers chunks 64 (wave + BWAVES m) ..).
@@ -1309,7 +1314,7 @@ __device__ __forceinline__ void blk_x_offsets(uint32_t (&xvo)[BX_RUNS], int tok0
 #pragma unroll
     for (int m = 0; m < BX_RUNS; ++m) {
         const int i = 64 * (wave + BWAVES * m) + lane;
-        xvo[m] = (uint32_t)min(tok0 + i / 19, tokens - 1) * nb * Q8K_WORDS * 4 + 16 * (i % 19);
+        xvo[m] = (uint32_t)min(tok0 + i / BX_TOK_CHUNKS, tokens - 1) * nb * Q8K_WORDS * 4 + 16 * (i % BX_TOK_CHUNKS);
     }
 }
 
@@ -1373,9 +1378,9 @@ void q6k_gemm_blk(const unsigned char* __restrict__ w, const uint32_t* __restric
     // Byte offset of the row's block in its staged dwords: 0 or 2, alternating with b.
     const int rpar = (min(row0 + 16 * wave + l16, n_rows - 1) * nb) & 1;
 
-    float acc[8][4];
+    float acc[BTILES][4];
 #pragma unroll
-    for (int tt = 0; tt < 8; ++tt)
+    for (int tt = 0; tt < BTILES; ++tt)
 #pragma unroll
         for (int r = 0; r < 4; ++r) acc[tt][r] = 0.0f;
 
@@ -1391,9 +1396,9 @@ void q6k_gemm_blk(const unsigned char* __restrict__ w, const uint32_t* __restric
         const unsigned char* wb = reinterpret_cast<const unsigned char*>(wr) + shift;
         auto wd = [&](int f) { return __builtin_amdgcn_alignbyte(wr[f + 1], wr[f], shift); };
         const uint32_t* X = reinterpret_cast<const uint32_t*>(xsh[buf]);
-        i32x4 dh[8], dl[8];
+        i32x4 dh[BTILES], dl[BTILES];
 #pragma unroll
-        for (int tt = 0; tt < 8; ++tt) dh[tt] = dl[tt] = i32x4{0, 0, 0, 0};
+        for (int tt = 0; tt < BTILES; ++tt) dh[tt] = dl[tt] = i32x4{0, 0, 0, 0};
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
             const int n = ks >> 1, j = 2 * (ks & 1) + (lg >> 1);
@@ -1411,18 +1416,18 @@ void q6k_gemm_blk(const unsigned char* __restrict__ w, const uint32_t* __restric
             const i32x4 bh = {(int)hi[0], (int)hi[1], (int)hi[2], (int)hi[3]};
             const i32x4 bl = {(int)lo[0], (int)lo[1], (int)lo[2], (int)lo[3]};
 #pragma unroll
-            for (int tt = 0; tt < 8; ++tt) {
-                const i32x4 a = *reinterpret_cast<const i32x4*>(X + (16 * tt + l16) * Q8K_WORDS + Q8K_QS + 16 * ks + 4 * lg);
+            for (int tt = 0; tt < BTILES; ++tt) {
+                const i32x4 a = *reinterpret_cast<const i32x4*>(X + (16 * tt + l16) * BX_TOK_WORDS + Q8K_QS + 16 * ks + 4 * lg);
                 dh[tt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, bh, dh[tt], 0, 0, 0);
                 dl[tt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, bl, dl[tt], 0, 0, 0);
             }
         }
         const float dw = half_bits_to_float((uint32_t)wb[208] | ((uint32_t)wb[209] << 8));
 #pragma unroll
-        for (int tt = 0; tt < 8; ++tt)
+        for (int tt = 0; tt < BTILES; ++tt)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const float dxr = __builtin_bit_cast(float, X[(16 * tt + 4 * lg + r) * Q8K_WORDS]);
+                const float dxr = __builtin_bit_cast(float, X[(16 * tt + 4 * lg + r) * BX_TOK_WORDS]);
                 const int isum = (int)((uint32_t)dh[tt][r] << 7) + dl[tt][r];
                 acc[tt][r] = fmaf((float)isum, dw * dxr, acc[tt][r]);
             }
@@ -1431,7 +1436,7 @@ void q6k_gemm_blk(const unsigned char* __restrict__ w, const uint32_t* __restric
     }
     const int row = row0 + 16 * wave + l16;
 #pragma unroll
-    for (int tt = 0; tt < 8; ++tt)
+    for (int tt = 0; tt < BTILES; ++tt)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
             const int t = tok0 + 16 * tt + 4 * lg + r;
