@@ -235,8 +235,9 @@ __device__ __forceinline__ int tri_cb(int i) { return i - tri_rb(i) * (tri_rb(i)
 // chunk's inputs (Prefill.cs:181-248), then the chunked WY preparation.
 //  - q and k of the k-head: conv + SiLU (thread = channel, 32 tokens) into a
 //    row-major LDS tile, L2 norm per token (q also / sqrt(dk)); q goes to the
-//    workspace in the A layout (for Q K^T and the scan's Q S), k in the D
-//    layout (the scan's K^T D), and k stays in LDS for the rest.
+//    workspace in the A layout (the scan's Q S) and stays in LDS for Q K^T
+//    (in the space the per-head tiles take later), k goes out in the D
+//    layout (the scan's K^T D) and stays in LDS for the rest.
 //  - beta = sigmoid(b), g = ssm_a * softplus(a + dt_bias) of the R v-heads.
 //  - K K^T and (Q K^T)^T once for the R v-heads (their 20 lower 16x16 blocks,
 //    5 per wave, kept in registers); (Q K^T)^T = K Q^T comes out of the MFMA
@@ -262,9 +263,15 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep(
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int g = lane >> 4, c16 = lane & 15;
 
-    __shared__ float Ks[CH][kDk + 4];  // q, then k^ of the chunk, row-major
-    __shared__ float Vs[CH][LDA];      // 64 channels of v, row-major
-    __shared__ float Am[CH][LDA];      // -A (strictly lower part of the lower blocks)
+    __shared__ float Ks[CH][kDk + 4];  // k^ of the chunk, row-major
+    // Vs (64 channels of v, row-major) and Am (-A, the strictly lower part of
+    // the lower blocks) of the per-head phase share their space with Qs, the
+    // chunk's q^ (row-major), which is needed only until Q K^T is formed.
+    static_assert(CH * (kDk + 4) <= 2 * CH * LDA, "q^ tile must fit in the v and A tiles");
+    __shared__ float4 vaq[2 * CH * LDA / 4];
+    float (*Vs)[LDA] = reinterpret_cast<float (*)[LDA]>(vaq);
+    float (*Am)[LDA] = reinterpret_cast<float (*)[LDA]>(reinterpret_cast<float*>(vaq) + CH * LDA);
+    float (*Qs)[kDk + 4] = reinterpret_cast<float (*)[kDk + 4]>(vaq);
     __shared__ float Td[4][16][17];    // inverses of the 16x16 diagonal blocks of I + A
     __shared__ double Gd[kMaxVPerK][CH];
     __shared__ float bet[kMaxVPerK][CH], gam[kMaxVPerK][CH];
@@ -278,8 +285,9 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep(
     const size_t gi = (size_t)min(t0 + gj, T - 1) * nv + gvh;
     const float gb_in = bin[gi], ga_in = ain[gi], g_sa = ssm_a[gvh], g_dt = dt_bias[gvh];
 
-    // q, then k: conv'd into Ks (thread = channel tid % 128, tokens 32 (tid /
-    // 128) ..), then the per-token sum of squares (thread = (token, quarter)).
+    // q, then k: conv'd into Qs, Ks (thread = channel tid % 128, tokens 32
+    // (tid / 128) ..), then the per-token sum of squares (thread = (token,
+    // quarter)).
     // The raw inputs of both are loaded up front.
     const int cq = tid & (kDk - 1), hq = __builtin_amdgcn_readfirstlane(tid >> 7);
     const int cq_q = kh * kDk + cq, cq_k = key_dim + kh * kDk + cq;
@@ -314,10 +322,10 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep(
             w.gdec[cidx * CH + lane] = __expf((float)(Glast - G));
         }
     }
-    auto conv_qk = [&](int ch, float4 wt, float (&x)[35], float (&y)[32]) {
+    auto conv_qk = [&](float (*X)[kDk + 4], int ch, float4 wt, float (&x)[35], float (&y)[32]) {
         conv_finish<32>(rows, wt, cs, ch, conv_dim, T, t0 + 32 * hq, x, y, R - 1, 2 * key_dim);
 #pragma unroll
-        for (int j = 0; j < 32; ++j) Ks[32 * hq + j][cq] = y[j];
+        for (int j = 0; j < 32; ++j) X[32 * hq + j][cq] = y[j];
         lds_barrier();
         {
             // Lanes l, l + 16, l + 32, l + 48 of a wave take the four quarters
@@ -328,7 +336,7 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep(
             float acc = 0.0f;
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
-                const float4 v = *reinterpret_cast<const float4*>(&Ks[row][32 * part + 4 * e]);
+                const float4 v = *reinterpret_cast<const float4*>(&X[row][32 * part + 4 * e]);
                 acc += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
             }
             acc = xor16_sum(acc);
@@ -340,9 +348,11 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep(
     const size_t kidx = (size_t)kh * nch + n;
     {
         float y[32];
-        conv_qk(cq_q, wq, xq, y);
-        // q^ = q / |q| / sqrt(dk) to the workspace, A layout: float4 o4 =
-        // (tb * 8 + kb) * 64 + lane holds row 16 tb + c, columns 16 kb + 4 g ..
+        conv_qk(Qs, cq_q, wq, xq, y);
+        // q^ = q / |q| / sqrt(dk) in place and to the workspace, A layout:
+        // float4 o4 = (tb * 8 + kb) * 64 + lane holds row 16 tb + c, columns
+        // 16 kb + 4 g ..  (The k conv's first barrier orders these reads of
+        // nrm before its norms overwrite it.)
         float4* qA = reinterpret_cast<float4*>(w.qa + kidx * CB);
         const float pre = 1.0f / sqrtf((float)kDk);
 #pragma unroll
@@ -350,24 +360,22 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep(
             const int o4 = tid + 256 * i, bk = o4 >> 6, ln = o4 & 63;
             const int row = 16 * (bk >> 3) + (ln & 15), col = 16 * (bk & 7) + 4 * (ln >> 4);
             const float sc = pre * nrm[row];
-            const float4 v = *reinterpret_cast<const float4*>(&Ks[row][col]);
-            qA[o4] = make_float4(v.x * sc, v.y * sc, v.z * sc, v.w * sc);
+            const float4 v = *reinterpret_cast<const float4*>(&Qs[row][col]);
+            const float4 qv = make_float4(v.x * sc, v.y * sc, v.z * sc, v.w * sc);
+            qA[o4] = qv;
+            *reinterpret_cast<float4*>(&Qs[row][col]) = qv;
         }
-        lds_barrier();
-        conv_qk(cq_k, wk, xk, y);
+        conv_qk(Ks, cq_k, wk, xk, y);
         // k^ = k / |k| in place (thread owns its channel's 32 rows).
 #pragma unroll
         for (int j = 0; j < 32; ++j) Ks[32 * hq + j][cq] = y[j] * nrm[32 * hq + j];
     }
-    // Also makes this workgroup's q^ stores visible to its own loads below
-    // (the only barrier here that waits for global stores).
-    __syncthreads();
+    lds_barrier();
 
     // Block bi: bi < 10 -> K K^T block (rb, cb), rows 16rb + 4g + r, cols 16cb + c;
     //           bi >= 10 -> (Q K^T)^T block: D rows = keys 16cb + 4g + r, cols = queries 16rb + c.
-    // The Q operand loads of block m + 1 are in flight while block m's 32
-    // MFMAs run; the K operands come from LDS.
-    const float* qA = w.qa + kidx * CB;
+    // The operands (from LDS; Q^ rows read as the A layout) of block m + 1
+    // are in flight while block m's 32 MFMAs run.
     f32x4 blk[5];
     float4 oa[2][8], ob[2][8];
     auto load_blk = [&](int m, float4 (&a)[8], float4 (&b)[8]) {
@@ -378,9 +386,9 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep(
         for (int q = 0; q < kDk / 16; ++q)
             a[q] = *reinterpret_cast<const float4*>(&Ks[16 * ra + c16][16 * q + 4 * g]);
         if (mat) {
-            const float* pb = qA + (size_t)rb * 8 * 256;
 #pragma unroll
-            for (int q = 0; q < kDk / 16; ++q) b[q] = *blk4(pb, 0, q, lane);
+            for (int q = 0; q < kDk / 16; ++q)
+                b[q] = *reinterpret_cast<const float4*>(&Qs[16 * rb + c16][16 * q + 4 * g]);
         } else {
 #pragma unroll
             for (int q = 0; q < kDk / 16; ++q)
@@ -413,6 +421,7 @@ __global__ __launch_bounds__(256, 2) void dn_chunk_prep(
             kD[o4] = make_float4(Ks[r0][c0], Ks[r0 + 1][c0], Ks[r0 + 2][c0], Ks[r0 + 3][c0]);
         }
     }
+    lds_barrier();   // Qs is read for the last time above; Am and Vs reuse it
 
 #pragma unroll 1
     for (int rr = 0; rr < R; ++rr) {
