@@ -31,8 +31,8 @@
 // after its cached rows.  Every chunk emits, per q head, its max score m,
 // sum of exp l and unnormalised o = sum exp(s - m) v.
 // Pass 2 (attn_decode_merge): per (sequence, q head, 32-dim slice) the chunk
-// partials are merged by log-sum-exp rescaling in one round of loads and the
-// sigmoid gate is applied.
+// partials are rescaled to the maximum of their maxima and summed, in one
+// round of loads, and the sigmoid gate is applied.
 //
 // Online softmax is the two-pass softmax regrouped; it omits the reference's
 // -80 floor on shifted logits, which only touches weights below e^-80
@@ -335,27 +335,17 @@ __global__ __launch_bounds__(NT, 2) void attn_decode_partial(
     }
 }
 
-// Log-sum-exp fold of the partial (m2, l2, o2) into (m, l, o).  An empty
-// partial has m = -inf and l = o = 0; two empty ones stay empty (no NaN).
-__device__ __forceinline__ void lse_fold(float& m, float& l, float4& o, float m2, float l2,
-                                         const float4& o2) {
-    const float mn = fmaxf(m, m2);
-    const float a = m == mn ? 1.0f : __expf(m - mn);
-    const float b = m2 == mn ? 1.0f : __expf(m2 - mn);
-    l = l * a + l2 * b;
-    o.x = o.x * a + o2.x * b;
-    o.y = o.y * a + o2.y * b;
-    o.z = o.z * a + o2.z * b;
-    o.w = o.w * a + o2.w * b;
-    m = mn;
-}
-
 // Merge of the chunk partials of one (sequence, q head, 32-dim slice): 256
-// threads, thread t holds 4 dims (d4 = t % 8) of the slice and folds the
-// chunks t / 8, t / 8 + 32, ... into a running (m, l, o): up to MU chunks per
-// thread with all their loads issued together, so up to 128 chunks take one
-// memory round trip.  The 32 running triples of a column are folded by
-// butterfly within each wave (8 per wave) and then across the 4 waves in LDS.
+// threads.  Every wave forms the maximum M of the chunk maxima itself (its
+// lanes stride the chunks; nothing is exchanged between waves).  Thread t
+// holds 4 dims (d4 = t % 8) of the slice and sums the chunks t / 8, t / 8 +
+// 32, ... weighted by w_c = e^{m_c - M}: l = sum w_c l_c, o = sum w_c o_c,
+// up to MU chunks per thread with all their loads issued together with those
+// of the maxima, so up to 128 chunks take one memory round trip and no
+// exponential waits on another (a running log-sum-exp fold chains two per
+// step).  The 32 partial sums of a column are added by butterfly within each
+// wave (8 per wave) and then across the 4 waves in LDS.  Every chunk that ran
+// holds at least one row (chunk 0 the new one), so M is finite.
 constexpr int MT = 256;
 constexpr int MSLICE = 32;                 // dims per merge workgroup
 constexpr int MD4 = MSLICE / 4;            // float4 columns per slice
@@ -373,7 +363,7 @@ __global__ __launch_bounds__(MT) void attn_decode_merge(
     const int nc = max(1, min(nchunks, (pos + rows - 1) / rows));   // chunks that ran
     const size_t base = ((size_t)i * (nh / hpw) + y) * nchunks;
     __shared__ float4 obuf[4][MD4];
-    __shared__ float mbuf[4], lbuf[4];
+    __shared__ float lbuf[4];
 
     const int d4 = t % MD4, g = t / MD4;
     const int col = slice * MD4 + d4;
@@ -382,11 +372,9 @@ __global__ __launch_bounds__(MT) void attn_decode_merge(
     const float4 gt = *reinterpret_cast<const float4*>(
         q_gate + (size_t)i * 2 * nh * kHd + (size_t)h * 2 * kHd + kHd + dim);
 
-    float m = -INFINITY, l = 0.0f;
-    float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int c0 = g; c0 < nc; c0 += MG * MU) {
-        float mc[MU], lc[MU];
-        float4 oc[MU];
+    float mc[MU], lc[MU];
+    float4 oc[MU];
+    auto load_round = [&](int c0) {
 #pragma unroll
         for (int u = 0; u < MU; ++u) {
             const size_t pidx = (base + min(c0 + u * MG, nc - 1)) * hpw + hl;
@@ -394,33 +382,48 @@ __global__ __launch_bounds__(MT) void attn_decode_merge(
             lc[u] = part_ml[2 * pidx + 1];
             oc[u] = reinterpret_cast<const float4*>(part_o + pidx * kHd)[col];
         }
+    };
+    load_round(g);
+    float M = -INFINITY;
+    for (int c = lane; c < nc; c += kWave) M = fmaxf(M, part_ml[2 * ((base + c) * hpw + hl)]);
+    M = wave_max(M);
+
+    float l = 0.0f;
+    float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int c0 = g; c0 < nc; c0 += MG * MU) {
+        if (c0 != g) load_round(c0);
 #pragma unroll
         for (int u = 0; u < MU; ++u)
-            if (c0 + u * MG < nc) lse_fold(m, l, o, mc[u], lc[u], oc[u]);
+            if (c0 + u * MG < nc) {
+                const float wc = __expf(mc[u] - M);
+                l = fmaf(wc, lc[u], l);
+                o.x = fmaf(wc, oc[u].x, o.x);
+                o.y = fmaf(wc, oc[u].y, o.y);
+                o.z = fmaf(wc, oc[u].z, o.z);
+                o.w = fmaf(wc, oc[u].w, o.w);
+            }
     }
     // Butterfly over the 8 groups of each wave (lanes d4 + 8 k share a column).
 #pragma unroll
     for (int k = MD4; k < kWave; k <<= 1) {
-        const float m2 = __shfl_xor(m, k, kWave), l2 = __shfl_xor(l, k, kWave);
-        float4 o2;
-        o2.x = __shfl_xor(o.x, k, kWave);
-        o2.y = __shfl_xor(o.y, k, kWave);
-        o2.z = __shfl_xor(o.z, k, kWave);
-        o2.w = __shfl_xor(o.w, k, kWave);
-        lse_fold(m, l, o, m2, l2, o2);
+        l += __shfl_xor(l, k, kWave);
+        o.x += __shfl_xor(o.x, k, kWave);
+        o.y += __shfl_xor(o.y, k, kWave);
+        o.z += __shfl_xor(o.z, k, kWave);
+        o.w += __shfl_xor(o.w, k, kWave);
     }
     if (lane < MD4) {
         obuf[wave][lane] = o;
-        if (lane == 0) {
-            mbuf[wave] = m;
-            lbuf[wave] = l;
-        }
+        if (lane == 0) lbuf[wave] = l;
     }
     __syncthreads();
     if (t < MD4) {
-#pragma unroll
-        for (int w = 1; w < 4; ++w) lse_fold(m, l, o, mbuf[w], lbuf[w], obuf[w][t]);
-        const float inv = 1.0f / l;
+        const float4 o1 = obuf[1][t], o2 = obuf[2][t], o3 = obuf[3][t];
+        o.x = (o.x + o1.x) + (o2.x + o3.x);
+        o.y = (o.y + o1.y) + (o2.y + o3.y);
+        o.z = (o.z + o1.z) + (o2.z + o3.z);
+        o.w = (o.w + o1.w) + (o2.w + o3.w);
+        const float inv = 1.0f / ((l + lbuf[1]) + (lbuf[2] + lbuf[3]));
         float4 r;
         r.x = o.x * inv * (1.0f / (1.0f + expf(-gt.x)));
         r.y = o.y * inv * (1.0f / (1.0f + expf(-gt.y)));
