@@ -345,7 +345,10 @@ __global__ __launch_bounds__(NT, 2) void attn_decode_partial(
 // exponential waits on another (a running log-sum-exp fold chains two per
 // step).  The 32 partial sums of a column are added by butterfly within each
 // wave (8 per wave) and then across the 4 waves in LDS.  Every chunk that ran
-// holds at least one row (chunk 0 the new one), so M is finite.
+// holds at least one row (chunk 0 the new one), so M is finite.  The loads
+// address all nchunks partials, not only the nc that ran, so they do not wait
+// for the sequence length; partials past nc (not written by this call) are
+// loaded and masked out by selects.
 constexpr int MT = 256;
 constexpr int MSLICE = 32;                 // dims per merge workgroup
 constexpr int MD4 = MSLICE / 4;            // float4 columns per slice
@@ -359,8 +362,6 @@ __global__ __launch_bounds__(MT) void attn_decode_merge(
     const int h = blockIdx.x / (kHd / MSLICE), slice = blockIdx.x % (kHd / MSLICE);
     const int i = blockIdx.y, t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int y = h / hpw, hl = h % hpw;     // head group of the partials
-    const int pos = min(lens[sb.seq[i]], cap - 1);
-    const int nc = max(1, min(nchunks, (pos + rows - 1) / rows));   // chunks that ran
     const size_t base = ((size_t)i * (nh / hpw) + y) * nchunks;
     __shared__ float4 obuf[4][MD4];
     __shared__ float lbuf[4];
@@ -377,15 +378,22 @@ __global__ __launch_bounds__(MT) void attn_decode_merge(
     auto load_round = [&](int c0) {
 #pragma unroll
         for (int u = 0; u < MU; ++u) {
-            const size_t pidx = (base + min(c0 + u * MG, nc - 1)) * hpw + hl;
+            const size_t pidx = (base + min(c0 + u * MG, nchunks - 1)) * hpw + hl;
             mc[u] = part_ml[2 * pidx];
             lc[u] = part_ml[2 * pidx + 1];
             oc[u] = reinterpret_cast<const float4*>(part_o + pidx * kHd)[col];
         }
     };
     load_round(g);
+    float mw[2];                             // the maxima of chunks lane, lane + 64
+#pragma unroll
+    for (int k = 0; k < 2; ++k) mw[k] = part_ml[2 * ((base + min(lane + kWave * k, nchunks - 1)) * hpw + hl)];
+    const int pos = min(lens[sb.seq[i]], cap - 1);
+    const int nc = max(1, min(nchunks, (pos + rows - 1) / rows));   // chunks that ran
     float M = -INFINITY;
-    for (int c = lane; c < nc; c += kWave) M = fmaxf(M, part_ml[2 * ((base + c) * hpw + hl)]);
+#pragma unroll
+    for (int k = 0; k < 2; ++k) M = fmaxf(M, lane + kWave * k < nc ? mw[k] : -INFINITY);
+    for (int c = lane + 2 * kWave; c < nc; c += kWave) M = fmaxf(M, part_ml[2 * ((base + c) * hpw + hl)]);
     M = wave_max(M);
 
     float l = 0.0f;
