@@ -102,8 +102,6 @@ __global__ __launch_bounds__(NT) void deltanet_decode_kernel(
     __shared__ float v_s[kDk];
     __shared__ float red[4][2];
     __shared__ float colred[4][kDk][2];
-    __shared__ float o_s[kDk];
-    __shared__ float nred[2];
 
     // Load order: the small conv and gate operands first, then the state
     // of the head, so the conv, norms and gates are computed while it is
@@ -114,10 +112,11 @@ __global__ __launch_bounds__(NT) void deltanet_decode_kernel(
     const ConvOperands ov = conv_load(conv_w, win, x, v_c, conv_dim);
     const float b_in = bin[(size_t)i * nv + vh], a_in = ain[(size_t)i * nv + vh];
     const float sa = ssm_a[vh], dtb = dt_bias[vh];
-    // Operands of the gated norm at the end (threads t >= 128 load channel 127
-    // and discard it).
-    const size_t o_off = (size_t)i * value_dim + (size_t)vh * kDk + min(t, kDk - 1);
-    const float z_t = zin[o_off], nw_t = ssm_norm[min(t, kDk - 1)];
+    // Operands of the gated norm at the end: channels 4 c4 .. 4 c4 + 3 (used
+    // by the first row group, loaded by every thread).
+    const size_t o_off = (size_t)i * value_dim + (size_t)vh * kDk + 4 * c4;
+    const float4 z4 = *reinterpret_cast<const float4*>(zin + o_off);
+    const float4 nw4 = *reinterpret_cast<const float4*>(ssm_norm + 4 * c4);
 
     // Thread owns columns 4*c4 .. +3 of rows rg + RG*j.  The loads stay in
     // row order (the scheduler may not reorder them across the barriers), so
@@ -146,7 +145,8 @@ __global__ __launch_bounds__(NT) void deltanet_decode_kernel(
     if (t < kDk) conv_shift(ov, win, v_c);
 
     // L2 norms of q and k, and q.k (GatedDeltaNetOps.cs:144-151): waves 0-1
-    // hold q, waves 2-3 hold k.
+    // hold q, waves 2-3 hold k.  Their sums go to LDS beside the column sums
+    // below, behind the same barrier.
     {
         float a0, a1 = 0.0f;
         if (t < kDk) {
@@ -164,17 +164,15 @@ __global__ __launch_bounds__(NT) void deltanet_decode_kernel(
             red[wave][1] = a1;
         }
     }
-    lds_barrier();
-    const float q_scale = (1.0f / sqrtf((float)kDk)) / sqrtf(red[0][0] + red[1][0] + eps);
-    const float k_scale = 1.0f / sqrtf(red[2][0] + red[3][0] + eps);
-    const float qk = (red[0][1] + red[1][1]) * q_scale * k_scale;
 
-    // Partial S^T k and S^T q over this thread's rows.
+    // Partial S^T k and S^T q over this thread's rows, on the conv outputs
+    // before the norms (so they do not wait for the norms' reduction): the
+    // scales apply to the column sums, S^T (s k) = s (S^T k).
     float kvp[4] = {0.f, 0.f, 0.f, 0.f}, sqp[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int j = 0; j < RPT; ++j) {
         const int a = rg + RG * j;
-        const float qa = qk_s[a] * q_scale, ka = qk_s[kDk + a] * k_scale;
+        const float qa = qk_s[a], ka = qk_s[kDk + a];
         kvp[0] += s[j].x * ka; kvp[1] += s[j].y * ka; kvp[2] += s[j].z * ka; kvp[3] += s[j].w * ka;
         sqp[0] += s[j].x * qa; sqp[1] += s[j].y * qa; sqp[2] += s[j].z * qa; sqp[3] += s[j].w * qa;
     }
@@ -193,13 +191,16 @@ __global__ __launch_bounds__(NT) void deltanet_decode_kernel(
             colred[wave][4 * c4 + c][1] = sqp[c];
         }
     lds_barrier();
+    const float q_scale = (1.0f / sqrtf((float)kDk)) / sqrtf(red[0][0] + red[1][0] + eps);
+    const float k_scale = 1.0f / sqrtf(red[2][0] + red[3][0] + eps);
+    const float qk = (red[0][1] + red[1][1]) * q_scale * k_scale;
 
     float delta[4], o[4];
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
         const int col = 4 * c4 + c;
-        const float kv = colred[0][col][0] + colred[1][col][0] + colred[2][col][0] + colred[3][col][0];
-        const float sq = colred[0][col][1] + colred[1][col][1] + colred[2][col][1] + colred[3][col][1];
+        const float kv = (colred[0][col][0] + colred[1][col][0] + colred[2][col][0] + colred[3][col][0]) * k_scale;
+        const float sq = (colred[0][col][1] + colred[1][col][1] + colred[2][col][1] + colred[3][col][1]) * q_scale;
         delta[c] = beta * (v_s[col] - decay * kv);
         o[c] = decay * sq + qk * delta[c];
     }
@@ -214,18 +215,19 @@ __global__ __launch_bounds__(NT) void deltanet_decode_kernel(
         store_nt(S + (size_t)(rg + RG * j) * kDk + 4 * c4, n);
     }
 
-    if (rg == 0)
-#pragma unroll
-        for (int c = 0; c < 4; ++c) o_s[4 * c4 + c] = o[c];
-    lds_barrier();
-    // Gated RMSNorm of the head (plain weight, Qwen35Ops.cs:98-110).
-    const float ov_t = t < kDk ? o_s[t] : 0.0f;
-    const float ss = wave_sum(ov_t * ov_t);
-    if (lane == 0 && wave < 2) nred[wave] = ss;
-    lds_barrier();
-    if (t < kDk) {
-        const float rs = 1.0f / sqrtf((nred[0] + nred[1]) / (float)kDk + eps);
-        out[o_off] = ov_t * rs * nw_t * silu(z_t);
+    // Gated RMSNorm of the head (plain weight, Qwen35Ops.cs:98-110).  Each
+    // half wave (one row group, all 32 column groups) holds the whole head's
+    // o, so the sum of squares is a 32-lane reduction, no exchange; the first
+    // row group writes the output.
+    const float ss = group_sum<32>(o[0] * o[0] + o[1] * o[1] + o[2] * o[2] + o[3] * o[3]);
+    if (rg == 0) {
+        const float rs = 1.0f / sqrtf(ss / (float)kDk + eps);
+        float4 r;
+        r.x = o[0] * rs * nw4.x * silu(z4.x);
+        r.y = o[1] * rs * nw4.y * silu(z4.y);
+        r.z = o[2] * rs * nw4.z * silu(z4.z);
+        r.w = o[3] * rs * nw4.w * silu(z4.w);
+        *reinterpret_cast<float4*>(out + o_off) = r;
     }
 }
 
