@@ -85,6 +85,46 @@ def test_null_context_is_rejected():
     assert L.q35m_snapshot_restore(None, 0, None, 0, ctypes.byref(info)) == q35mix.ERR_INVALID
 
 
+def test_null_handles_of_decode_graph_and_settings_are_rejected():
+    """The decode-graph, projection-order, snapshot-check, no-alloc and
+    profiling entry points refuse a null context or graph before any device
+    work, with a message in q35m_last_error."""
+    L = q35mix.lib()
+    seqs = (ctypes.c_int * 1)(0)
+    io = (q35mix.DecodeIO * 4)()
+    g = ctypes.c_void_p(1234)
+    assert L.q35m_decode_graph_create(None, 1, seqs, io, 16, ctypes.byref(g)) == q35mix.ERR_INVALID
+    assert g.value is None                       # *out cleared before the checks
+    assert "context" in L.q35m_last_error().decode()
+    assert L.q35m_decode_graph_create(None, 1, seqs, io, 16, None) == q35mix.ERR_INVALID
+    assert L.q35m_decode_graph_run(None, 1) == q35mix.ERR_INVALID
+    assert "graph" in L.q35m_last_error().decode()
+    assert L.q35m_decode_graph_destroy(None) == q35mix.OK
+    assert L.q35m_set_projection_order(None, q35mix.PROJ_BLOCK) == q35mix.ERR_INVALID
+    info = q35mix.SnapshotInfo()
+    assert L.q35m_snapshot_valid(None, 0, ctypes.byref(info)) == q35mix.ERR_INVALID
+    assert L.q35m_attn_decode_noalloc(None, 3, 1, seqs, None, None, None, None) == q35mix.ERR_INVALID
+    assert L.q35m_deltanet_decode(None, 0, 1, seqs, None, None, None, None, None) == q35mix.ERR_INVALID
+    assert L.q35m_attn_decode(None, 3, 1, seqs, None, None, None, None) == q35mix.ERR_INVALID
+    assert L.q35m_profile(None, 1) == q35mix.ERR_INVALID
+    ms, n = ctypes.c_double(), ctypes.c_long()
+    assert L.q35m_profile_read(None, 0, ctypes.byref(ms), ctypes.byref(n)) == q35mix.ERR_INVALID
+
+
+def test_profile_kernel_names_end_with_null():
+    L = q35mix.lib()
+    names = []
+    k = 0
+    while L.q35m_profile_kernel_name(k) is not None:
+        names.append(L.q35m_profile_kernel_name(k).decode())
+        k += 1
+    assert L.q35m_profile_kernel_name(-1) is None
+    assert len(names) == len(set(names))
+    for must in ("deltanet_decode_kernel", "dn_chunk_prep", "dn_chunk_scan", "dn_chunk_out",
+                 "attn_decode_merge", "q4k_gemm", "q6k_gemm", "q6k_gemm_blk"):
+        assert must in names, must
+
+
 def test_no_device_here_is_an_error_not_a_fallback():
     if q35mix.device_count() > 0:
         pytest.skip("a HIP device is present")
