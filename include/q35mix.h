@@ -375,7 +375,7 @@ int q35m_linear_f32(q35m_ctx* ctx, const float* w, const float* x, float* y, int
  * 32) * q8 over all its sub-blocks, in int32) times its fp32 scales, once per
  * block: the reference's integer part exactly, its 8 per-lane fp32 chains
  * regrouped, so results agree with it within fp32 rounding of the exact value
- * rather than bit for bit (about 1.5x faster at 2048 tokens).  Other formats,
+ * rather than bit for bit (about 2x faster at 2048 tokens).  Other formats,
  * one token and the other Q6_K shapes keep the reference's order.  No
  * counterpart in the reference (it has one order per path). */
 #define Q35M_PROJ_REFERENCE 0
