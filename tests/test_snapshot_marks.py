@@ -9,10 +9,10 @@ model's events are those of the library: decode/prefill appends rows at the
 current length, truncate, reset, restore of a snapshot, and K/V state writes
 of rows from 0.  Random histories must agree on every query.
 
-A two-round prefix reuse (the scenario q35m_reuse_plan serves) shows why the
-host passes only accepted snapshots to the plan: after the first round
+A multi-turn prefix reuse (the scenario q35m_reuse_plan serves) shows why the
+host passes only accepted snapshots to the plan: after a later turn
 restores a shorter snapshot and forwards new tokens, a longer snapshot of the
-first round is refused, and the plan over the accepted lengths picks the
+first turn is refused, and the plan over the accepted lengths picks the
 snapshot the restore then accepts.
 """
 import os
@@ -147,12 +147,12 @@ def test_rule_matches_row_versions(driver, seed):
     m.close()
 
 
-def test_two_round_prefix_reuse(driver):
-    """Round 1 forwards prompt P1 (12 tokens) saving snapshots at 3, 6 and 9.
-    Round 2's prompt keeps 7 tokens: the plan picks the snapshot at 6, which
+def test_multi_turn_prefix_reuse(driver):
+    """Turn 1 forwards prompt P1 (12 tokens) saving snapshots at 3, 6 and 9.
+    Turn 2's prompt keeps 7 tokens: the plan picks the snapshot at 6, which
     is restored, and 7 new tokens are forwarded with snapshots at 8 and 12.
-    Round 3's prompt keeps 10 tokens of that history: the snapshot at 9 (of
-    round 1, before the cut to 6) is refused; the plan over the accepted
+    Turn 3's prompt keeps 10 tokens of that history: the snapshot at 9 (of
+    turn 1, before the cut to 6) is refused; the plan over the accepted
     lengths picks 8, which the restore accepts."""
     m = Marks(driver)
     s = Sequence(m)
